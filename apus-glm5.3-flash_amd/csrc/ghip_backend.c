@@ -1,0 +1,776 @@
+/*
+ * ghip_backend.c — the C host layer of the MI355X backend (C11 over the HIP
+ * runtime C API). Implements include/backend_hip.h: the hook table and its
+ * enable/disable lifecycle, region registration (device mirrors of
+ * model-owned weights), counters, the direct and device-pointer entry
+ * points, the HBM expert slab store and the MoE decode entry points.
+ *
+ * Kernels live in the .hip units and are reached only through the launchers
+ * of ghip_internal.h. Nothing here computes on the CPU: when the device or a
+ * launch is unavailable an entry point returns nonzero and records why
+ * (apus_ghip_last_error); the hook contract then lets the engine run its own
+ * CPU kernel (c/bf16.h:717-719, c/gdsa.h:529-531).
+ *
+ * Reference counterparts: c/backend_gmetal.mm:378-487 (init, floors, hook
+ * trampolines, region wraps), c/gcache.h:832-1004 (store layout/open).
+ */
+#include "backend_hip.h"
+#include "apus_synth.h"
+#include "ghip_internal.h"
+
+#include <hip/hip_runtime_api.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* weak default of the hook table (an engine TU may define the strong one) */
+__attribute__((weak)) ApusGhipHooks apus_ghip_hooks;
+
+#define GHIP_MAX_TOPK 16
+
+/* ------------------------------------------------------------------------ */
+/* state                                                                    */
+/* ------------------------------------------------------------------------ */
+
+typedef struct {
+    const uint8_t *host;
+    size_t len;
+    void *dev;
+} GhipRegion;
+
+typedef struct {
+    const void *dev;
+    size_t n;
+    int slot;                    /* index into the flag pool */
+} GhipScan;
+
+#define GHIP_SCAN_SLOTS 4096
+
+static struct {
+    int inited, enabled, device;
+    hipStream_t stream;
+    /* grow-only staging (device) */
+    void *d_w, *d_s, *d_x, *d_y;
+    size_t cap_w, cap_s, cap_x, cap_y;
+    uint32_t *d_flag;            /* ephemeral NaN-scan flag */
+    uint32_t *d_flags;           /* pool of cached scan flags */
+    int n_scan;
+    GhipScan scan[GHIP_SCAN_SLOTS];
+    GhipRegion *reg;
+    size_t nreg, capreg;
+    /* env floors (read once at enable) */
+    size_t min_kb, fp8_min_kb;
+    long max_m;
+    /* counters */
+    uint64_t bytes_wrapped, bytes_pinned, dispatches, off_bf16, off_fp8;
+    uint64_t h2d, d2h;
+} G;
+
+static _Thread_local char g_err[512];
+
+static void ghip_seterr(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+}
+
+const char *apus_ghip_last_error(void) { return g_err; }
+
+#define HIPCHK(call)                                                       \
+    do {                                                                   \
+        hipError_t e_ = (call);                                            \
+        if (e_ != hipSuccess) {                                            \
+            ghip_seterr("%s: %s (%s:%d)", #call, hipGetErrorString(e_),    \
+                        __FILE__, __LINE__);                               \
+            return 1;                                                      \
+        }                                                                  \
+    } while (0)
+
+static long env_long(const char *name, long dflt) {
+    const char *v = getenv(name);
+    if (!v || !*v) return dflt;
+    return strtol(v, NULL, 10);
+}
+
+/* Device selection and backend stream (default priority). */
+static int ghip_init(void) {
+    if (G.inited) return 0;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n <= 0) {
+        ghip_seterr("no HIP device (%s)",
+                    e != hipSuccess ? hipGetErrorString(e) : "count 0");
+        return 1;
+    }
+    int dev = (int)env_long("APUS_GHIP_DEVICE", 0);
+    if (dev < 0 || dev >= n) {
+        ghip_seterr("APUS_GHIP_DEVICE=%d out of range (%d devices)", dev, n);
+        return 1;
+    }
+    hipDeviceProp_t prop;
+    HIPCHK(hipGetDeviceProperties(&prop, dev));
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        ghip_seterr("device %d is %s; this backend is built for gfx950", dev,
+                    prop.gcnArchName);
+        return 1;
+    }
+    HIPCHK(hipSetDevice(dev));
+    HIPCHK(hipStreamCreate(&G.stream));
+    HIPCHK(hipMalloc((void **)&G.d_flag, 256));
+    HIPCHK(hipMalloc((void **)&G.d_flags, GHIP_SCAN_SLOTS * sizeof(uint32_t)));
+    HIPCHK(hipMemset(G.d_flags, 0, GHIP_SCAN_SLOTS * sizeof(uint32_t)));
+    G.device = dev;
+    G.inited = 1;
+    return 0;
+}
+
+static int grow(void **p, size_t *cap, size_t need) {
+    if (need <= *cap) return 0;
+    size_t nc = need < 4096 ? 4096 : need;
+    nc = (nc + 4095) & ~(size_t)4095;
+    if (*p) {
+        HIPCHK(hipStreamSynchronize(G.stream));
+        HIPCHK(hipFree(*p));
+        *p = NULL;
+        *cap = 0;
+    }
+    HIPCHK(hipMalloc(p, nc));
+    *cap = nc;
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* regions                                                                  */
+/* ------------------------------------------------------------------------ */
+
+/* Device address of host range [p, p+n) when a registered region covers it
+ * (sub-ranges included, as c/backend_gmetal.mm:240-251). */
+static void *region_find(const void *p, size_t n) {
+    const uint8_t *q = (const uint8_t *)p;
+    for (size_t i = 0; i < G.nreg; i++) {
+        const GhipRegion *r = &G.reg[i];
+        if (q >= r->host && q + n <= r->host + r->len && n <= r->len)
+            return (uint8_t *)r->dev + (q - r->host);
+    }
+    return NULL;
+}
+
+int apus_ghip_register_region(const void *ptr, size_t len) {
+    if (!G.enabled || !ptr || len == 0) {
+        ghip_seterr("register_region: backend disabled or empty range");
+        return 1;
+    }
+    for (size_t i = 0; i < G.nreg; i++)
+        if (G.reg[i].host == ptr) return 0;          /* idempotent */
+    if (G.nreg == G.capreg) {
+        size_t nc = G.capreg ? 2 * G.capreg : 64;
+        GhipRegion *nr = (GhipRegion *)realloc(G.reg, nc * sizeof *nr);
+        if (!nr) { ghip_seterr("register_region: out of host memory"); return 1; }
+        G.reg = nr;
+        G.capreg = nc;
+    }
+    void *d = NULL;
+    HIPCHK(hipMalloc(&d, len));
+    hipError_t e = hipMemcpy(d, ptr, len, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        hipFree(d);
+        ghip_seterr("register_region: H2D %s", hipGetErrorString(e));
+        return 1;
+    }
+    G.reg[G.nreg].host = (const uint8_t *)ptr;
+    G.reg[G.nreg].len = len;
+    G.reg[G.nreg].dev = d;
+    G.nreg++;
+    G.bytes_pinned += len;
+    G.h2d += len;
+    return 0;
+}
+
+void apus_ghip_unregister_region(const void *ptr) {
+    for (size_t i = 0; i < G.nreg; i++) {
+        if (G.reg[i].host != ptr) continue;
+        GhipRegion r = G.reg[i];
+        hipStreamSynchronize(G.stream);
+        /* drop cached scans that point into this region */
+        for (int s = 0; s < G.n_scan; s++) {
+            const uint8_t *d = (const uint8_t *)G.scan[s].dev;
+            if (d >= (uint8_t *)r.dev && d < (uint8_t *)r.dev + r.len)
+                G.scan[s].dev = NULL;
+        }
+        hipFree(r.dev);
+        G.bytes_pinned -= r.len;
+        G.reg[i] = G.reg[--G.nreg];
+        return;
+    }
+}
+
+/* Cached NaN-code scan of resident device codes: returns a device flag
+ * (u32, nonzero = exact decode needed), or NULL when the pool is full. */
+static const uint32_t *scan_cached(const void *dcodes, size_t n) {
+    for (int s = 0; s < G.n_scan; s++)
+        if (G.scan[s].dev == dcodes && G.scan[s].n == n)
+            return G.d_flags + G.scan[s].slot;
+    if (G.n_scan >= GHIP_SCAN_SLOTS) return NULL;
+    int slot = G.n_scan;
+    if (ghip_launch_fill_u32(G.d_flags + slot, 1, 0u, G.stream) != hipSuccess
+        || ghip_launch_nan_scan((const uint8_t *)dcodes, n, G.d_flags + slot,
+                                G.stream) != hipSuccess)
+        return NULL;
+    G.scan[slot].dev = dcodes;
+    G.scan[slot].n = n;
+    G.scan[slot].slot = slot;
+    G.n_scan++;
+    return G.d_flags + slot;
+}
+
+/* ------------------------------------------------------------------------ */
+/* lifecycle                                                                */
+/* ------------------------------------------------------------------------ */
+
+static int hook_bf16_gemm(const uint16_t *w, const uint16_t *x, uint16_t *y,
+                          size_t M, size_t O, size_t K);
+static int hook_fp8blk_linear(const uint8_t *codes, const float *scales,
+                              const uint16_t *x, uint16_t *y, size_t M,
+                              size_t O, size_t K);
+
+int apus_ghip_enable(char *err, size_t errcap) {
+    if (G.enabled) return 0;
+    if (ghip_init()) {
+        if (err && errcap) snprintf(err, errcap, "%s", g_err);
+        return 1;
+    }
+    long v = env_long("APUS_GHIP_MIN_KB", 0);
+    G.min_kb = v > 0 ? (size_t)v : 0;
+    v = env_long("APUS_GHIP_FP8_MIN_KB", 0);
+    G.fp8_min_kb = v > 0 ? (size_t)v : 0;
+    G.max_m = env_long("APUS_GHIP_MAX_M", 0);
+    apus_ghip_hooks.bf16_gemm = hook_bf16_gemm;
+    apus_ghip_hooks.fp8blk_linear = hook_fp8blk_linear;
+    G.enabled = 1;
+    return 0;
+}
+
+void apus_ghip_disable(void) {
+    apus_ghip_hooks.bf16_gemm = NULL;
+    apus_ghip_hooks.fp8blk_linear = NULL;
+    if (!G.enabled) return;
+    hipStreamSynchronize(G.stream);
+    while (G.nreg) apus_ghip_unregister_region(G.reg[G.nreg - 1].host);
+    free(G.reg);
+    G.reg = NULL;
+    G.capreg = 0;
+    G.n_scan = 0;
+    hipMemset(G.d_flags, 0, GHIP_SCAN_SLOTS * sizeof(uint32_t));
+    void **bufs[4] = { &G.d_w, &G.d_s, &G.d_x, &G.d_y };
+    size_t *caps[4] = { &G.cap_w, &G.cap_s, &G.cap_x, &G.cap_y };
+    for (int i = 0; i < 4; i++) {
+        if (*bufs[i]) hipFree(*bufs[i]);
+        *bufs[i] = NULL;
+        *caps[i] = 0;
+    }
+    G.enabled = 0;
+}
+
+int apus_ghip_is_enabled(void) { return G.enabled; }
+
+uint64_t apus_ghip_bytes_wrapped(void) { return G.bytes_wrapped; }
+uint64_t apus_ghip_bytes_pinned(void) { return G.bytes_pinned; }
+uint64_t apus_ghip_dispatches(void) { return G.dispatches; }
+uint64_t apus_ghip_offload_bf16(void) { return G.off_bf16; }
+uint64_t apus_ghip_offload_fp8blk(void) { return G.off_fp8; }
+uint64_t apus_ghip_bytes_h2d(void) { return G.h2d; }
+uint64_t apus_ghip_bytes_d2h(void) { return G.d2h; }
+
+/* ------------------------------------------------------------------------ */
+/* host-pointer entry points                                                */
+/* ------------------------------------------------------------------------ */
+
+static int h2d(void *d, const void *h, size_t n) {
+    if (n == 0) return 0;
+    HIPCHK(hipMemcpyAsync(d, h, n, hipMemcpyHostToDevice, G.stream));
+    G.h2d += n;
+    return 0;
+}
+
+/* Device address for a weight range: the registered mirror, else an upload
+ * into the given staging buffer. */
+static const void *weight_dev(const void *h, size_t n, void **stage,
+                              size_t *cap) {
+    void *d = region_find(h, n);
+    if (d) return d;
+    if (grow(stage, cap, n) || h2d(*stage, h, n)) return NULL;
+    G.bytes_wrapped += n;
+    return *stage;
+}
+
+static int sync_out(void *h, const void *d, size_t n) {
+    HIPCHK(hipMemcpyAsync(h, d, n, hipMemcpyDeviceToHost, G.stream));
+    HIPCHK(hipStreamSynchronize(G.stream));
+    G.d2h += n;
+    return 0;
+}
+
+static int check_sizes(size_t M, size_t O, size_t K) {
+    if (M == 0 || O == 0 || K == 0) {
+        ghip_seterr("empty shape M=%zu O=%zu K=%zu", M, O, K);
+        return 1;
+    }
+    if (O > 0x7fffffffu || K > 0x7fffffffu || M > 0x7fffffffu) {
+        ghip_seterr("shape too large M=%zu O=%zu K=%zu", M, O, K);
+        return 1;
+    }
+    return 0;
+}
+
+int apus_ghip_bf16_gemm(const uint16_t *w, const uint16_t *x, uint16_t *y,
+                        size_t M, size_t O, size_t K) {
+    if (ghip_init() || check_sizes(M, O, K)) return 1;
+    const void *dw = weight_dev(w, O * K * 2, &G.d_w, &G.cap_w);
+    if (!dw) return 1;
+    if (grow(&G.d_x, &G.cap_x, M * K * 2) || grow(&G.d_y, &G.cap_y, M * O * 2)
+        || h2d(G.d_x, x, M * K * 2))
+        return 1;
+    HIPCHK(ghip_launch_bf16_linear((const uint16_t *)dw, (const uint16_t *)G.d_x,
+                                   (uint16_t *)G.d_y, M, O, K, G.stream));
+    G.dispatches++;
+    if (sync_out(y, G.d_y, M * O * 2)) return 1;
+    G.off_bf16++;
+    return 0;
+}
+
+int apus_ghip_fp8blk_linear(const uint8_t *codes, const float *scales,
+                            const uint16_t *x, uint16_t *y,
+                            size_t M, size_t O, size_t K) {
+    if (ghip_init() || check_sizes(M, O, K)) return 1;
+    size_t nsb = ((O + 127) / 128) * ((K + 127) / 128) * sizeof(float);
+    int reg = region_find(codes, O * K) != NULL;
+    const void *dc = weight_dev(codes, O * K, &G.d_w, &G.cap_w);
+    const void *ds = dc ? weight_dev(scales, nsb, &G.d_s, &G.cap_s) : NULL;
+    if (!dc || !ds) return 1;
+    const uint32_t *flag = reg ? scan_cached(dc, O * K) : NULL;
+    if (!flag) {
+        HIPCHK(ghip_launch_fill_u32(G.d_flag, 1, 0u, G.stream));
+        HIPCHK(ghip_launch_nan_scan((const uint8_t *)dc, O * K, G.d_flag,
+                                    G.stream));
+        flag = G.d_flag;
+    }
+    if (grow(&G.d_x, &G.cap_x, M * K * 2) || grow(&G.d_y, &G.cap_y, M * O * 2)
+        || h2d(G.d_x, x, M * K * 2))
+        return 1;
+    HIPCHK(ghip_launch_fp8_linear((const uint8_t *)dc, (const float *)ds,
+                                  (const uint16_t *)G.d_x, (uint16_t *)G.d_y,
+                                  M, O, K, flag, G.stream));
+    G.dispatches++;
+    if (sync_out(y, G.d_y, M * O * 2)) return 1;
+    G.off_fp8++;
+    return 0;
+}
+
+int apus_ghip_fp8blk_dequant(const uint8_t *codes, const float *scales,
+                             uint16_t *out, size_t O, size_t K) {
+    if (ghip_init() || check_sizes(1, O, K)) return 1;
+    size_t nsb = ((O + 127) / 128) * ((K + 127) / 128) * sizeof(float);
+    const void *dc = weight_dev(codes, O * K, &G.d_w, &G.cap_w);
+    const void *ds = dc ? weight_dev(scales, nsb, &G.d_s, &G.cap_s) : NULL;
+    if (!dc || !ds || grow(&G.d_y, &G.cap_y, O * K * 2)) return 1;
+    /* the exact integer decode is bitwise for every code; the host-pointer
+     * path is PCIe-bound, so it always takes it */
+    HIPCHK(ghip_launch_dequant((const uint8_t *)dc, (const float *)ds,
+                               (uint16_t *)G.d_y, O, K, 1, G.stream));
+    G.dispatches++;
+    return sync_out(out, G.d_y, O * K * 2);
+}
+
+/* Hooks: the floors of c/backend_gmetal.mm:437-474, then the direct path. */
+static int hook_bf16_gemm(const uint16_t *w, const uint16_t *x, uint16_t *y,
+                          size_t M, size_t O, size_t K) {
+    if (!G.enabled) return 1;
+    if (G.max_m > 0 && M > (size_t)G.max_m) return 1;
+    if (O * K * 2 < G.min_kb * 1024) return 1;
+    return apus_ghip_bf16_gemm(w, x, y, M, O, K);
+}
+
+static int hook_fp8blk_linear(const uint8_t *codes, const float *scales,
+                              const uint16_t *x, uint16_t *y, size_t M,
+                              size_t O, size_t K) {
+    if (!G.enabled) return 1;
+    if (G.max_m > 0 && M > (size_t)G.max_m) return 1;
+    if (O * K < G.fp8_min_kb * 1024) return 1;
+    return apus_ghip_fp8blk_linear(codes, scales, x, y, M, O, K);
+}
+
+/* ------------------------------------------------------------------------ */
+/* device-pointer entry points                                              */
+/* ------------------------------------------------------------------------ */
+
+static const uint32_t *exact_flag_dev(const uint8_t *codes, size_t n,
+                                      int exact, hipStream_t st, int *rc) {
+    static const uint32_t *one = NULL;
+    *rc = 0;
+    if (exact == 0) return NULL;
+    if (exact > 0) {
+        if (!one) {
+            uint32_t *p = G.d_flag + 1;
+            if (ghip_launch_fill_u32(p, 1, 1u, st) != hipSuccess) { *rc = 1; return NULL; }
+            one = p;
+        }
+        return one;
+    }
+    if (ghip_launch_fill_u32(G.d_flag, 1, 0u, st) != hipSuccess
+        || ghip_launch_nan_scan(codes, n, G.d_flag, st) != hipSuccess) {
+        *rc = 1;
+        return NULL;
+    }
+    return G.d_flag;
+}
+
+int apus_ghip_fp8blk_linear_dev(const uint8_t *codes, const float *scales,
+                                const uint16_t *x, uint16_t *y,
+                                size_t M, size_t O, size_t K,
+                                int exact, void *stream) {
+    if (ghip_init() || check_sizes(M, O, K)) return 1;
+    hipStream_t st = (hipStream_t)stream;
+    int rc;
+    const uint32_t *flag = exact_flag_dev(codes, O * K, exact, st, &rc);
+    if (rc) { ghip_seterr("fp8blk_linear_dev: flag setup failed"); return 1; }
+    HIPCHK(ghip_launch_fp8_linear(codes, scales, x, y, M, O, K, flag, st));
+    G.dispatches++;
+    return 0;
+}
+
+int apus_ghip_fp8blk_dequant_dev(const uint8_t *codes, const float *scales,
+                                 uint16_t *out, size_t O, size_t K,
+                                 int exact, void *stream) {
+    if (ghip_init() || check_sizes(1, O, K)) return 1;
+    /* dequant has no device-side selection: auto means exact (bitwise for
+     * every code; the fast decode is for callers that know their codes) */
+    HIPCHK(ghip_launch_dequant(codes, scales, out, O, K, exact != 0,
+                               (hipStream_t)stream));
+    G.dispatches++;
+    return 0;
+}
+
+int apus_ghip_bf16_gemm_dev(const uint16_t *w, const uint16_t *x,
+                            uint16_t *y, size_t M, size_t O, size_t K,
+                            void *stream) {
+    if (ghip_init() || check_sizes(M, O, K)) return 1;
+    HIPCHK(ghip_launch_bf16_linear(w, x, y, M, O, K, (hipStream_t)stream));
+    G.dispatches++;
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* HBM expert slab store                                                    */
+/* ------------------------------------------------------------------------ */
+
+struct ApusGhipStore {
+    int n_experts;
+    size_t dim, inter;
+    float limit;
+    /* host slab layout (c/gcache.h:852-861) */
+    size_t h_gw, h_gs, h_uw, h_us, h_dw, h_ds, h_bytes;
+    /* device layout: same order, members 256-byte aligned */
+    size_t d_gw, d_gs, d_uw, d_us, d_dw, d_ds, d_stride;
+    uint8_t *arena;
+    uint32_t *nan_flags;                 /* device [n_experts] */
+    GhipMoeDecodeWs ws;
+    /* decode staging for the host-pointer entry */
+    uint16_t *d_x, *d_out;
+    int32_t *d_idx;
+    float *d_w;
+};
+
+static size_t up256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+int apus_ghip_store_open(ApusGhipStore **out, int n_experts, size_t dim,
+                         size_t inter, float limit, char *err, size_t errcap) {
+    *out = NULL;
+    if (ghip_init()) {
+        if (err && errcap) snprintf(err, errcap, "%s", g_err);
+        return 1;
+    }
+    if (n_experts <= 0 || dim == 0 || inter == 0) {
+        ghip_seterr("store_open: bad shape E=%d dim=%zu inter=%zu", n_experts,
+                    dim, inter);
+        if (err && errcap) snprintf(err, errcap, "%s", g_err);
+        return 1;
+    }
+    ApusGhipStore *s = (ApusGhipStore *)calloc(1, sizeof *s);
+    if (!s) return 1;
+    s->n_experts = n_experts;
+    s->dim = dim;
+    s->inter = inter;
+    s->limit = limit;
+    size_t nbg = ((inter + 127) / 128) * ((dim + 127) / 128) * sizeof(float);
+    size_t nbd = ((dim + 127) / 128) * ((inter + 127) / 128) * sizeof(float);
+    s->h_gw = 0;
+    s->h_gs = inter * dim;
+    s->h_uw = s->h_gs + nbg;
+    s->h_us = s->h_uw + inter * dim;
+    s->h_dw = s->h_us + nbg;
+    s->h_ds = s->h_dw + dim * inter;
+    s->h_bytes = s->h_ds + nbd;
+    s->d_gw = 0;
+    s->d_gs = up256(inter * dim);
+    s->d_uw = s->d_gs + up256(nbg);
+    s->d_us = s->d_uw + up256(inter * dim);
+    s->d_dw = s->d_us + up256(nbg);
+    s->d_ds = s->d_dw + up256(dim * inter);
+    s->d_stride = s->d_ds + up256(nbd);
+    size_t total = s->d_stride * (size_t)n_experts;
+    hipError_t e = hipMalloc((void **)&s->arena, total);
+    if (e != hipSuccess) {
+        ghip_seterr("store_open: hipMalloc(%zu) %s", total, hipGetErrorString(e));
+        if (err && errcap) snprintf(err, errcap, "%s", g_err);
+        free(s);
+        return 1;
+    }
+    int bad = hipMalloc((void **)&s->nan_flags, (size_t)n_experts * 4) != hipSuccess
+           || hipMemset(s->nan_flags, 0, (size_t)n_experts * 4) != hipSuccess
+           || hipMalloc((void **)&s->ws.counters, GHIP_MOE_DEC_COUNTERS * 4) != hipSuccess
+           || hipMemset(s->ws.counters, 0, GHIP_MOE_DEC_COUNTERS * 4) != hipSuccess
+           || hipMalloc((void **)&s->ws.err, 4) != hipSuccess
+           || hipMemset(s->ws.err, 0, 4) != hipSuccess
+           || hipMalloc((void **)&s->ws.h, GHIP_MAX_TOPK * inter * 2) != hipSuccess
+           || hipMalloc((void **)&s->ws.contrib, GHIP_MAX_TOPK * dim * 2) != hipSuccess
+           || hipMalloc((void **)&s->d_x, dim * 2) != hipSuccess
+           || hipMalloc((void **)&s->d_out, dim * 2) != hipSuccess
+           || hipMalloc((void **)&s->d_idx, GHIP_MAX_TOPK * 4) != hipSuccess
+           || hipMalloc((void **)&s->d_w, GHIP_MAX_TOPK * 4) != hipSuccess;
+    if (bad) {
+        ghip_seterr("store_open: workspace allocation failed");
+        if (err && errcap) snprintf(err, errcap, "%s", g_err);
+        apus_ghip_store_close(s);
+        return 1;
+    }
+    *out = s;
+    return 0;
+}
+
+void apus_ghip_store_close(ApusGhipStore *s) {
+    if (!s) return;
+    hipDeviceSynchronize();
+    hipFree(s->arena);
+    hipFree(s->nan_flags);
+    hipFree(s->ws.counters);
+    hipFree(s->ws.err);
+    hipFree(s->ws.h);
+    hipFree(s->ws.contrib);
+    hipFree(s->d_x);
+    hipFree(s->d_out);
+    hipFree(s->d_idx);
+    hipFree(s->d_w);
+    free(s);
+}
+
+size_t apus_ghip_store_slab_bytes(const ApusGhipStore *s) {
+    return s ? s->h_bytes : 0;
+}
+
+const void *apus_ghip_store_slab_dev(const ApusGhipStore *s, int expert) {
+    if (!s || expert < 0 || expert >= s->n_experts) return NULL;
+    return s->arena + (size_t)expert * s->d_stride;
+}
+
+/* NaN-code scan of an expert's three code members into nan_flags[e]. */
+static int store_scan(ApusGhipStore *s, int e, hipStream_t st) {
+    uint8_t *b = s->arena + (size_t)e * s->d_stride;
+    uint32_t *f = s->nan_flags + e;
+    HIPCHK(ghip_launch_fill_u32(f, 1, 0u, st));
+    HIPCHK(ghip_launch_nan_scan(b + s->d_gw, s->inter * s->dim, f, st));
+    HIPCHK(ghip_launch_nan_scan(b + s->d_uw, s->inter * s->dim, f, st));
+    HIPCHK(ghip_launch_nan_scan(b + s->d_dw, s->dim * s->inter, f, st));
+    return 0;
+}
+
+int apus_ghip_store_put(ApusGhipStore *s, int expert, const void *slab,
+                        size_t nbytes) {
+    if (!s || expert < 0 || expert >= s->n_experts || nbytes != s->h_bytes) {
+        ghip_seterr("store_put: bad expert %d or slab size %zu (want %zu)",
+                    expert, nbytes, s ? s->h_bytes : 0);
+        return 1;
+    }
+    uint8_t *b = s->arena + (size_t)expert * s->d_stride;
+    const uint8_t *h = (const uint8_t *)slab;
+    int same = s->d_gs == s->h_gs && s->d_uw == s->h_uw && s->d_us == s->h_us
+            && s->d_dw == s->h_dw && s->d_ds == s->h_ds;
+    if (same) {
+        HIPCHK(hipMemcpyAsync(b, h, s->h_bytes, hipMemcpyHostToDevice, G.stream));
+    } else {
+        const size_t hs[6] = { s->h_gw, s->h_gs, s->h_uw, s->h_us, s->h_dw, s->h_ds };
+        const size_t ds[6] = { s->d_gw, s->d_gs, s->d_uw, s->d_us, s->d_dw, s->d_ds };
+        for (int i = 0; i < 6; i++) {
+            size_t len = (i < 5 ? hs[i + 1] : s->h_bytes) - hs[i];
+            HIPCHK(hipMemcpyAsync(b + ds[i], h + hs[i], len,
+                                  hipMemcpyHostToDevice, G.stream));
+        }
+    }
+    G.h2d += s->h_bytes;
+    if (store_scan(s, expert, G.stream)) return 1;
+    HIPCHK(hipStreamSynchronize(G.stream));
+    return 0;
+}
+
+int apus_ghip_store_synth(ApusGhipStore *s, uint64_t seed, int bank,
+                          float scale_lo, float scale_hi) {
+    if (!s) return 1;
+    size_t nbg = ((s->inter + 127) / 128) * ((s->dim + 127) / 128);
+    size_t nbd = ((s->dim + 127) / 128) * ((s->inter + 127) / 128);
+    size_t nmax = nbg > nbd ? nbg : nbd;
+    float *hs = (float *)malloc(nmax * sizeof(float));
+    if (!hs) { ghip_seterr("store_synth: out of host memory"); return 1; }
+    int rc = 0;
+    for (int e = 0; e < s->n_experts && !rc; e++) {
+        uint8_t *b = s->arena + (size_t)e * s->d_stride;
+        const size_t cw[3] = { s->d_gw, s->d_uw, s->d_dw };
+        const size_t cs[3] = { s->d_gs, s->d_us, s->d_ds };
+        const size_t ns[3] = { nbg, nbg, nbd };
+        for (int j = 0; j < 3 && !rc; j++) {
+            uint64_t kc = apus_synth_key(seed, apus_synth_expert_stream(bank, e, 2 * j));
+            if (ghip_launch_synth_codes(b + cw[j], s->inter * s->dim, kc, 0,
+                                        G.stream) != hipSuccess) {
+                ghip_seterr("store_synth: code fill launch failed");
+                rc = 1;
+                break;
+            }
+            apus_synth_scales(hs, ns[j], seed,
+                              apus_synth_expert_stream(bank, e, 2 * j + 1),
+                              scale_lo, scale_hi);
+            if (hipMemcpyAsync(b + cs[j], hs, ns[j] * sizeof(float),
+                               hipMemcpyHostToDevice, G.stream) != hipSuccess
+                || hipStreamSynchronize(G.stream) != hipSuccess) {
+                ghip_seterr("store_synth: scale upload failed");
+                rc = 1;
+            }
+        }
+        /* synthetic codes exclude 0x7F/0xFF by construction */
+        if (!rc && ghip_launch_fill_u32(s->nan_flags + e, 1, 0u, G.stream) != hipSuccess)
+            rc = 1;
+    }
+    free(hs);
+    if (!rc && hipStreamSynchronize(G.stream) != hipSuccess) {
+        ghip_seterr("store_synth: sync failed");
+        rc = 1;
+    }
+    return rc;
+}
+
+int apus_ghip_store_expert_bf16(ApusGhipStore *s, int expert,
+                                uint16_t *payload) {
+    if (!s || expert < 0 || expert >= s->n_experts) {
+        ghip_seterr("store_expert_bf16: bad expert %d", expert);
+        return 1;
+    }
+    size_t n = s->inter * s->dim;
+    if (grow(&G.d_y, &G.cap_y, 3 * n * 2)) return 1;
+    const uint8_t *b = s->arena + (size_t)expert * s->d_stride;
+    uint16_t *o = (uint16_t *)G.d_y;
+    HIPCHK(ghip_launch_dequant(b + s->d_gw, (const float *)(b + s->d_gs), o,
+                               s->inter, s->dim, 1, G.stream));
+    HIPCHK(ghip_launch_dequant(b + s->d_uw, (const float *)(b + s->d_us), o + n,
+                               s->inter, s->dim, 1, G.stream));
+    HIPCHK(ghip_launch_dequant(b + s->d_dw, (const float *)(b + s->d_ds),
+                               o + 2 * n, s->dim, s->inter, 1, G.stream));
+    G.dispatches += 3;
+    return sync_out(payload, G.d_y, 3 * n * 2);
+}
+
+static void store_bank(const ApusGhipStore *s, GhipBank *bk) {
+    bk->base = s->arena;
+    bk->stride = s->d_stride;
+    bk->off_gw = s->d_gw;
+    bk->off_gs = s->d_gs;
+    bk->off_uw = s->d_uw;
+    bk->off_us = s->d_us;
+    bk->off_dw = s->d_dw;
+    bk->off_ds = s->d_ds;
+    bk->n_experts = (uint32_t)s->n_experts;
+    bk->dim = (uint32_t)s->dim;
+    bk->inter = (uint32_t)s->inter;
+    bk->nan_flags = s->nan_flags;
+}
+
+/* ------------------------------------------------------------------------ */
+/* synthetic device fills (include/apus_synth.h)                            */
+/* ------------------------------------------------------------------------ */
+
+static uint16_t *g_dtab;
+
+int apus_synth_fp8_codes_dev(uint8_t *out, size_t n, uint64_t seed,
+                             uint64_t sstream, uint64_t offset, void *stream) {
+    if (ghip_init()) return 1;
+    HIPCHK(ghip_launch_synth_codes(out, n, apus_synth_key(seed, sstream), offset,
+                                   (hipStream_t)stream));
+    return 0;
+}
+
+int apus_synth_bf16_normal_dev(uint16_t *out, size_t n, uint64_t seed,
+                               uint64_t sstream, uint64_t offset, void *stream) {
+    if (ghip_init()) return 1;
+    if (!g_dtab) {
+        HIPCHK(hipMalloc((void **)&g_dtab, 65536 * 2));
+        HIPCHK(hipMemcpy(g_dtab, apus_synth_normal_table_ptr(), 65536 * 2,
+                         hipMemcpyHostToDevice));
+    }
+    HIPCHK(ghip_launch_synth_bf16(out, n, apus_synth_key(seed, sstream), offset,
+                                  g_dtab, (hipStream_t)stream));
+    return 0;
+}
+
+int apus_ghip_moe_decode_dev(ApusGhipStore *s, const uint16_t *x,
+                             const float *logits, const int32_t *idx,
+                             const float *w, int topk, uint16_t *out,
+                             void *stream) {
+    if (!s) { ghip_seterr("moe_decode: no store"); return 1; }
+    if (topk <= 0 || topk > GHIP_MAX_TOPK || topk > s->n_experts) {
+        ghip_seterr("moe_decode: topk %d outside 1..%d", topk, GHIP_MAX_TOPK);
+        return 1;
+    }
+    if (!logits && (!idx || !w)) {
+        ghip_seterr("moe_decode: need logits or idx+w");
+        return 1;
+    }
+    GhipBank bk;
+    store_bank(s, &bk);
+    hipError_t e = ghip_launch_moe_decode(&bk, x, logits, idx, w, topk,
+                                          s->limit, out, &s->ws,
+                                          (hipStream_t)stream);
+    if (e != hipSuccess) {
+        ghip_seterr("moe_decode launch: %s", hipGetErrorString(e));
+        return 1;
+    }
+    G.dispatches++;
+    return 0;
+}
+
+int apus_ghip_moe_decode(ApusGhipStore *s, const uint16_t *x,
+                         const int32_t *idx, const float *w, int topk,
+                         uint16_t *out) {
+    if (!s) { ghip_seterr("moe_decode: no store"); return 1; }
+    if (topk <= 0 || topk > GHIP_MAX_TOPK) {
+        ghip_seterr("moe_decode: topk %d outside 1..%d", topk, GHIP_MAX_TOPK);
+        return 1;
+    }
+    for (int j = 0; j < topk; j++)
+        if (idx[j] < 0 || idx[j] >= s->n_experts) {
+            ghip_seterr("moe_decode: expert id %d out of range", idx[j]);
+            return 1;
+        }
+    if (h2d(s->d_x, x, s->dim * 2) || h2d(s->d_idx, idx, (size_t)topk * 4)
+        || h2d(s->d_w, w, (size_t)topk * 4))
+        return 1;
+    if (apus_ghip_moe_decode_dev(s, s->d_x, NULL, s->d_idx, s->d_w, topk,
+                                 s->d_out, G.stream))
+        return 1;
+    if (sync_out(out, s->d_out, s->dim * 2)) return 1;
+    uint32_t err = 0;
+    HIPCHK(hipMemcpy(&err, s->ws.err, 4, hipMemcpyDeviceToHost));
+    if (err) {
+        ghip_seterr("moe_decode: device wait bound expired (code %u)", err);
+        hipMemset(s->ws.err, 0, 4);
+        return 1;
+    }
+    return 0;
+}

@@ -1,0 +1,89 @@
+/*
+ * ghip_internal.h — launchers exported by the .hip kernel units to the C
+ * host layer (ghip_backend.c). Plain C ABI: device pointers, sizes and a
+ * hipStream_t. Every launcher validates the shape it is given against what
+ * its kernel and grid assume and returns a hipError_t (hipErrorInvalidValue
+ * for a shape the kernel cannot take) without launching anything invalid.
+ */
+#ifndef GHIP_INTERNAL_H
+#define GHIP_INTERNAL_H
+
+#include <hip/hip_runtime_api.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* K1: out[O,K] bf16 = bf16(e4m3(codes) * scale of the 128x128 block).
+ * exact != 0 selects the integer decode (required for NaN codes). */
+hipError_t ghip_launch_dequant(const uint8_t *codes, const float *scales,
+                               uint16_t *out, size_t O, size_t K, int exact,
+                               hipStream_t st);
+
+/* Scan codes for the NaN codes 0x7F/0xFF: *flag (device u32) |= 1 when any
+ * is present. The caller zeroes *flag first. */
+hipError_t ghip_launch_nan_scan(const uint8_t *codes, size_t n,
+                                uint32_t *flag, hipStream_t st);
+
+/* K2: y[M,O] bf16 = x[M,K] . dequant(W)^T, fp32 accumulate, RNE narrow.
+ * exact_dev: device u32 flag (nonzero -> exact decode); may be NULL (fast).
+ * Any M >= 1, any O, K >= 1. */
+hipError_t ghip_launch_fp8_linear(const uint8_t *codes, const float *scales,
+                                  const uint16_t *x, uint16_t *y, size_t M,
+                                  size_t O, size_t K, const uint32_t *exact_dev,
+                                  hipStream_t st);
+
+/* BF16-weight GEMV/GEMM: y[M,O] = x[M,K] . W[O,K]^T. Any shape. */
+hipError_t ghip_launch_bf16_linear(const uint16_t *w, const uint16_t *x,
+                                   uint16_t *y, size_t M, size_t O, size_t K,
+                                   hipStream_t st);
+
+/* K3 MoE decode state: counters that the kernel leaves at zero on exit
+ * (allocated zeroed once, never cleared with a memset in the hot path). */
+typedef struct {
+    uint32_t *counters;   /* device, GHIP_MOE_DEC_COUNTERS u32 */
+    uint16_t *h;          /* device [topk, inter] bf16 */
+    uint16_t *contrib;    /* device [topk, dim] bf16 */
+    uint32_t *err;        /* device u32: nonzero after a bounded wait expired */
+} GhipMoeDecodeWs;
+
+#define GHIP_MOE_DEC_COUNTERS 4096
+
+/* Expert bank view for the kernels: slab s of expert e at base + e*stride;
+ * member byte offsets inside a slab (c/gcache.h:852-861 order). */
+typedef struct {
+    const uint8_t *base;
+    size_t stride;               /* bytes between consecutive slabs */
+    size_t off_gw, off_gs, off_uw, off_us, off_dw, off_ds;
+    uint32_t n_experts, dim, inter;
+    const uint32_t *nan_flags;   /* device [n_experts] u32 or NULL */
+} GhipBank;
+
+/* K3: routed MoE decode for one token, one launch. Either logits (device
+ * f32 [n_experts], the kernel computes top-k + softmax) or idx/w (device
+ * [topk]) must be given. out: device [dim] bf16. */
+hipError_t ghip_launch_moe_decode(const GhipBank *bank, const uint16_t *x,
+                                  const float *logits, const int32_t *idx,
+                                  const float *w, int topk, float limit,
+                                  uint16_t *out, const GhipMoeDecodeWs *ws,
+                                  hipStream_t st);
+
+/* Fill n u32 words with value (a kernel, not a memset, so callers may
+ * capture it in a graph). */
+hipError_t ghip_launch_fill_u32(uint32_t *p, size_t n, uint32_t value,
+                                hipStream_t st);
+
+/* Device fill of synthetic FP8 codes (same bytes as apus_synth_fp8_codes). */
+hipError_t ghip_launch_synth_codes(uint8_t *out, size_t n, uint64_t key,
+                                   uint64_t offset, hipStream_t st);
+/* Device fill of bf16 N(0,1) through a device copy of the quantile table. */
+hipError_t ghip_launch_synth_bf16(uint16_t *out, size_t n, uint64_t key,
+                                  uint64_t offset, const uint16_t *table,
+                                  hipStream_t st);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GHIP_INTERNAL_H */

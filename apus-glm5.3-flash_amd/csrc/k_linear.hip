@@ -1,0 +1,324 @@
+/*
+ * k_linear.hip — gfx950 kernels for the dense FP8-block path:
+ *   K1  k_dequant16 / k_dequant_any : FP8-E4M3 + F32 128x128 scales -> BF16,
+ *       bit-exact vs c/fp8blk.h:115-136 (apus_fp8blk_rows_scalar).
+ *   K2  k_fp8_gemv : decode / MTP-verify GEMV (M <= 4 per launch) with the
+ *       dequant fused in registers and the k reduction on MFMA
+ *       (v_mfma_f32_16x16x32_bf16), the composition of c/gdsa.h:525-534
+ *       (dequant -> bf16 -> fp32-accumulated GEMM -> RNE bf16).
+ *   k_fp8_linear_any / k_bf16_linear_any : shape-general fallbacks (ceil
+ *       shapes, K not a multiple of 64) with the exact integer decode.
+ *   k_nan_scan : flags the out-of-contract NaN codes 0x7F/0xFF so callers
+ *       can select the exact decode for such weights.
+ *
+ * GEMV tiling (K2). A workgroup owns 16 consecutive output rows; its NW
+ * waves split K into 64-wide chunks (wave w takes chunks w, w+NW, ...). Per
+ * chunk, lane l loads 16 codes of row (l % 16) at k offset 16*(l / 16)
+ * (one 16-byte load; a wave load covers 16 rows x 64 contiguous bytes),
+ * dequantizes them to two bf16x8 operands and issues two MFMAs whose A
+ * operand is x staged in LDS. The MFMA k-slot
+ * to k mapping is any permutation used identically for A and B, so the
+ * result is an exact-product fp32 sum in a different order than the
+ * reference's sequential k: a tolerance-class result, per the contract.
+ * Partial sums of the NW waves are combined in LDS in a fixed order, so the
+ * output is deterministic run to run.
+ */
+#include "ghip_device.h"
+#include "ghip_internal.h"
+
+#define GEMV_NW 8          /* waves per workgroup (k split) */
+#define GEMV_U 8           /* 16-byte loads in flight per lane per batch */
+
+/* ------------------------------------------------------------------------ */
+/* K1: dequant                                                              */
+/* ------------------------------------------------------------------------ */
+
+/* K % 16 == 0: one thread per 16 consecutive codes of a row (they share
+ * one 128-block scale because 16 divides 128). */
+template <bool EXACT>
+__global__ __launch_bounds__(256) void k_dequant16(
+    const uint8_t *__restrict__ w, const float *__restrict__ s,
+    uint16_t *__restrict__ out, uint32_t O, uint32_t K, uint32_t nkb) {
+    const uint32_t cpr = K >> 4;                       /* chunks per row */
+    const size_t n = (size_t)O * cpr;
+    for (size_t c = (size_t)blockIdx.x * 256 + threadIdx.x; c < n;
+         c += (size_t)gridDim.x * 256) {
+        uint32_t o = (uint32_t)(c / cpr);
+        uint32_t k0 = (uint32_t)(c - (size_t)o * cpr) << 4;
+        float sc = s[(size_t)(o >> 7) * nkb + (k0 >> 7)];
+        ghip_u32x4 v = *(const ghip_u32x4 *)(w + (size_t)o * K + k0);
+        ghip_u32x4 r0, r1;
+        ghip_deq16_u32<EXACT>(v, sc, r0, r1);
+        ghip_u32x4 *dst = (ghip_u32x4 *)(out + (size_t)o * K + k0);
+        dst[0] = r0;
+        dst[1] = r1;
+    }
+}
+
+/* Any K: one thread per element, exact integer path. */
+__global__ __launch_bounds__(256) void k_dequant_any(
+    const uint8_t *__restrict__ w, const float *__restrict__ s,
+    uint16_t *__restrict__ out, uint32_t O, uint32_t K, uint32_t nkb) {
+    const size_t n = (size_t)O * K;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * 256) {
+        uint32_t o = (uint32_t)(i / K), k = (uint32_t)(i - (size_t)o * K);
+        float sc = s[(size_t)(o >> 7) * nkb + (k >> 7)];
+        out[i] = (uint16_t)ghip_bf16_bits(ghip_e4m3_exact(w[i]) * sc);
+    }
+}
+
+/* NaN-code scan: bytes whose low 7 bits are all ones (0x7F / 0xFF). */
+__global__ __launch_bounds__(256) void k_nan_scan(
+    const uint8_t *__restrict__ p, size_t n, uint32_t *flag) {
+    const size_t nv = n >> 4;
+    uint32_t hit = 0;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < nv;
+         i += (size_t)gridDim.x * 256) {
+        ghip_u32x4 v = *(const ghip_u32x4 *)(p + (i << 4));
+        for (int j = 0; j < 4; j++)
+            hit |= ((v[j] & 0x7f7f7f7fu) + 0x01010101u) & 0x80808080u;
+    }
+    if (blockIdx.x == 0)
+        for (size_t i = (nv << 4) + threadIdx.x; i < n; i += 256)
+            hit |= ((p[i] & 0x7fu) == 0x7fu);
+    if (hit) atomicOr(flag, 1u);
+}
+
+/* ------------------------------------------------------------------------ */
+/* K2: FP8 GEMV, M <= 4, K % 64 == 0                                        */
+/* ------------------------------------------------------------------------ */
+
+template <int M, bool EXACT>
+__device__ __forceinline__ ghip_f32x4 gemv16_rows(
+    const uint8_t *__restrict__ wr, const float *__restrict__ srow,
+    const uint16_t *xa, uint32_t nch, uint32_t wv) {
+    ghip_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (uint32_t c0 = wv; c0 < nch; c0 += GEMV_NW * GEMV_U) {
+        ghip_u32x4 buf[GEMV_U];
+#pragma unroll
+        for (int u = 0; u < GEMV_U; u++) {
+            uint32_t c = c0 + u * GEMV_NW;
+            if (c < nch) buf[u] = __builtin_nontemporal_load(
+                (const ghip_u32x4 *)(wr + (size_t)c * 64));
+        }
+#pragma unroll
+        for (int u = 0; u < GEMV_U; u++) {
+            uint32_t c = c0 + u * GEMV_NW;
+            if (c < nch) {
+                float sc = srow[c >> 1];
+                ghip_bf16x8 b0, b1;
+                ghip_deq16<EXACT>(buf[u], sc, b0, b1);
+                ghip_bf16x8 a0 = *(const ghip_bf16x8 *)(xa + c * 64);
+                ghip_bf16x8 a1 = *(const ghip_bf16x8 *)(xa + c * 64 + 8);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1, acc, 0, 0, 0);
+            }
+        }
+    }
+    return acc;
+}
+
+template <int M>
+__global__ __launch_bounds__(GEMV_NW * 64) void k_fp8_gemv(
+    const uint8_t *__restrict__ W, const float *__restrict__ S,
+    const uint16_t *__restrict__ X, uint16_t *__restrict__ Y, uint32_t O,
+    uint32_t K, uint32_t nkb, const uint32_t *__restrict__ exact_flag) {
+    extern __shared__ __align__(16) uint16_t xs[];     /* M x K */
+    __shared__ float red[GEMV_NW][M][16];
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    /* stage x rows 0..M-1 (16-byte vectors) */
+    const uint32_t nvec = (M * K) >> 3;
+    for (uint32_t i = tid; i < nvec; i += GEMV_NW * 64)
+        *(ghip_u32x4 *)(xs + ((size_t)i << 3)) =
+            *(const ghip_u32x4 *)(X + ((size_t)i << 3));
+    __syncthreads();
+    const bool exact = exact_flag != nullptr && *exact_flag != 0u;
+    const uint32_t row0 = blockIdx.x * 16u;
+    const uint32_t n = lane & 15u, g = lane >> 4;
+    const uint32_t row = min(row0 + n, O - 1u);
+    const uint8_t *wr = W + (size_t)row * K + 16u * g;
+    const float *srow = S + (size_t)(row0 >> 7) * nkb;
+    /* MFMA A row i = lane % 16 is token m; rows m >= M only feed output
+     * rows that are discarded, so they read row M-1 instead of zeros. */
+    const uint16_t *xa = xs + (size_t)min(n, (uint32_t)M - 1u) * K + 16u * g;
+    const uint32_t nch = K >> 6;
+    ghip_f32x4 acc = exact ? gemv16_rows<M, true>(wr, srow, xa, nch, wv)
+                           : gemv16_rows<M, false>(wr, srow, xa, nch, wv);
+    if (g == 0) {
+#pragma unroll
+        for (int i = 0; i < M; i++) red[wv][i][n] = acc[i];
+    }
+    __syncthreads();
+    if (tid < (uint32_t)M * 16u) {
+        uint32_t m = tid >> 4, nn = tid & 15u;
+        float s = 0.0f;
+#pragma unroll
+        for (int w = 0; w < GEMV_NW; w++) s += red[w][m][nn];
+        if (row0 + nn < O) Y[(size_t)m * O + row0 + nn] = (uint16_t)ghip_bf16_bits(s);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* shape-general fallbacks: one wave per (row, m), exact decode             */
+/* ------------------------------------------------------------------------ */
+
+__device__ __forceinline__ float wave_sum(float v) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__global__ __launch_bounds__(256) void k_fp8_linear_any(
+    const uint8_t *__restrict__ W, const float *__restrict__ S,
+    const uint16_t *__restrict__ X, uint16_t *__restrict__ Y, uint32_t M,
+    uint32_t O, uint32_t K, uint32_t nkb) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const size_t item = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (item >= (size_t)M * O) return;
+    const uint32_t m = (uint32_t)(item / O), o = (uint32_t)(item - (size_t)m * O);
+    const uint8_t *wr = W + (size_t)o * K;
+    const float *srow = S + (size_t)(o >> 7) * nkb;
+    const uint16_t *xr = X + (size_t)m * K;
+    float acc = 0.0f;
+    for (uint32_t k = lane; k < K; k += 64) {
+        float wv = ghip_bf16_round(ghip_e4m3_exact(wr[k]) * srow[k >> 7]);
+        acc += wv * ghip_bf16_f32(xr[k]);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) Y[(size_t)m * O + o] = (uint16_t)ghip_bf16_bits(acc);
+}
+
+__global__ __launch_bounds__(256) void k_bf16_linear_any(
+    const uint16_t *__restrict__ W, const uint16_t *__restrict__ X,
+    uint16_t *__restrict__ Y, uint32_t M, uint32_t O, uint32_t K) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const size_t item = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (item >= (size_t)M * O) return;
+    const uint32_t m = (uint32_t)(item / O), o = (uint32_t)(item - (size_t)m * O);
+    const uint16_t *wr = W + (size_t)o * K;
+    const uint16_t *xr = X + (size_t)m * K;
+    float acc = 0.0f;
+    for (uint32_t k = lane; k < K; k += 64)
+        acc += ghip_bf16_f32(wr[k]) * ghip_bf16_f32(xr[k]);
+    acc = wave_sum(acc);
+    if (lane == 0) Y[(size_t)m * O + o] = (uint16_t)ghip_bf16_bits(acc);
+}
+
+/* ------------------------------------------------------------------------ */
+/* launchers                                                                */
+/* ------------------------------------------------------------------------ */
+
+static uint32_t grid_for(size_t items, size_t per_block, uint32_t cap) {
+    size_t g = (items + per_block - 1) / per_block;
+    if (g < 1) g = 1;
+    if (g > cap) g = cap;
+    return (uint32_t)g;
+}
+
+extern "C" hipError_t ghip_launch_dequant(const uint8_t *codes,
+                                          const float *scales, uint16_t *out,
+                                          size_t O, size_t K, int exact,
+                                          hipStream_t st) {
+    if (O == 0 || K == 0) return hipSuccess;
+    if (O > 0xffffffffu || K > 0xffffffffu) return hipErrorInvalidValue;
+    uint32_t nkb = (uint32_t)((K + 127) / 128);
+    bool aligned = (K % 16 == 0) && (((uintptr_t)codes & 15) == 0)
+                && (((uintptr_t)out & 15) == 0);
+    if (aligned) {
+        uint32_t g = grid_for(O * (K / 16), 256, 65536);
+        if (exact)
+            hipLaunchKernelGGL(k_dequant16<true>, dim3(g), dim3(256), 0, st,
+                               codes, scales, out, (uint32_t)O, (uint32_t)K, nkb);
+        else
+            hipLaunchKernelGGL(k_dequant16<false>, dim3(g), dim3(256), 0, st,
+                               codes, scales, out, (uint32_t)O, (uint32_t)K, nkb);
+    } else {
+        uint32_t g = grid_for(O * K, 256, 65536);
+        hipLaunchKernelGGL(k_dequant_any, dim3(g), dim3(256), 0, st, codes,
+                           scales, out, (uint32_t)O, (uint32_t)K, nkb);
+    }
+    return hipGetLastError();
+}
+
+extern "C" hipError_t ghip_launch_nan_scan(const uint8_t *codes, size_t n,
+                                           uint32_t *flag, hipStream_t st) {
+    if (n == 0) return hipSuccess;
+    if (((uintptr_t)codes & 15) != 0) return hipErrorInvalidValue;
+    uint32_t g = grid_for(n / 16 + 1, 256 * 8, 4096);
+    hipLaunchKernelGGL(k_nan_scan, dim3(g), dim3(256), 0, st, codes, n, flag);
+    return hipGetLastError();
+}
+
+template <int M>
+static hipError_t launch_gemv_m(const uint8_t *codes, const float *scales,
+                                const uint16_t *x, uint16_t *y, size_t O,
+                                size_t K, const uint32_t *exact_dev,
+                                hipStream_t st) {
+    size_t lds = (size_t)M * K * 2;
+    uint32_t nkb = (uint32_t)((K + 127) / 128);
+    uint32_t g = (uint32_t)((O + 15) / 16);
+    hipLaunchKernelGGL(k_fp8_gemv<M>, dim3(g), dim3(GEMV_NW * 64), lds, st,
+                       codes, scales, x, y, (uint32_t)O, (uint32_t)K, nkb,
+                       exact_dev);
+    return hipGetLastError();
+}
+
+/* Largest dynamic LDS the GEMV stages x into (per workgroup). */
+#define GEMV_LDS_MAX (48u * 1024u)
+
+extern "C" hipError_t ghip_launch_fp8_linear(const uint8_t *codes,
+                                             const float *scales,
+                                             const uint16_t *x, uint16_t *y,
+                                             size_t M, size_t O, size_t K,
+                                             const uint32_t *exact_dev,
+                                             hipStream_t st) {
+    if (M == 0 || O == 0) return hipSuccess;
+    if (K == 0 || O > 0x7fffffffu || K > 0x7fffffffu || M > 0x7fffffffu)
+        return hipErrorInvalidValue;
+    bool fast = (K % 64 == 0) && (((uintptr_t)codes & 15) == 0)
+             && (((uintptr_t)x & 15) == 0) && K * 2 <= GEMV_LDS_MAX;
+    if (!fast) {
+        uint32_t nkb = (uint32_t)((K + 127) / 128);
+        size_t items = M * O;
+        if (items > 0xffffffffull * 4) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(k_fp8_linear_any, dim3((uint32_t)((items + 3) / 4)),
+                           dim3(256), 0, st, codes, scales, x, y, (uint32_t)M,
+                           (uint32_t)O, (uint32_t)K, nkb);
+        return hipGetLastError();
+    }
+    /* m-groups of up to 4 rows, each as large as the x staging allows */
+    size_t m0 = 0;
+    while (m0 < M) {
+        size_t mc = M - m0;
+        if (mc > 4) mc = 4;
+        while (mc > 1 && mc * K * 2 > GEMV_LDS_MAX) mc--;
+        const uint16_t *xm = x + m0 * K;
+        uint16_t *ym = y + m0 * O;
+        hipError_t e;
+        switch (mc) {
+        case 4: e = launch_gemv_m<4>(codes, scales, xm, ym, O, K, exact_dev, st); break;
+        case 3: e = launch_gemv_m<3>(codes, scales, xm, ym, O, K, exact_dev, st); break;
+        case 2: e = launch_gemv_m<2>(codes, scales, xm, ym, O, K, exact_dev, st); break;
+        default: e = launch_gemv_m<1>(codes, scales, xm, ym, O, K, exact_dev, st); break;
+        }
+        if (e != hipSuccess) return e;
+        m0 += mc;
+    }
+    return hipSuccess;
+}
+
+extern "C" hipError_t ghip_launch_bf16_linear(const uint16_t *w,
+                                              const uint16_t *x, uint16_t *y,
+                                              size_t M, size_t O, size_t K,
+                                              hipStream_t st) {
+    if (M == 0 || O == 0) return hipSuccess;
+    if (K == 0 || O > 0x7fffffffu || K > 0x7fffffffu || M > 0x7fffffffu)
+        return hipErrorInvalidValue;
+    size_t items = M * O;
+    if (items > 0xffffffffull * 4) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_bf16_linear_any, dim3((uint32_t)((items + 3) / 4)),
+                       dim3(256), 0, st, w, x, y, (uint32_t)M, (uint32_t)O,
+                       (uint32_t)K);
+    return hipGetLastError();
+}

@@ -1,0 +1,193 @@
+/*
+ * include/backend_hip.h — MI355X (gfx950) backend for the apus GLM-5.3-Flash
+ * dense FP8-block / BF16 compute and the routed-expert SwiGLU. Pure C ABI,
+ * implemented by libapus_ghip.so (C host layer + hand-written HIP kernels).
+ *
+ * DROP-IN BOUNDARY. The first block mirrors the reference's Metal backend
+ * interface c/backend_gmetal.h one for one (the g-prefix "gmetal" becomes
+ * "ghip"); the engine's call sites (c/bf16.h:717-719, 743-745 and
+ * c/gdsa.h:529-531) try the hook first and fall back to the pinned CPU
+ * kernel when the pointer is NULL or the call returns nonzero — per-op
+ * fail-soft, never a crash. The hook table is all-NULL until
+ * apus_ghip_enable() succeeds.
+ *
+ * NUMERICS CONTRACT (differs from the Metal backend's, which is bitwise):
+ *   - FP8-block dequant (apus_ghip_fp8blk_dequant*, and every kernel that
+ *     consumes FP8 weights): BITWISE equal to c/fp8blk.h
+ *     (bf16_rne(e4m3(code) * scale), one fp32 multiply; NaN codes 0x7F/0xFF
+ *     decode as +-480 like c/num.h:136-141).
+ *   - GEMV/GEMM outputs: the products of bf16 operands are exact in fp32 and
+ *     are accumulated in fp32 in a blocked order (MFMA k-slices and a fixed
+ *     cross-wave reduction) instead of the reference's strictly sequential k
+ *     (c/bf16.h:27-37). Results agree with the CPU kernels to <= 1 bf16 ulp
+ *     on >= 99.9% of elements, max relative error 1e-2 against
+ *     max(|ref|, 2^-12 * sum_k |w*x|). Deterministic run to run.
+ *   - SwiGLU / combine: the reference's clamp order, bf16 roundings and
+ *     ascending-expert bf16-per-add combine (c/gmoe.h:210-227, 307-320);
+ *     sigmoid uses the device expf (tolerance class as above).
+ *
+ * BUFFERS. Discrete HBM, no zero-copy: host-pointer entry points copy x in
+ * and y out on every call and keep weights resident only for REGISTERED
+ * regions (uploaded once at registration, looked up by host range like
+ * c/backend_gmetal.mm:240-251). Unregistered weights are uploaded per op.
+ * The *_dev entry points take device pointers and a hipStream_t and are
+ * asynchronous; the expert store keeps whole expert slabs resident in HBM.
+ *
+ * THREADING. Host-pointer entry points are synchronous (one stream, waited
+ * on before return) and compute-thread only, as the Metal backend
+ * (c/backend_gmetal.h:97-99). *_dev calls are stream-ordered; calls that
+ * share an expert store's decode workspace must not overlap in time.
+ *
+ * ENV KNOBS (read once at apus_ghip_enable, like c/backend_gmetal.mm:437-453):
+ *   APUS_GHIP_MIN_KB      BF16 hook floor: weights below it stay on the CPU
+ *                         (default 0 = offload all).
+ *   APUS_GHIP_FP8_MIN_KB  FP8 hook floor (default 0).
+ *   APUS_GHIP_MAX_M       activation rows above it stay on the CPU
+ *                         (default 0 = unlimited).
+ *   APUS_GHIP_DEVICE      HIP device ordinal (default 0).
+ */
+#ifndef APUS_BACKEND_HIP_H
+#define APUS_BACKEND_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ======================================================================== */
+/* 1. Mirror of c/backend_gmetal.h                                           */
+/* ======================================================================== */
+
+/* Hook table — replaces ApusGmetalHooks (c/backend_gmetal.h:120-126); same
+ * two signatures byte for byte. 0 = produced the result; nonzero = declined
+ * (the caller runs its CPU kernel). Shapes: w/codes [O,K] row-major, scales
+ * [ceil(O/128)*ceil(K/128)] F32, x [M,K] and y [M,O] BF16 codes. */
+typedef struct {
+    int (*bf16_gemm)(const uint16_t *w, const uint16_t *x, uint16_t *y,
+                     size_t M, size_t O, size_t K);
+    int (*fp8blk_linear)(const uint8_t *codes, const float *scales,
+                         const uint16_t *x, uint16_t *y,
+                         size_t M, size_t O, size_t K);
+} ApusGhipHooks;
+
+/* replaces `extern ApusGmetalHooks apus_gmetal_hooks;` (c/backend_gmetal.h:128).
+ * The library carries a weak definition so a standalone process links; an
+ * engine TU that defines the table (as c/bf16.h:162 does for Metal) wins. */
+extern ApusGhipHooks apus_ghip_hooks;
+
+/* replaces apus_gmetal_enable / _disable / _is_enabled
+ * (c/backend_gmetal.h:134-137). enable: select the device, create the
+ * backend stream, read the env floors, fill the hooks. 0 = ok; nonzero with
+ * err filled when no usable gfx950 device is present. Idempotent. */
+int  apus_ghip_enable(char *err, size_t errcap);
+void apus_ghip_disable(void);
+int  apus_ghip_is_enabled(void);
+
+/* replaces apus_gmetal_register_region / _unregister_region
+ * (c/backend_gmetal.h:147-148): upload a MODEL-OWNED weight region to HBM
+ * once; later ops whose weight range lies inside it use the device mirror.
+ * 0 = ok, nonzero = not registered (ops fall back to per-op uploads).
+ * Idempotent per pointer; the caller unregisters before freeing. */
+int  apus_ghip_register_region(const void *ptr, size_t len);
+void apus_ghip_unregister_region(const void *ptr);
+
+/* replaces the counters of c/backend_gmetal.h:153-157. bytes_wrapped =
+ * per-op weight uploads (no zero-copy on discrete HBM), bytes_pinned =
+ * registered device-mirror bytes. Plus the host<->device copy totals. */
+uint64_t apus_ghip_bytes_wrapped(void);
+uint64_t apus_ghip_bytes_pinned(void);
+uint64_t apus_ghip_dispatches(void);
+uint64_t apus_ghip_offload_bf16(void);
+uint64_t apus_ghip_offload_fp8blk(void);
+uint64_t apus_ghip_bytes_h2d(void);
+uint64_t apus_ghip_bytes_d2h(void);
+
+/* replaces apus_gmetal_bf16_gemm / apus_gmetal_fp8blk_linear
+ * (c/backend_gmetal.h:162-166): direct entry points, no floors, lazy init.
+ * 0 = ok, 1 = no device / unsupported / failure. */
+int apus_ghip_bf16_gemm(const uint16_t *w, const uint16_t *x, uint16_t *y,
+                        size_t M, size_t O, size_t K);
+int apus_ghip_fp8blk_linear(const uint8_t *codes, const float *scales,
+                            const uint16_t *x, uint16_t *y,
+                            size_t M, size_t O, size_t K);
+
+/* Last error message of the calling process ("" when none). */
+const char *apus_ghip_last_error(void);
+
+/* ======================================================================== */
+/* 2. Extensions (no Metal counterpart)                                      */
+/* ======================================================================== */
+
+/* FP8-block dequant to BF16 on the device (K1). Replaces the CPU
+ * apus_fp8blk_dequant / _mt (c/fp8blk.h:115-136, 277-317) for callers that
+ * want BF16 weights (e.g. dequant-on-fill, c/gcache.h:413-426). Host
+ * pointers, synchronous. Bitwise equal to the CPU result. */
+int apus_ghip_fp8blk_dequant(const uint8_t *codes, const float *scales,
+                             uint16_t *out, size_t O, size_t K);
+
+/* Device-pointer variants (asynchronous on `stream`, a hipStream_t; NULL =
+ * the null stream). exact: 0 = fast decode (caller guarantees no 0x7F/0xFF
+ * code), 1 = exact integer decode, -1 = scan the codes first and pick. */
+int apus_ghip_fp8blk_dequant_dev(const uint8_t *codes, const float *scales,
+                                 uint16_t *out, size_t O, size_t K,
+                                 int exact, void *stream);
+int apus_ghip_fp8blk_linear_dev(const uint8_t *codes, const float *scales,
+                                const uint16_t *x, uint16_t *y,
+                                size_t M, size_t O, size_t K,
+                                int exact, void *stream);
+int apus_ghip_bf16_gemm_dev(const uint16_t *w, const uint16_t *x,
+                            uint16_t *y, size_t M, size_t O, size_t K,
+                            void *stream);
+
+/* --- HBM-resident expert slab store (replaces the ApusGcacheW views of
+ * c/gcache.h:592-643 behind the expert seam c/gmodel.h:1155-1178). One
+ * device arena holds every expert's FP8 slab in the reference member order
+ * gate.w | gate.s | up.w | up.s | down.w | down.s (c/gcache.h:852-861):
+ * 2*(inter*dim + nb) + dim*inter + nb bytes per slab, nb = F32 scale bytes;
+ * 25,171,968 B at dim 4096 / inter 2048. Slabs stay FP8 in HBM; kernels
+ * dequantize on the fly (bit-exact). */
+typedef struct ApusGhipStore ApusGhipStore;
+
+/* Allocate the arena for n_experts slabs (+ the decode workspace). limit =
+ * swiglu_limit (10 for GLM-5.3-Flash, reference/config.json:253). */
+int apus_ghip_store_open(ApusGhipStore **out, int n_experts, size_t dim,
+                         size_t inter, float limit, char *err, size_t errcap);
+void apus_ghip_store_close(ApusGhipStore *s);
+size_t apus_ghip_store_slab_bytes(const ApusGhipStore *s);
+/* One H2D copy of one slab (the reference's one pread per slab). Scans the
+ * codes for NaN codes and records the decode path for the expert. */
+int apus_ghip_store_put(ApusGhipStore *s, int expert, const void *slab,
+                        size_t nbytes);
+/* Fill every slab with the deterministic synthetic generator
+ * (include/apus_synth.h; bank id selects the streams): codes on device,
+ * scales log-uniform in [scale_lo, scale_hi] from the host. */
+int apus_ghip_store_synth(ApusGhipStore *s, uint64_t seed, int bank,
+                          float scale_lo, float scale_hi);
+/* Device address of expert e's slab (NULL when out of range). */
+const void *apus_ghip_store_slab_dev(const ApusGhipStore *s, int expert);
+/* Dequant-on-fill: expert e's BF16 payload [gate | up | down] into a host
+ * buffer (3*inter*dim u16), bitwise c/gcache.h:413-426. */
+int apus_ghip_store_expert_bf16(ApusGhipStore *s, int expert,
+                                uint16_t *payload);
+
+/* --- routed MoE decode (one token): SwiGLU experts + ordered combine,
+ * c/gmoe.h:210-227 + 307-320 without the router and shared expert. One
+ * kernel launch: gate/up GEMVs with the SwiGLU epilogue, down GEMVs, and
+ * the ascending-expert bf16-per-add combine.
+ * Routing either given (idx/w [topk]) or computed on the device from
+ * logits [n_experts] f32: stable top-k (ties -> lower id), w = softmax over
+ * the k selected logits. Host-pointer variant is synchronous. */
+int apus_ghip_moe_decode(ApusGhipStore *s, const uint16_t *x,
+                         const int32_t *idx, const float *w, int topk,
+                         uint16_t *out);
+int apus_ghip_moe_decode_dev(ApusGhipStore *s, const uint16_t *x,
+                             const float *logits, const int32_t *idx,
+                             const float *w, int topk, uint16_t *out,
+                             void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* APUS_BACKEND_HIP_H */

@@ -1,0 +1,216 @@
+#!/usr/bin/env python3
+"""Golden fixtures for the FP8-block MoE hot path, computed by the
+REFERENCE's own CPU kernels (oracle/_ref/libapusref.so, compiled from
+/root/reference/c by oracle/Makefile) — run in the development container,
+where the reference tree exists. The GPU box never runs this script; it only
+reads the committed fixtures.
+
+Inputs follow the reference's generators in spirit (tests/m3g/gen_golden.py
+shapes, edge-code injection and scale corners; tests/m4g expert cases) but
+are drawn here with numpy RandomState seeds or the shared synthetic
+generator (include/apus_synth.h); only the expected OUTPUTS come from the
+reference kernels:
+  apus_fp8blk_dequant_scalar  (c/fp8blk.h:115-136)
+  apus_bf16_gemm_scalar       (c/bf16.h:213-217)
+  apus_fp8blk_dequant + apus_bf16_gemm (c/gdsa.h:532-533 composition)
+  apus_gmoe_expert            (c/gmoe.h:210-227)
+The MoE combine of the BASELINE config 2 case applies the reference loop
+(c/gmoe.h:314-320) to the reference expert outputs.
+
+Writes tests/golden/fixtures.npz and tests/golden/manifest.json.
+"""
+import hashlib
+import json
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, os.path.join(ROOT, "oracle"))
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+
+import oracle as O  # noqa: E402
+from conftest import load_pkg  # noqa: E402
+
+R = O.ref()
+P = O.ptr
+SYN = load_pkg().load()
+
+DEQ_SHAPES = [(128, 128), (256, 384), (200, 136), (1, 128), (384, 128),
+              (160, 200), (128, 127), (300, 264), (5, 129)]
+GEM_SHAPES = [(1, 1, 1), (1, 3, 5), (2, 8, 32), (1, 7, 33), (4, 16, 128),
+              (5, 17, 129), (8, 64, 256), (3, 13, 200), (1, 128, 384),
+              (7, 200, 160), (2, 33, 31), (6, 40, 100), (1, 256, 128)]
+LIN_SHAPES = [(1, 128, 256), (4, 256, 512), (3, 200, 300), (1, 384, 1024)]
+EDGE = np.array([0x00, 0x80, 0x01, 0x07, 0x08, 0x38, 0x7E, 0xFE, 0xC0, 0x81,
+                 0x77, 0x6F], np.uint8)
+SCALE_CORNERS = [1.0, 0.0, 2.0 ** -126, 2.0 ** -127, 2.0 ** 40, 0.5]
+LIMIT = 10.0
+
+
+def digest(*arrays):
+    h = hashlib.sha256()
+    for a in arrays:
+        h.update(np.ascontiguousarray(a).tobytes())
+    return h.hexdigest()[:16]
+
+
+def rand_codes(rng, shape):
+    c = rng.randint(0, 256, size=shape).astype(np.uint8)
+    c[c == 0x7F] = 0x7E
+    c[c == 0xFF] = 0xFE
+    return c
+
+
+def rand_scales(rng, shape):
+    s = np.exp2(rng.uniform(-20.0, 20.0, size=shape)).astype(np.float32)
+    flat = s.reshape(-1)
+    for i, c in enumerate(SCALE_CORNERS):
+        if i < flat.size:
+            flat[i] = c
+    return s
+
+
+def ref_dequant(codes, scales):
+    O_, K = codes.shape
+    out = np.empty((O_, K), np.uint16)
+    R.ref_fp8blk_dequant_scalar(P(codes), P(scales), P(out), O_, K)
+    return out
+
+
+def ref_gemm(w, x):
+    O_, K = w.shape
+    M = x.shape[0]
+    y = np.empty((M, O_), np.uint16)
+    R.ref_bf16_gemm_scalar(P(w), P(x), P(y), M, O_, K)
+    return y
+
+
+def ref_expert(payload_g, payload_u, payload_d, x):
+    inter, dim = payload_g.shape
+    out = np.empty(dim, np.uint16)
+    assert R.ref_gmoe_expert(P(payload_g), P(payload_u), P(payload_d), P(x),
+                             dim, inter, LIMIT, P(out)) == 0
+    return out
+
+
+def bf16_round(v):
+    return O.bf16_to_f32(O.f32_to_bf16(np.float32(v)))
+
+
+def synth_linear(seed, M, N, K):
+    """BASELINE configs 0/1 inputs from the shared generator."""
+    codes = np.empty((N, K), np.uint8)
+    SYN.apus_synth_fp8_codes(P(codes), codes.size, seed, 10, 0)
+    scales = np.empty((O.nblocks(N), O.nblocks(K)), np.float32)
+    SYN.apus_synth_scales(P(scales), scales.size, seed, 11, 1e-4, 1e-2)
+    x = np.empty((M, K), np.uint16)
+    SYN.apus_synth_bf16_normal(P(x), x.size, seed, 12, 0)
+    return codes, scales, x
+
+
+def synth_slab(seed, bank, e, dim, inter):
+    """One expert's three FP8 members + scales (include/apus_synth.h)."""
+    mats = []
+    for j, (o, k) in enumerate([(inter, dim), (inter, dim), (dim, inter)]):
+        c = np.empty((o, k), np.uint8)
+        SYN.apus_synth_fp8_codes(P(c), c.size, seed,
+                                 SYN.apus_synth_expert_stream(bank, e, 2 * j), 0)
+        s = np.empty((O.nblocks(o), O.nblocks(k)), np.float32)
+        SYN.apus_synth_scales(P(s), s.size, seed,
+                              SYN.apus_synth_expert_stream(bank, e, 2 * j + 1),
+                              1e-4, 1e-2)
+        mats.append((c, s))
+    return mats
+
+
+def main():
+    fx = {}
+    man = {"dequant": [], "gemm": [], "linear": [], "expert": [],
+           "config0": {}, "config1": {}, "config2": {}}
+    rng = np.random.RandomState(0x33)
+    for i, (o, k) in enumerate(DEQ_SHAPES):
+        codes = rand_codes(rng, (o, k))
+        codes.reshape(-1)[:EDGE.size] = EDGE[:codes.size]
+        scales = rand_scales(rng, (O.nblocks(o), O.nblocks(k)))
+        fx[f"deq{i}_codes"], fx[f"deq{i}_scales"] = codes, scales
+        fx[f"deq{i}_out"] = ref_dequant(codes, scales)
+        man["dequant"].append({"O": o, "K": k})
+    for i, (m, o, k) in enumerate(GEM_SHAPES):
+        w = O.f32_to_bf16(rng.uniform(-2, 2, (o, k)).astype(np.float32))
+        x = O.f32_to_bf16(rng.uniform(-2, 2, (m, k)).astype(np.float32))
+        w.reshape(-1)[0] = 0x0000
+        if w.size > 1:
+            w.reshape(-1)[1] = 0x8000
+        fx[f"gem{i}_w"], fx[f"gem{i}_x"] = w, x
+        fx[f"gem{i}_y"] = ref_gemm(w, x)
+        man["gemm"].append({"M": m, "O": o, "K": k})
+    for i, (m, o, k) in enumerate(LIN_SHAPES):
+        codes = rand_codes(rng, (o, k))
+        scales = np.exp2(rng.uniform(-12, -4, (O.nblocks(o), O.nblocks(k)))).astype(np.float32)
+        x = O.f32_to_bf16(rng.standard_normal((m, k)).astype(np.float32))
+        fx[f"lin{i}_codes"], fx[f"lin{i}_scales"], fx[f"lin{i}_x"] = codes, scales, x
+        fx[f"lin{i}_y"] = ref_gemm(ref_dequant(codes, scales), x)
+        man["linear"].append({"M": m, "O": o, "K": k})
+    # expert cases (tests/m4g xp0-2 shapes: d=256, inter 128/256; xp1
+    # saturating with x_std = 8 so the clamps fire)
+    for i, (dim, inter, xstd) in enumerate([(256, 128, 1.0), (256, 128, 8.0),
+                                            (256, 256, 1.0)]):
+        mats = []
+        for (o, k) in [(inter, dim), (inter, dim), (dim, inter)]:
+            c = rand_codes(rng, (o, k))
+            s = np.exp2(rng.uniform(-9, -5, (O.nblocks(o), O.nblocks(k)))).astype(np.float32)
+            mats.append((c, s))
+        x = O.f32_to_bf16((rng.standard_normal(dim) * xstd).astype(np.float32))
+        pl = [ref_dequant(c, s) for c, s in mats]
+        fx[f"xp{i}_x"] = x
+        for j, nm in enumerate("gud"):
+            fx[f"xp{i}_{nm}_codes"], fx[f"xp{i}_{nm}_scales"] = mats[j]
+        fx[f"xp{i}_out"] = ref_expert(pl[0], pl[1], pl[2], x)
+        man["expert"].append({"dim": dim, "inter": inter, "x_std": xstd})
+    # BASELINE config 0 and config 1 (synthetic generator, seed pinned)
+    codes, scales, x = synth_linear(0xC0, 1, 2048, 4096)
+    fx["cfg0_y"] = ref_gemm(ref_dequant(codes, scales), x)
+    man["config0"] = {"seed": 0xC0, "M": 1, "N": 2048, "K": 4096,
+                      "inputs_sha": digest(codes, scales, x)}
+    codes, scales, x = synth_linear(0xC1, 4, 16384, 4096)
+    wb = ref_dequant(codes, scales)
+    fx["cfg1_y"] = ref_gemm(wb, x)             # rows are M-independent
+    man["config1"] = {"seed": 0xC1, "M": 4, "N": 16384, "K": 4096,
+                      "inputs_sha": digest(codes, scales, x)}
+    # one token over the 288-expert synthetic bank (bank 0)
+    seed, E, k, dim, inter = 0xC2, 288, 8, 4096, 2048
+    logits = np.empty(E, np.float32)
+    SYN.apus_synth_f32_normal(P(logits), E, seed, 20, 0)
+    x = np.empty(dim, np.uint16)
+    SYN.apus_synth_bf16_normal(P(x), dim, seed, 21, 0)
+    idx = np.empty(k, np.int32)
+    R.ref_topk_stable(P(logits), E, k, P(idx))
+    y = np.zeros(dim, np.float32)
+    order = np.argsort(idx, kind="stable")
+    # harness routing (softmax over the k selected logits; not a reference
+    # function): weights from the oracle, the rest from reference kernels
+    w_or = O.route_softmax(logits, k)[1]
+    eo_all = {}
+    for j in order:
+        mats = synth_slab(seed, 0, int(idx[j]), dim, inter)
+        pl = [ref_dequant(c, s) for c, s in mats]
+        eo = ref_expert(pl[0], pl[1], pl[2], x)
+        eo_all[int(idx[j])] = eo
+        contrib = bf16_round(O.bf16_to_f32(eo) * w_or[j])
+        y = bf16_round(y + contrib)
+    fx["cfg2_out"] = O.f32_to_bf16(y)
+    fx["cfg2_expert_out"] = np.stack([eo_all[int(e)] for e in idx])
+    man["config2"] = {"seed": seed, "E": E, "topk": k, "dim": dim,
+                      "inter": inter, "idx": [int(v) for v in idx],
+                      "inputs_sha": digest(logits, x)}
+    np.savez_compressed(os.path.join(HERE, "fixtures.npz"), **fx)
+    with open(os.path.join(HERE, "manifest.json"), "w") as f:
+        json.dump(man, f, indent=1)
+    print("wrote", len(fx), "arrays")
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,177 @@
+"""Pins of the oracle's SwiGLU expert, combine and routing — CPU only.
+
+sigmoid: c/gmhc.h:157-160 (and the reference build). pw_sum: numpy's own
+float32 pairwise sum, which c/gmhc.h:165-185 replicates. top-k: a stable
+argsort (descending value, ties -> lower index), c/gmoe.h:175-189. expert:
+golden fixtures written by the reference's apus_gmoe_expert
+(c/gmoe.h:210-227). combine: order/rounding invariants of c/gmoe.h:307-320
+and the config-2 golden (reference expert outputs, reference loop).
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+GOLD = os.path.join(os.path.dirname(__file__), "golden")
+
+
+@pytest.fixture(scope="module")
+def fx():
+    return np.load(os.path.join(GOLD, "fixtures.npz"))
+
+
+@pytest.fixture(scope="module")
+def man():
+    with open(os.path.join(GOLD, "manifest.json")) as f:
+        return json.load(f)
+
+
+def test_sigmoid_closed_form():
+    L = O.lib()
+    for x in [-30.0, -10.0, -1.5, -1e-3, 0.0, 1e-3, 0.75, 10.0, 30.0]:
+        want = 1.0 / (1.0 + np.exp(-x))
+        assert abs(L.apo_sigmoid_np(x) - want) <= 2e-7 * max(1.0, want)
+    if O.ref_available():
+        R = O.ref()
+        for x in np.linspace(-20, 20, 4001, dtype=np.float32):
+            assert L.apo_sigmoid_np(float(x)) == R.ref_sigmoid(float(x))
+
+
+@pytest.mark.parametrize("n", [1, 2, 7, 8, 9, 16, 31, 128, 129, 300, 1000])
+def test_pw_sum_is_numpy_pairwise(n):
+    a = np.random.default_rng(n).standard_normal(n).astype(np.float32)
+    got = O.lib().apo_pw_sum(O.ptr(a), n)
+    assert np.float32(got) == np.add.reduce(a, dtype=np.float32)
+
+
+def test_topk_stable():
+    rng = np.random.default_rng(5)
+    L = O.lib()
+    for trial in range(50):
+        n = int(rng.integers(8, 300))
+        row = rng.integers(-5, 5, n).astype(np.float32)   # many ties
+        k = int(rng.integers(1, 9))
+        idx = np.empty(k, np.int32)
+        L.apo_topk_stable(O.ptr(row), n, k, O.ptr(idx))
+        want = np.argsort(-row, kind="stable")[:k]
+        assert np.array_equal(idx, want)
+        if O.ref_available():
+            ridx = np.empty(k, np.int32)
+            O.ref().ref_topk_stable(O.ptr(row), n, k, O.ptr(ridx))
+            assert np.array_equal(idx, ridx)
+
+
+def test_route_softmax():
+    rng = np.random.default_rng(9)
+    logits = rng.standard_normal(288).astype(np.float32)
+    idx, w = O.route_softmax(logits, 8)
+    assert np.array_equal(idx, np.argsort(-logits, kind="stable")[:8])
+    sel = logits[idx].astype(np.float64)
+    want = np.exp(sel - sel.max()) / np.exp(sel - sel.max()).sum()
+    assert np.allclose(w, want, rtol=1e-6, atol=0)
+    assert abs(float(w.astype(np.float64).sum()) - 1.0) < 1e-6
+
+
+def test_expert_golden(fx, man):
+    for i, sh in enumerate(man["expert"]):
+        pl = [O.dequant(fx[f"xp{i}_{nm}_codes"], fx[f"xp{i}_{nm}_scales"])
+              for nm in "gud"]
+        out, g, u, h = O.swiglu_expert(pl[0], pl[1], pl[2], fx[f"xp{i}_x"])
+        assert np.array_equal(out, fx[f"xp{i}_out"]), sh
+        out_mt = O.swiglu_expert(pl[0], pl[1], pl[2], fx[f"xp{i}_x"], threads=4)[0]
+        assert np.array_equal(out_mt, out), sh
+        if sh["x_std"] > 4:
+            gf, uf = O.bf16_to_f32(g), O.bf16_to_f32(u)
+            assert (gf > 10).any() and (np.abs(uf) > 10).any(), "clamps must fire"
+
+
+def _bank(dim, inter, E, rng):
+    from test_oracle_dequant_gemm import deq_exact_f64  # noqa: F401
+    slabs = []
+    for e in range(E):
+        parts = []
+        for (o, k) in [(inter, dim), (inter, dim), (dim, inter)]:
+            c = rng.integers(0, 254, (o, k), dtype=np.uint8)
+            c[c >= 0x7F] += 1
+            s = np.exp2(rng.uniform(-9, -5, (O.nblocks(o), O.nblocks(k)))).astype(np.float32)
+            parts += [c.ravel(), s.view(np.uint8).ravel()]
+        slabs.append(np.concatenate(parts))
+    return slabs
+
+
+def _expert_of(slab, dim, inter):
+    n = inter * dim
+    nbs = O.nblocks(inter) * O.nblocks(dim) * 4
+    gw = slab[:n].reshape(inter, dim)
+    gs = slab[n:n + nbs].view(np.float32).reshape(O.nblocks(inter), O.nblocks(dim))
+    uw = slab[n + nbs:2 * n + nbs].reshape(inter, dim)
+    us = slab[2 * n + nbs:2 * n + 2 * nbs].view(np.float32).reshape(gs.shape)
+    dw = slab[2 * n + 2 * nbs:3 * n + 2 * nbs].reshape(dim, inter)
+    ds = slab[3 * n + 2 * nbs:].view(np.float32).reshape(O.nblocks(dim), O.nblocks(inter))
+    return O.dequant(gw, gs), O.dequant(uw, us), O.dequant(dw, ds)
+
+
+def test_moe_combine_semantics():
+    """Combine = ascending expert id, contrib = bf16(out_e * w), y = bf16(y +
+    contrib): checked by recomputing from per-expert outputs, slot-order
+    invariance, and k = 1 reducing to bf16(out * w)."""
+    dim, inter, E, k = 128, 64, 12, 6
+    rng = np.random.default_rng(21)
+    slabs = _bank(dim, inter, E, rng)
+    T = 5
+    x = O.f32_to_bf16(rng.standard_normal((T, dim)).astype(np.float32) * 3)
+    idx = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int32)
+    w = rng.uniform(0.05, 0.6, (T, k)).astype(np.float32)
+    out, eo = O.moe_forward(slabs, dim, inter, x, idx, w, want_expert_out=True)
+    for t in range(T):
+        y = np.zeros(dim, np.float32)
+        for j in np.argsort(idx[t]):
+            pg, pu, pd = _expert_of(slabs[idx[t, j]], dim, inter)
+            assert np.array_equal(O.swiglu_expert(pg, pu, pd, x[t])[0], eo[t, j])
+            c = O.bf16_to_f32(O.f32_to_bf16(O.bf16_to_f32(eo[t, j]) * w[t, j]))
+            y = O.bf16_to_f32(O.f32_to_bf16(y + c))
+        assert np.array_equal(O.f32_to_bf16(y), out[t])
+    perm = rng.permutation(k)
+    out2 = O.moe_forward(slabs, dim, inter, x, idx[:, perm].copy(),
+                         w[:, perm].copy())
+    assert np.array_equal(out, out2)
+    out1, eo1 = O.moe_forward(slabs, dim, inter, x, idx[:, :1].copy(),
+                              w[:, :1].copy(), want_expert_out=True)
+    assert np.array_equal(out1, O.f32_to_bf16(O.bf16_to_f32(eo1[:, 0]) * w[:, :1]))
+
+
+def test_moe_planted_order_mistake_is_detected():
+    """Descending-order combine differs from ascending on some token: the
+    order pin bites (bf16 rounding per add is not associative)."""
+    dim, inter, E, k = 128, 64, 10, 8
+    rng = np.random.default_rng(4)
+    slabs = _bank(dim, inter, E, rng)
+    x = O.f32_to_bf16(rng.standard_normal((4, dim)).astype(np.float32) * 4)
+    idx = np.stack([rng.permutation(E)[:k] for _ in range(4)]).astype(np.int32)
+    w = rng.uniform(0.05, 0.6, (4, k)).astype(np.float32)
+    out, eo = O.moe_forward(slabs, dim, inter, x, idx, w, want_expert_out=True)
+    differs = False
+    for t in range(4):
+        y = np.zeros(dim, np.float32)
+        for j in np.argsort(idx[t])[::-1]:
+            c = O.bf16_to_f32(O.f32_to_bf16(O.bf16_to_f32(eo[t, j]) * w[t, j]))
+            y = O.bf16_to_f32(O.f32_to_bf16(y + c))
+        differs |= not np.array_equal(O.f32_to_bf16(y), out[t])
+    assert differs
+
+
+@pytest.mark.skipif(not O.ref_available(), reason="reference build absent")
+def test_expert_vs_reference_build_real_shape():
+    R = O.ref()
+    rng = np.random.default_rng(17)
+    dim, inter = 4096, 2048
+    pl = [O.f32_to_bf16((rng.standard_normal((o, k)) * 0.02).astype(np.float32))
+          for (o, k) in [(inter, dim), (inter, dim), (dim, inter)]]
+    x = O.f32_to_bf16(rng.standard_normal(dim).astype(np.float32))
+    out_ref = np.empty(dim, np.uint16)
+    assert R.ref_gmoe_expert(O.ptr(pl[0]), O.ptr(pl[1]), O.ptr(pl[2]), O.ptr(x),
+                             dim, inter, 10.0, O.ptr(out_ref)) == 0
+    assert np.array_equal(O.swiglu_expert(*pl, x, threads=8)[0], out_ref)

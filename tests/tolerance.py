@@ -1,0 +1,55 @@
+"""The GEMM/MoE output tolerance of the contract:
+<= 1 bf16 ulp on >= 99.9% of elements and max relative error <= 1e-2.
+
+ulp distance: |ord(a) - ord(b)| with ord the monotone integer image of the
+bf16 code (sign-magnitude folded to two's complement; +0 == -0).
+relative error: |a - b| / max(|b|, floor). The floor makes the bound
+meaningful where the exact result cancels to ~0:
+  GEMV/GEMM output   floor = 2^-8 * sum_k |w_k * x_k|  (f64, oracle)
+  MoE combine output floor = sum_e |contrib_e|         (the combined terms)
+An fp32 reordering moves a sum by ~sqrt(K)*2^-24*sum|terms|, far below the
+floor; a wrong term or index moves it by O(|term|), far above 1e-2.
+"""
+import numpy as np
+
+ULP_FRAC_MIN = 0.999
+REL_MAX = 1e-2
+
+
+def bf16_ord(b):
+    b = np.asarray(b, np.uint16).astype(np.int32)
+    mag = b & 0x7FFF
+    return np.where(b & 0x8000, -mag, mag)
+
+
+def bf16_f32(b):
+    return (np.asarray(b, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def compare(got, ref, floor):
+    got = np.asarray(got, np.uint16).ravel()
+    ref = np.asarray(ref, np.uint16).ravel()
+    floor = np.asarray(floor, np.float64)
+    floor = (np.full(ref.shape, float(floor)) if floor.size == 1
+             else floor.ravel())
+    assert floor.shape == ref.shape, "floor must match the output size"
+    ulp = np.abs(bf16_ord(got) - bf16_ord(ref))
+    g = bf16_f32(got).astype(np.float64)
+    r = bf16_f32(ref).astype(np.float64)
+    den = np.maximum(np.abs(r), floor)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        rel = np.where(den > 0, np.abs(g - r) / den, np.where(g == r, 0.0, np.inf))
+    return {
+        "n": int(ref.size),
+        "frac_le1ulp": float(np.mean(ulp <= 1)) if ref.size else 1.0,
+        "max_ulp": int(ulp.max()) if ref.size else 0,
+        "max_rel": float(rel.max()) if ref.size else 0.0,
+        "n_exact": int(np.sum(ulp == 0)),
+    }
+
+
+def assert_close(got, ref, floor, what=""):
+    st = compare(got, ref, floor)
+    assert st["frac_le1ulp"] >= ULP_FRAC_MIN and st["max_rel"] <= REL_MAX, \
+        "%s: %s" % (what, st)
+    return st
