@@ -529,12 +529,11 @@ int apus_ghip_store_open(ApusGhipStore **out, int n_experts, size_t dim,
     }
     int bad = hipMalloc((void **)&s->nan_flags, (size_t)n_experts * 4) != hipSuccess
            || hipMemset(s->nan_flags, 0, (size_t)n_experts * 4) != hipSuccess
-           || hipMalloc((void **)&s->ws.counters, GHIP_MOE_DEC_COUNTERS * 4) != hipSuccess
-           || hipMemset(s->ws.counters, 0, GHIP_MOE_DEC_COUNTERS * 4) != hipSuccess
+           || hipMalloc((void **)&s->ws.route, GHIP_MOE_ROUTE_WORDS * 4) != hipSuccess
+           || hipMemset(s->ws.route, 0, GHIP_MOE_ROUTE_WORDS * 4) != hipSuccess
            || hipMalloc((void **)&s->ws.err, 4) != hipSuccess
            || hipMemset(s->ws.err, 0, 4) != hipSuccess
            || hipMalloc((void **)&s->ws.h, GHIP_MAX_TOPK * inter * 2) != hipSuccess
-           || hipMalloc((void **)&s->ws.contrib, GHIP_MAX_TOPK * dim * 2) != hipSuccess
            || hipMalloc((void **)&s->d_x, dim * 2) != hipSuccess
            || hipMalloc((void **)&s->d_out, dim * 2) != hipSuccess
            || hipMalloc((void **)&s->d_idx, GHIP_MAX_TOPK * 4) != hipSuccess
@@ -554,10 +553,9 @@ void apus_ghip_store_close(ApusGhipStore *s) {
     hipDeviceSynchronize();
     hipFree(s->arena);
     hipFree(s->nan_flags);
-    hipFree(s->ws.counters);
+    hipFree(s->ws.route);
     hipFree(s->ws.err);
     hipFree(s->ws.h);
-    hipFree(s->ws.contrib);
     hipFree(s->d_x);
     hipFree(s->d_out);
     hipFree(s->d_idx);
@@ -768,7 +766,7 @@ int apus_ghip_moe_decode(ApusGhipStore *s, const uint16_t *x,
     uint32_t err = 0;
     HIPCHK(hipMemcpy(&err, s->ws.err, 4, hipMemcpyDeviceToHost));
     if (err) {
-        ghip_seterr("moe_decode: device wait bound expired (code %u)", err);
+        ghip_seterr("moe_decode: invalid expert id in routing (code %u)", err);
         hipMemset(s->ws.err, 0, 4);
         return 1;
     }

@@ -103,6 +103,138 @@ __device__ __forceinline__ void ghip_deq16(ghip_u32x4 c, float s,
     b1 = __builtin_bit_cast(ghip_bf16x8, hi);
 }
 
+/* ---- 16-row GEMV chunk (the streaming unit of every GEMV kernel) --------
+ * A wave owns 16 output rows; a chunk is one 128-wide k block of each row
+ * (one F32 scale). Lane l = 16*g + n holds row n, codes [32g, 32g+32) of
+ * the chunk: two 16-byte loads, so one wave covers 16 full 128-byte lines.
+ * The 32 codes dequantize to four bf16x8 MFMA B operands; MFMA i uses codes
+ * [8i, 8i+8) of every lane group, i.e. k-slot (g, j) <-> k = 32g + 8i + j,
+ * and the A operand (activation, from LDS) is read with the same mapping,
+ * so each v_mfma_f32_16x16x32_bf16 sums a permutation of 32 exact
+ * products. */
+struct ghip_chunk {
+    ghip_u32x4 lo, hi;
+};
+
+__device__ __forceinline__ ghip_chunk ghip_chunk_load(const uint8_t *p) {
+    ghip_chunk c;
+    c.lo = __builtin_nontemporal_load((const ghip_u32x4 *)p);
+    c.hi = __builtin_nontemporal_load((const ghip_u32x4 *)(p + 16));
+    return c;
+}
+
+/* acc += A(xa[0..32)) . B(dequant(chunk)); xa points at this lane's 32
+ * activations of the chunk (row m of x, k = 128c + 32g). */
+template <bool EXACT>
+__device__ __forceinline__ void ghip_chunk_mfma(const ghip_chunk &c, float sc,
+                                                const uint16_t *xa,
+                                                ghip_f32x4 &acc) {
+    ghip_bf16x8 b0, b1, b2, b3;
+    ghip_deq16<EXACT>(c.lo, sc, b0, b1);
+    ghip_deq16<EXACT>(c.hi, sc, b2, b3);
+    const ghip_bf16x8 *a = (const ghip_bf16x8 *)xa;
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b0, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1], b1, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[2], b2, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[3], b3, acc, 0, 0, 0);
+}
+
+/* ---- activation staging without serializing the weight stream ----------
+ * vmcnt retires loads in issue order, so an activation load issued AFTER
+ * the weight loads makes its LDS write wait for every weight byte. Stage in
+ * two steps instead: ghip_stage_load (before the weight loads) pulls up to
+ * GHIP_STAGE_V 16-byte vectors per thread into registers; ghip_stage_store
+ * (after them) writes them to LDS, waiting only for the activation loads.
+ * Any remainder (larger activations) is copied directly. nvec >= 1. */
+#define GHIP_STAGE_V 4
+
+struct ghip_stage {
+    ghip_u32x4 v[GHIP_STAGE_V];
+};
+
+__device__ __forceinline__ void ghip_stage_load(ghip_stage &st, const uint16_t *src,
+                                                uint32_t nvec, uint32_t tid,
+                                                uint32_t nthr) {
+    /* unconditional loads (index clamped, extra values unused): straight-line
+     * code lets the compiler wait for these with vmcnt(#weight loads) */
+#pragma unroll
+    for (int j = 0; j < GHIP_STAGE_V; j++) {
+        uint32_t i = min(tid + j * nthr, nvec - 1u);
+        st.v[j] = *(const ghip_u32x4 *)(src + ((size_t)i << 3));
+    }
+}
+
+__device__ __forceinline__ void ghip_stage_store(const ghip_stage &st, uint16_t *dst,
+                                                 const uint16_t *src, uint32_t nvec,
+                                                 uint32_t tid, uint32_t nthr) {
+    /* unconditional too (a clamped index rewrites element nvec-1 with its
+     * own value): a conditional store lets the compiler sink the load into
+     * the branch, behind the weight loads */
+#pragma unroll
+    for (int j = 0; j < GHIP_STAGE_V; j++) {
+        uint32_t i = min(tid + j * nthr, nvec - 1u);
+        *(ghip_u32x4 *)(dst + ((size_t)i << 3)) = st.v[j];
+    }
+    for (uint32_t i = tid + GHIP_STAGE_V * nthr; i < nvec; i += nthr)
+        *(ghip_u32x4 *)(dst + ((size_t)i << 3)) = *(const ghip_u32x4 *)(src + ((size_t)i << 3));
+}
+
+/* ---- wave-local activation staging -------------------------------------
+ * A wave that owns chunks c = w, w + step, ... of a row stages only those
+ * 128-wide slices of the activation rows (M rows, row stride K elements)
+ * into LDS (same [M][K] layout), and only its own lanes read them back: no
+ * workgroup barrier, and 1/step of the activation traffic per wave. Vector
+ * v (16 bytes) of the wave's list = (chunk u, row m, part p) with
+ * v = (u*M + m)*16 + p. Up to GHIP_STAGE_V vectors per lane go through
+ * registers (loaded before the weights, see ghip_stage_load); the rest is
+ * copied directly. */
+__device__ __forceinline__ size_t ghip_wst_off(uint32_t v, uint32_t M, uint32_t K,
+                                               uint32_t w, uint32_t step) {
+    const uint32_t p = v & 15u, um = v >> 4, u = um / M, m = um - u * M;
+    return (size_t)m * K + (size_t)(w + u * step) * 128u + p * 8u;
+}
+
+__device__ __forceinline__ void ghip_wstage_load(ghip_stage &st, const uint16_t *src,
+                                                 uint32_t M, uint32_t K, uint32_t nch,
+                                                 uint32_t w, uint32_t step,
+                                                 uint32_t lane) {
+    const uint32_t nwch = w < nch ? (nch - w + step - 1) / step : 0u;
+    const uint32_t nv = nwch * M * 16u;
+#pragma unroll
+    for (int j = 0; j < GHIP_STAGE_V; j++) {
+        uint32_t v = min(lane + 64u * j, nv ? nv - 1u : 0u);
+        st.v[j] = *(const ghip_u32x4 *)(src + ghip_wst_off(v, M, K, w, step));
+    }
+}
+
+__device__ __forceinline__ void ghip_wstage_store(const ghip_stage &st, uint16_t *dst,
+                                                  const uint16_t *src, uint32_t M,
+                                                  uint32_t K, uint32_t nch, uint32_t w,
+                                                  uint32_t step, uint32_t lane) {
+    const uint32_t nwch = w < nch ? (nch - w + step - 1) / step : 0u;
+    const uint32_t nv = nwch * M * 16u;
+#pragma unroll
+    for (int j = 0; j < GHIP_STAGE_V; j++) {
+        uint32_t v = min(lane + 64u * j, nv ? nv - 1u : 0u);
+        *(ghip_u32x4 *)(dst + ghip_wst_off(v, M, K, w, step)) = st.v[j];
+    }
+    for (uint32_t v = lane + 64u * GHIP_STAGE_V; v < nv; v += 64u)
+        *(ghip_u32x4 *)(dst + ghip_wst_off(v, M, K, w, step)) =
+            *(const ghip_u32x4 *)(src + ghip_wst_off(v, M, K, w, step));
+    /* the wave's own LDS writes complete before its lanes read them */
+    __builtin_amdgcn_s_waitcnt(0xc07f);           /* lgkmcnt(0) */
+    __builtin_amdgcn_wave_barrier();
+}
+
+/* Direct wave-local copy of nvec 16-byte vectors (no register staging). */
+__device__ __forceinline__ void ghip_wcopy(uint16_t *dst, const uint16_t *src,
+                                           uint32_t nvec, uint32_t lane) {
+    for (uint32_t v = lane; v < nvec; v += 64u)
+        *(ghip_u32x4 *)(dst + ((size_t)v << 3)) = *(const ghip_u32x4 *)(src + ((size_t)v << 3));
+    __builtin_amdgcn_s_waitcnt(0xc07f);           /* lgkmcnt(0) */
+    __builtin_amdgcn_wave_barrier();
+}
+
 /* numpy-stable sigmoid (c/gmhc.h:157-160) with the device expf. */
 __device__ __forceinline__ float ghip_sigmoid_np(float x) {
     float e = expf(-fabsf(x));

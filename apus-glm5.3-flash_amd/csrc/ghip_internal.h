@@ -40,16 +40,15 @@ hipError_t ghip_launch_bf16_linear(const uint16_t *w, const uint16_t *x,
                                    uint16_t *y, size_t M, size_t O, size_t K,
                                    hipStream_t st);
 
-/* K3 MoE decode state: counters that the kernel leaves at zero on exit
- * (allocated zeroed once, never cleared with a memset in the hot path). */
+/* K3 MoE decode workspace (device): the routing handoff between the
+ * launches, the SwiGLU activations, and an error word. */
 typedef struct {
-    uint32_t *counters;   /* device, GHIP_MOE_DEC_COUNTERS u32 */
-    uint16_t *h;          /* device [topk, inter] bf16 */
-    uint16_t *contrib;    /* device [topk, dim] bf16 */
-    uint32_t *err;        /* device u32: nonzero after a bounded wait expired */
+    uint32_t *route;      /* device, GHIP_MOE_ROUTE_WORDS u32 */
+    uint16_t *h;          /* device [max topk, inter] bf16 */
+    uint32_t *err;        /* device u32: nonzero after an invalid expert id */
 } GhipMoeDecodeWs;
 
-#define GHIP_MOE_DEC_COUNTERS 4096
+#define GHIP_MOE_ROUTE_WORDS 64
 
 /* Expert bank view for the kernels: slab s of expert e at base + e*stride;
  * member byte offsets inside a slab (c/gcache.h:852-861 order). */
@@ -61,9 +60,10 @@ typedef struct {
     const uint32_t *nan_flags;   /* device [n_experts] u32 or NULL */
 } GhipBank;
 
-/* K3: routed MoE decode for one token, one launch. Either logits (device
- * f32 [n_experts], the kernel computes top-k + softmax) or idx/w (device
- * [topk]) must be given. out: device [dim] bf16. */
+/* K3: routed MoE decode for one token (routing, gate/up + SwiGLU, down +
+ * ordered combine: three launches on st). Either logits (device f32
+ * [n_experts]; top-k + softmax on the device) or idx/w (device [topk]) must
+ * be given. out: device [dim] bf16. */
 hipError_t ghip_launch_moe_decode(const GhipBank *bank, const uint16_t *x,
                                   const float *logits, const int32_t *idx,
                                   const float *w, int topk, float limit,

@@ -12,11 +12,11 @@
  *       can select the exact decode for such weights.
  *
  * GEMV tiling (K2). A workgroup owns 16 consecutive output rows; its NW
- * waves split K into 64-wide chunks (wave w takes chunks w, w+NW, ...). Per
- * chunk, lane l loads 16 codes of row (l % 16) at k offset 16*(l / 16)
- * (one 16-byte load; a wave load covers 16 rows x 64 contiguous bytes),
- * dequantizes them to two bf16x8 operands and issues two MFMAs whose A
- * operand is x staged in LDS. The MFMA k-slot
+ * waves split K into 128-wide chunks (one scale block; wave w takes chunks
+ * w, w+NW, ...). Per chunk, lane l loads 32 codes of row (l % 16) at k
+ * offset 32*(l / 16) (two 16-byte loads; a wave covers 16 full 128-byte
+ * lines), dequantizes them to four bf16x8 operands and issues four MFMAs
+ * whose A operand is x staged in LDS. The MFMA k-slot
  * to k mapping is any permutation used identically for A and B, so the
  * result is an exact-product fp32 sum in a different order than the
  * reference's sequential k: a tolerance-class result, per the contract.
@@ -27,7 +27,7 @@
 #include "ghip_internal.h"
 
 #define GEMV_NW 8          /* waves per workgroup (k split) */
-#define GEMV_U 8           /* 16-byte loads in flight per lane per batch */
+#define GEMV_U 4           /* 128-wide chunks (2 loads each) per batch */
 
 /* ------------------------------------------------------------------------ */
 /* K1: dequant                                                              */
@@ -86,41 +86,53 @@ __global__ __launch_bounds__(256) void k_nan_scan(
 }
 
 /* ------------------------------------------------------------------------ */
-/* K2: FP8 GEMV, M <= 4, K % 64 == 0                                        */
+/* K2: FP8 GEMV, M <= 4, K % 128 == 0                                       */
 /* ------------------------------------------------------------------------ */
 
-template <int M, bool EXACT>
+/* One batch of a wave's chunk loads: chunks c0, c0 + NW, ... (GEMV_U of
+ * them). The first batch is issued before x is staged so the two latencies
+ * overlap. */
+__device__ __forceinline__ void gemv16_fetch(const uint8_t *__restrict__ wr,
+                                             uint32_t nch, uint32_t c0,
+                                             ghip_chunk *buf) {
+    /* unconditional (chunk clamped; the compute loop skips c >= nch) so the
+     * waitcnt pass sees a fixed number of loads */
+#pragma unroll
+    for (int u = 0; u < GEMV_U; u++) {
+        uint32_t c = min(c0 + u * GEMV_NW, nch - 1u);
+        buf[u] = ghip_chunk_load(wr + (size_t)c * 128);
+    }
+}
+
+/* buf holds the first batch on entry and is refilled in place. */
+/* sc holds the first batch's scales (fetched with the weights). */
+template <bool EXACT>
 __device__ __forceinline__ ghip_f32x4 gemv16_rows(
     const uint8_t *__restrict__ wr, const float *__restrict__ srow,
-    const uint16_t *xa, uint32_t nch, uint32_t wv) {
+    const uint16_t *xa, uint32_t nch, uint32_t wv, ghip_chunk (&buf)[GEMV_U],
+    const float (&sc)[GEMV_U]) {
     ghip_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     for (uint32_t c0 = wv; c0 < nch; c0 += GEMV_NW * GEMV_U) {
-        ghip_u32x4 buf[GEMV_U];
+        float s2[GEMV_U];
+        if (c0 != wv) {
+            gemv16_fetch(wr, nch, c0, buf);
 #pragma unroll
-        for (int u = 0; u < GEMV_U; u++) {
-            uint32_t c = c0 + u * GEMV_NW;
-            if (c < nch) buf[u] = __builtin_nontemporal_load(
-                (const ghip_u32x4 *)(wr + (size_t)c * 64));
+            for (int u = 0; u < GEMV_U; u++) s2[u] = srow[min(c0 + u * GEMV_NW, nch - 1u)];
+        } else {
+#pragma unroll
+            for (int u = 0; u < GEMV_U; u++) s2[u] = sc[u];
         }
 #pragma unroll
         for (int u = 0; u < GEMV_U; u++) {
             uint32_t c = c0 + u * GEMV_NW;
-            if (c < nch) {
-                float sc = srow[c >> 1];
-                ghip_bf16x8 b0, b1;
-                ghip_deq16<EXACT>(buf[u], sc, b0, b1);
-                ghip_bf16x8 a0 = *(const ghip_bf16x8 *)(xa + c * 64);
-                ghip_bf16x8 a1 = *(const ghip_bf16x8 *)(xa + c * 64 + 8);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1, acc, 0, 0, 0);
-            }
+            if (c < nch) ghip_chunk_mfma<EXACT>(buf[u], s2[u], xa + c * 128, acc);
         }
     }
     return acc;
 }
 
 template <int M>
-__global__ __launch_bounds__(GEMV_NW * 64) void k_fp8_gemv(
+__global__ __launch_bounds__(GEMV_NW * 64, 4) void k_fp8_gemv(
     const uint8_t *__restrict__ W, const float *__restrict__ S,
     const uint16_t *__restrict__ X, uint16_t *__restrict__ Y, uint32_t O,
     uint32_t K, uint32_t nkb, const uint32_t *__restrict__ exact_flag) {
@@ -128,24 +140,28 @@ __global__ __launch_bounds__(GEMV_NW * 64) void k_fp8_gemv(
     __shared__ float red[GEMV_NW][M][16];
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    /* stage x rows 0..M-1 (16-byte vectors) */
-    const uint32_t nvec = (M * K) >> 3;
-    for (uint32_t i = tid; i < nvec; i += GEMV_NW * 64)
-        *(ghip_u32x4 *)(xs + ((size_t)i << 3)) =
-            *(const ghip_u32x4 *)(X + ((size_t)i << 3));
-    __syncthreads();
-    const bool exact = exact_flag != nullptr && *exact_flag != 0u;
     const uint32_t row0 = blockIdx.x * 16u;
     const uint32_t n = lane & 15u, g = lane >> 4;
     const uint32_t row = min(row0 + n, O - 1u);
-    const uint8_t *wr = W + (size_t)row * K + 16u * g;
+    const uint8_t *wr = W + (size_t)row * K + 32u * g;
+    const uint32_t nch = K >> 7;
+    /* this wave's x slices first, then the weights, then the slices into
+     * LDS (ghip_wstage_*: no workgroup barrier) */
+    ghip_stage stx;
+    ghip_wstage_load(stx, X, M, K, nch, wv, GEMV_NW, lane);
+    ghip_chunk pre[GEMV_U];
+    gemv16_fetch(wr, nch, wv, pre);
     const float *srow = S + (size_t)(row0 >> 7) * nkb;
+    float sc[GEMV_U];
+#pragma unroll
+    for (int u = 0; u < GEMV_U; u++) sc[u] = srow[min(wv + u * GEMV_NW, nch - 1u)];
+    const bool exact = exact_flag != nullptr && *exact_flag != 0u;
+    ghip_wstage_store(stx, xs, X, M, K, nch, wv, GEMV_NW, lane);
     /* MFMA A row i = lane % 16 is token m; rows m >= M only feed output
      * rows that are discarded, so they read row M-1 instead of zeros. */
-    const uint16_t *xa = xs + (size_t)min(n, (uint32_t)M - 1u) * K + 16u * g;
-    const uint32_t nch = K >> 6;
-    ghip_f32x4 acc = exact ? gemv16_rows<M, true>(wr, srow, xa, nch, wv)
-                           : gemv16_rows<M, false>(wr, srow, xa, nch, wv);
+    const uint16_t *xa = xs + (size_t)min(n, (uint32_t)M - 1u) * K + 32u * g;
+    ghip_f32x4 acc = exact ? gemv16_rows<true>(wr, srow, xa, nch, wv, pre, sc)
+                           : gemv16_rows<false>(wr, srow, xa, nch, wv, pre, sc);
     if (g == 0) {
 #pragma unroll
         for (int i = 0; i < M; i++) red[wv][i][n] = acc[i];
@@ -276,7 +292,7 @@ extern "C" hipError_t ghip_launch_fp8_linear(const uint8_t *codes,
     if (M == 0 || O == 0) return hipSuccess;
     if (K == 0 || O > 0x7fffffffu || K > 0x7fffffffu || M > 0x7fffffffu)
         return hipErrorInvalidValue;
-    bool fast = (K % 64 == 0) && (((uintptr_t)codes & 15) == 0)
+    bool fast = (K % 128 == 0) && (((uintptr_t)codes & 15) == 0)
              && (((uintptr_t)x & 15) == 0) && K * 2 <= GEMV_LDS_MAX;
     if (!fast) {
         uint32_t nkb = (uint32_t)((K + 127) / 128);

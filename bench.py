@@ -1,0 +1,367 @@
+#!/usr/bin/env python3
+"""bench.py — MI355X throughput of the apus FP8-block MoE hot path.
+
+Default workload = BASELINE.json config 2, the metric's "FP8 MoE decode GEMV":
+one routed-MoE decode step per launch (288-expert FP8 bank resident in HBM,
+one token, device top-8 of f32 logits + softmax, SwiGLU experts, ordered
+bf16 combine). Inputs rotate over R tokens/routings so every step streams
+8 experts' weights from HBM. value = algorithmic bytes per step (8 expert
+slabs + x + out + logits = 201,393,280 B) / measured time, in GB/s.
+
+--workload dense_gemv runs config 1 (W [16384,4096] FP8, M in {1,2,4}) over
+rotating weight copies (>= 3x the 256 MB MALL).
+
+Prints ONE JSON line (rank 0). Extra objects: "roofline" (dominant kernel,
+HIP-event timed on its stream) and "cpu_baseline" (the reference CPU path,
+compiled from the reference sources into oracle/_ref, timed on this host on
+a bounded sample; the C restatement in oracle/ when that is absent).
+"""
+import argparse
+import ctypes
+import importlib.util
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "apus-glm5.3-flash_amd")
+HBM_PEAK_GBS = 8000.0            # MI355X HBM3E, AMD published
+BF16_PEAK_TFLOPS = 2500.0        # MI355X dense BF16 MFMA, AMD published
+CPU_THREADS = 16                 # the GPU box's CPU share per GPU
+
+
+def load_pkg():
+    spec = importlib.util.spec_from_file_location(
+        "apus_ghip", os.path.join(PKG, "__init__.py"),
+        submodule_search_locations=[PKG])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["apus_ghip"] = mod
+    spec.loader.exec_module(mod)
+    import apus_ghip.hiprt as rt  # noqa: E402
+    return mod, rt
+
+
+def traffic_from_profiles(kernel):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE +
+    WRITE_SIZE, scaled by the copy-kernel calibration) and committed under
+    profiles/; None when no measurement exists for this kernel."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        d = json.load(f)
+    v = d.get(kernel)
+    return v.get("hbm_bytes_per_launch") if isinstance(v, dict) else None
+
+
+# --------------------------------------------------------------------------
+# config 2: MoE decode
+# --------------------------------------------------------------------------
+
+MOE = dict(E=288, k=8, dim=4096, inter=2048, seed=0xC2, limit=10.0)
+
+
+def moe_algorithmic_bytes(E, k, dim, inter):
+    nb = lambda n: (n + 127) // 128  # noqa: E731
+    slab = 2 * (inter * dim + nb(inter) * nb(dim) * 4) + dim * inter \
+        + nb(dim) * nb(inter) * 4
+    return k * slab + dim * 2 + dim * 2 + E * 4, 2 * k * 3 * inter * dim
+
+
+def bench_moe_decode(lib, pkg, rt, steps, warmup, rotate=64):
+    E, k, dim, inter, seed = (MOE[x] for x in ("E", "k", "dim", "inter", "seed"))
+    store = ctypes.c_void_p()
+    err = ctypes.create_string_buffer(256)
+    pkg.check(lib.apus_ghip_store_open(ctypes.byref(store), E, dim, inter,
+                                       MOE["limit"], err, 256), "store_open")
+    pkg.check(lib.apus_ghip_store_synth(store, seed, 0, 1e-4, 1e-2), "store_synth")
+    logits = np.empty((rotate, E), np.float32)
+    lib.apus_synth_f32_normal(logits.ctypes.data_as(ctypes.c_void_p), logits.size,
+                              seed, 30, 0)
+    xs = np.empty((rotate, dim), np.uint16)
+    lib.apus_synth_bf16_normal(xs.ctypes.data_as(ctypes.c_void_p), xs.size, seed,
+                               31, 0)
+    d_log = rt.DevBuf.of(logits)
+    d_x = rt.DevBuf.of(xs)
+    d_out = rt.DevBuf(rotate * dim * 2)
+    st = rt.Stream()
+
+    def step(i):
+        j = i % rotate
+        rc = lib.apus_ghip_moe_decode_dev(
+            store, ctypes.c_void_p(d_x.ptr + j * dim * 2),
+            ctypes.c_void_p(d_log.ptr + j * E * 4), None, None, k,
+            ctypes.c_void_p(d_out.ptr + j * dim * 2), st.vp)
+        if rc:
+            pkg.check(rc, "moe_decode_dev")
+
+    for i in range(warmup):
+        step(i)
+    st.synchronize()
+    rt.synchronize()
+    e0, e1 = rt.Event(), rt.Event()
+    t0 = time.perf_counter()
+    e0.record(st)
+    for i in range(steps):
+        step(warmup + i)
+    e1.record(st)
+    e1.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_ms(e1) / steps
+    nbytes, flops = moe_algorithmic_bytes(E, k, dim, inter)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    lib.apus_ghip_store_close(store)
+    return {
+        "ms_per_step": ms, "value": gbs, "wall_s": wall,
+        "bytes": nbytes, "flops": flops, "kernel": "k_moe_decode",
+        "config": {"workload": "moe_decode (BASELINE config 2)", "experts": E,
+                   "topk": k, "dim": dim, "inter": inter, "tokens": 1,
+                   "rotated_tokens": rotate, "weights": "fp8-e4m3 128x128 blocks",
+                   "routing": "device top-8 of f32 logits, softmax"},
+    }
+
+
+def cpu_moe_decode(lib, budget_s=12.0):
+    """Reference CPU path for config 2 on this host: per token, the 8
+    routed experts (c/gmoe.h:210-227 on BF16 payloads, dequantized on fill as
+    c/gcache.h:413-426) and the ordered combine (c/gmoe.h:307-320). The
+    dequant-on-fill is timed separately. Bounded sample: tokens until the
+    budget is spent."""
+    os.environ.setdefault("APUS_THREADS", str(CPU_THREADS))
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    E, k, dim, inter, seed = (MOE[x] for x in ("E", "k", "dim", "inter", "seed"))
+    use_ref = O.ref_available()
+    P = O.ptr
+    logits = np.empty(E, np.float32)
+    lib.apus_synth_f32_normal(P(logits), E, seed, 30, 0)
+    idx, w = O.route_softmax(logits, k)
+    payloads, t_deq = [], 0.0
+    for e in sorted(int(v) for v in idx):
+        mats = []
+        for j, (o, kk) in enumerate([(inter, dim), (inter, dim), (dim, inter)]):
+            c = np.empty((o, kk), np.uint8)
+            lib.apus_synth_fp8_codes(P(c), c.size, seed,
+                                     lib.apus_synth_expert_stream(0, e, 2 * j), 0)
+            s = np.empty((O.nblocks(o), O.nblocks(kk)), np.float32)
+            lib.apus_synth_scales(P(s), s.size, seed,
+                                  lib.apus_synth_expert_stream(0, e, 2 * j + 1),
+                                  1e-4, 1e-2)
+            out = np.empty((o, kk), np.uint16)
+            t0 = time.perf_counter()
+            if use_ref:
+                O.ref().ref_fp8blk_dequant_mt(P(c), P(s), P(out), o, kk)
+            else:
+                O.lib().apo_fp8blk_dequant_mt(P(c), P(s), P(out), o, kk, CPU_THREADS)
+            t_deq += time.perf_counter() - t0
+            mats.append(out)
+        payloads.append((e, mats))
+    wsorted = {int(i): float(v) for i, v in zip(idx, w)}
+    x = np.empty(dim, np.uint16)
+    ntok, t_tok = 0, 0.0
+    eo = np.empty(dim, np.uint16)
+    while t_tok < budget_s and ntok < 4000:
+        lib.apus_synth_bf16_normal(P(x), dim, seed, 31, ntok * dim)
+        t0 = time.perf_counter()
+        y = np.zeros(dim, np.float32)
+        for e, (g, u, d) in payloads:
+            if use_ref:
+                O.ref().ref_gmoe_expert(P(g), P(u), P(d), P(x), dim, inter,
+                                        MOE["limit"], P(eo))
+            else:
+                eo[:] = O.swiglu_expert(g, u, d, x, threads=CPU_THREADS)[0]
+            c = O.bf16_to_f32(O.f32_to_bf16(O.bf16_to_f32(eo) * np.float32(wsorted[e])))
+            y = O.bf16_to_f32(O.f32_to_bf16(y + c))
+        t_tok += time.perf_counter() - t0
+        ntok += 1
+    nbytes, _ = moe_algorithmic_bytes(E, k, dim, inter)
+    per_tok = t_tok / ntok
+    return {
+        "value": nbytes / per_tok / 1e9, "unit": "GB/s",
+        "cores": int(os.environ.get("APUS_THREADS", CPU_THREADS)),
+        "kind": "reference" if use_ref else "port",
+        "sample": ("%d decode tokens x 8 experts on pre-dequantized BF16 payloads "
+                   "(%.1f ms/token); dequant-on-fill of the 8 experts %.1f ms "
+                   "reported separately, not in value" % (ntok, per_tok * 1e3,
+                                                          t_deq * 1e3)),
+        "ms_per_token": per_tok * 1e3, "dequant_fill_ms": t_deq * 1e3,
+    }
+
+
+# --------------------------------------------------------------------------
+# config 1: dense FP8 GEMV at M = 1, 2, 4
+# --------------------------------------------------------------------------
+
+def bench_dense_gemv(lib, pkg, rt, steps, warmup, M=1, copies=12):
+    N, K, seed = 16384, 4096, 0xC1
+    nsb = (N // 128) * (K // 128)
+    codes = rt.DevBuf(copies * N * K)
+    for c in range(copies):
+        pkg.check(lib.apus_synth_fp8_codes_dev(ctypes.c_void_p(codes.ptr + c * N * K),
+                                               N * K, seed + c, 10, 0, None),
+                  "synth codes")
+    sc = np.empty((copies, nsb), np.float32)
+    for c in range(copies):
+        lib.apus_synth_scales(sc[c].ctypes.data_as(ctypes.c_void_p), nsb, seed + c,
+                              11, 1e-4, 1e-2)
+    d_s = rt.DevBuf.of(sc)
+    x = np.empty((M, K), np.uint16)
+    lib.apus_synth_bf16_normal(x.ctypes.data_as(ctypes.c_void_p), x.size, seed, 12, 0)
+    d_x = rt.DevBuf.of(x)
+    d_y = rt.DevBuf(M * N * 2)
+    st = rt.Stream()
+
+    def step(i):
+        c = i % copies
+        rc = lib.apus_ghip_fp8blk_linear_dev(
+            ctypes.c_void_p(codes.ptr + c * N * K),
+            ctypes.c_void_p(d_s.ptr + c * nsb * 4), d_x.vp, d_y.vp, M, N, K, 0, st.vp)
+        if rc:
+            pkg.check(rc, "fp8blk_linear_dev")
+
+    for i in range(warmup):
+        step(i)
+    st.synchronize()
+    e0, e1 = rt.Event(), rt.Event()
+    e0.record(st)
+    for i in range(steps):
+        step(warmup + i)
+    e1.record(st)
+    e1.synchronize()
+    ms = e0.elapsed_ms(e1) / steps
+    nbytes = N * K + nsb * 4 + M * K * 2 + M * N * 2
+    return {"ms_per_step": ms, "value": nbytes / (ms * 1e-3) / 1e9,
+            "bytes": nbytes, "flops": 2 * M * N * K, "kernel": "k_fp8_gemv",
+            "config": {"workload": "dense_gemv (BASELINE config 1)", "N": N, "K": K,
+                       "M": M, "weight_copies": copies}}
+
+
+def cpu_dense_gemv(lib, M=1, budget_s=10.0):
+    os.environ.setdefault("APUS_THREADS", str(CPU_THREADS))
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    N, K, seed = 16384, 4096, 0xC1
+    P = O.ptr
+    codes = np.empty((N, K), np.uint8)
+    lib.apus_synth_fp8_codes(P(codes), codes.size, seed, 10, 0)
+    sc = np.empty((N // 128, K // 128), np.float32)
+    lib.apus_synth_scales(P(sc), sc.size, seed, 11, 1e-4, 1e-2)
+    x = np.empty((M, K), np.uint16)
+    lib.apus_synth_bf16_normal(P(x), x.size, seed, 12, 0)
+    y = np.empty((M, N), np.uint16)
+    use_ref = O.ref_available()
+    n, t = 0, 0.0
+    while t < budget_s and n < 2000:
+        t0 = time.perf_counter()
+        if use_ref:
+            O.ref().ref_fp8blk_linear_mt(P(codes), P(sc), P(x), P(y), M, N, K)
+        else:
+            O.lib().apo_fp8blk_linear(P(codes), P(sc), P(x), P(y), M, N, K, CPU_THREADS)
+        t += time.perf_counter() - t0
+        n += 1
+    nbytes = N * K + sc.size * 4 + M * K * 2 + M * N * 2
+    return {"value": nbytes / (t / n) / 1e9, "unit": "GB/s",
+            "cores": int(os.environ.get("APUS_THREADS", CPU_THREADS)),
+            "kind": "reference" if use_ref else "port",
+            "sample": "%d calls of dequant_mt + gemm_mt (c/gdsa.h:532-533), "
+                      "M=%d, %.1f ms/call" % (n, M, t / n * 1e3)}
+
+
+# --------------------------------------------------------------------------
+# calibration: a plain device-to-device copy of known size
+# --------------------------------------------------------------------------
+
+def bench_copy(rt, steps, warmup, nbytes=256 << 20):
+    """hipMemcpyAsync D2D of 256 MiB (the runtime's copy kernel): the
+    known-size reference that scales rocprofv3 FETCH_SIZE / WRITE_SIZE."""
+    a, b = rt.DevBuf(nbytes), rt.DevBuf(nbytes)
+    a.zero()
+    st = rt.Stream()
+    h = rt.hip()
+    for _ in range(warmup):
+        rt.check(h.hipMemcpyAsync(b.vp, a.vp, nbytes, rt.D2D, st.vp), "copy")
+    st.synchronize()
+    e0, e1 = rt.Event(), rt.Event()
+    e0.record(st)
+    for _ in range(steps):
+        rt.check(h.hipMemcpyAsync(b.vp, a.vp, nbytes, rt.D2D, st.vp), "copy")
+    e1.record(st)
+    e1.synchronize()
+    ms = e0.elapsed_ms(e1) / steps
+    return {"ms_per_step": ms, "value": 2 * nbytes / (ms * 1e-3) / 1e9,
+            "bytes": 2 * nbytes, "flops": 0, "kernel": "copy",
+            "config": {"workload": "copy (FETCH/WRITE calibration)",
+                       "bytes_read": nbytes, "bytes_written": nbytes}}
+
+
+# --------------------------------------------------------------------------
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="moe_decode",
+                    choices=["moe_decode", "dense_gemv", "copy"])
+    ap.add_argument("--m", type=int, default=1, help="dense_gemv rows (1, 2, 4)")
+    ap.add_argument("--no-cpu", action="store_true",
+                    help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(the sharding design is described in DESIGN.md); run --gpus 1",
+              file=sys.stderr)
+        sys.exit(2)
+    pkg, rt = load_pkg()
+    lib = pkg.load()
+    err = ctypes.create_string_buffer(256)
+    pkg.check(lib.apus_ghip_enable(err, 256), "apus_ghip_enable")
+
+    if args.workload == "moe_decode":
+        r = bench_moe_decode(lib, pkg, rt, args.steps, args.warmup)
+        metric = "FP8 MoE decode GEMV HBM GB/s"
+        cpu = None if args.no_cpu else cpu_moe_decode(lib)
+    elif args.workload == "dense_gemv":
+        r = bench_dense_gemv(lib, pkg, rt, args.steps, args.warmup, M=args.m)
+        metric = "FP8 dense decode GEMV HBM GB/s"
+        cpu = None if args.no_cpu else cpu_dense_gemv(lib, M=args.m)
+    else:
+        r = bench_copy(rt, args.steps, args.warmup)
+        metric = "device copy HBM GB/s (read + write)"
+        cpu = None
+    traffic = traffic_from_profiles(r["kernel"])
+    line = {
+        "metric": metric,
+        "value": round(r["value"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r["ms_per_step"], 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (include/apus_synth.h generator, seeded)",
+        "config": r["config"],
+        "roofline": {
+            "bound": "hbm",
+            "kernel": r["kernel"],
+            "achieved": round(r["value"], 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(r["value"] / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "algorithmic_bytes_per_launch": r["bytes"],
+            "mfma_tflops": round(r["flops"] / (r["ms_per_step"] * 1e-3) / 1e12, 3),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()
