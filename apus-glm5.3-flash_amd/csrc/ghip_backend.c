@@ -65,6 +65,9 @@ static struct {
     /* counters */
     uint64_t bytes_wrapped, bytes_pinned, dispatches, off_bf16, off_fp8;
     uint64_t h2d, d2h;
+    /* caller-owned timing events (apus_ghip_set_trace_events), n = 0: off */
+    hipEvent_t trace_ev[6];
+    int trace_n;
 } G;
 
 static _Thread_local char g_err[512];
@@ -361,7 +364,7 @@ int apus_ghip_fp8blk_linear(const uint8_t *codes, const float *scales,
         return 1;
     HIPCHK(ghip_launch_fp8_linear((const uint8_t *)dc, (const float *)ds,
                                   (const uint16_t *)G.d_x, (uint16_t *)G.d_y,
-                                  M, O, K, flag, G.stream));
+                                  M, O, K, flag, NULL, G.stream));
     G.dispatches++;
     if (sync_out(y, G.d_y, M * O * 2)) return 1;
     G.off_fp8++;
@@ -435,9 +438,18 @@ int apus_ghip_fp8blk_linear_dev(const uint8_t *codes, const float *scales,
     int rc;
     const uint32_t *flag = exact_flag_dev(codes, O * K, exact, st, &rc);
     if (rc) { ghip_seterr("fp8blk_linear_dev: flag setup failed"); return 1; }
-    HIPCHK(ghip_launch_fp8_linear(codes, scales, x, y, M, O, K, flag, st));
+    HIPCHK(ghip_launch_fp8_linear(codes, scales, x, y, M, O, K, flag,
+                                  G.trace_n >= 2 ? G.trace_ev : NULL, st));
     G.dispatches++;
     return 0;
+}
+
+void apus_ghip_set_trace_events(void *const *events, int n) {
+    G.trace_n = 0;
+    if (!events || n <= 0) return;
+    if (n > 6) n = 6;
+    for (int i = 0; i < n; i++) G.trace_ev[i] = (hipEvent_t)events[i];
+    G.trace_n = n;
 }
 
 int apus_ghip_fp8blk_dequant_dev(const uint8_t *codes, const float *scales,
@@ -734,6 +746,7 @@ int apus_ghip_moe_decode_dev(ApusGhipStore *s, const uint16_t *x,
     store_bank(s, &bk);
     hipError_t e = ghip_launch_moe_decode(&bk, x, logits, idx, w, topk,
                                           s->limit, out, &s->ws,
+                                          G.trace_n >= 6 ? G.trace_ev : NULL,
                                           (hipStream_t)stream);
     if (e != hipSuccess) {
         ghip_seterr("moe_decode launch: %s", hipGetErrorString(e));

@@ -20,6 +20,7 @@
 #define GHIP_DEVICE_H
 
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <stdint.h>
 
 typedef __bf16 ghip_bf16x8 __attribute__((ext_vector_type(8)));
@@ -250,5 +251,17 @@ __device__ __forceinline__ uint32_t ghip_swiglu(float g, float u, float limit) {
     float hv = ghip_bf16_round(g * ghip_sigmoid_np(g));
     return ghip_bf16_bits(hv * u);
 }
+
+/* Launch with optional start/stop timing events carried by the dispatch
+ * packet itself (hipExtLaunchKernelGGL): no extra marker packets between
+ * launches, so the measured span is the kernel's own. */
+#define GHIP_LAUNCH(ev0, ev1, kern, grid, block, lds, st, ...)                  \
+    do {                                                                       \
+        if ((ev0) || (ev1))                                                    \
+            hipExtLaunchKernelGGL(kern, grid, block, lds, st, ev0, ev1, 0,     \
+                                  __VA_ARGS__);                                \
+        else                                                                   \
+            hipLaunchKernelGGL(kern, grid, block, lds, st, __VA_ARGS__);       \
+    } while (0)
 
 #endif /* GHIP_DEVICE_H */

@@ -33,7 +33,7 @@ hipError_t ghip_launch_nan_scan(const uint8_t *codes, size_t n,
 hipError_t ghip_launch_fp8_linear(const uint8_t *codes, const float *scales,
                                   const uint16_t *x, uint16_t *y, size_t M,
                                   size_t O, size_t K, const uint32_t *exact_dev,
-                                  hipStream_t st);
+                                  const hipEvent_t *ev, hipStream_t st);
 
 /* BF16-weight GEMV/GEMM: y[M,O] = x[M,K] . W[O,K]^T. Any shape. */
 hipError_t ghip_launch_bf16_linear(const uint16_t *w, const uint16_t *x,
@@ -68,7 +68,7 @@ hipError_t ghip_launch_moe_decode(const GhipBank *bank, const uint16_t *x,
                                   const float *logits, const int32_t *idx,
                                   const float *w, int topk, float limit,
                                   uint16_t *out, const GhipMoeDecodeWs *ws,
-                                  hipStream_t st);
+                                  const hipEvent_t *ev, hipStream_t st);
 
 /* Fill n u32 words with value (a kernel, not a memset, so callers may
  * capture it in a graph). */

@@ -270,13 +270,12 @@ template <int M>
 static hipError_t launch_gemv_m(const uint8_t *codes, const float *scales,
                                 const uint16_t *x, uint16_t *y, size_t O,
                                 size_t K, const uint32_t *exact_dev,
-                                hipStream_t st) {
+                                hipEvent_t ev0, hipEvent_t ev1, hipStream_t st) {
     size_t lds = (size_t)M * K * 2;
     uint32_t nkb = (uint32_t)((K + 127) / 128);
     uint32_t g = (uint32_t)((O + 15) / 16);
-    hipLaunchKernelGGL(k_fp8_gemv<M>, dim3(g), dim3(GEMV_NW * 64), lds, st,
-                       codes, scales, x, y, (uint32_t)O, (uint32_t)K, nkb,
-                       exact_dev);
+    GHIP_LAUNCH(ev0, ev1, k_fp8_gemv<M>, dim3(g), dim3(GEMV_NW * 64), lds, st,
+                codes, scales, x, y, (uint32_t)O, (uint32_t)K, nkb, exact_dev);
     return hipGetLastError();
 }
 
@@ -288,19 +287,22 @@ extern "C" hipError_t ghip_launch_fp8_linear(const uint8_t *codes,
                                              const uint16_t *x, uint16_t *y,
                                              size_t M, size_t O, size_t K,
                                              const uint32_t *exact_dev,
+                                             const hipEvent_t *ev,
                                              hipStream_t st) {
     if (M == 0 || O == 0) return hipSuccess;
     if (K == 0 || O > 0x7fffffffu || K > 0x7fffffffu || M > 0x7fffffffu)
         return hipErrorInvalidValue;
+    /* timing events: start on the first launch, stop on the last */
+    hipEvent_t ev0 = ev ? ev[0] : nullptr, ev1 = ev ? ev[1] : nullptr;
     bool fast = (K % 128 == 0) && (((uintptr_t)codes & 15) == 0)
              && (((uintptr_t)x & 15) == 0) && K * 2 <= GEMV_LDS_MAX;
     if (!fast) {
         uint32_t nkb = (uint32_t)((K + 127) / 128);
         size_t items = M * O;
         if (items > 0xffffffffull * 4) return hipErrorInvalidValue;
-        hipLaunchKernelGGL(k_fp8_linear_any, dim3((uint32_t)((items + 3) / 4)),
-                           dim3(256), 0, st, codes, scales, x, y, (uint32_t)M,
-                           (uint32_t)O, (uint32_t)K, nkb);
+        GHIP_LAUNCH(ev0, ev1, k_fp8_linear_any, dim3((uint32_t)((items + 3) / 4)),
+                    dim3(256), 0, st, codes, scales, x, y, (uint32_t)M,
+                    (uint32_t)O, (uint32_t)K, nkb);
         return hipGetLastError();
     }
     /* m-groups of up to 4 rows, each as large as the x staging allows */
@@ -311,12 +313,13 @@ extern "C" hipError_t ghip_launch_fp8_linear(const uint8_t *codes,
         while (mc > 1 && mc * K * 2 > GEMV_LDS_MAX) mc--;
         const uint16_t *xm = x + m0 * K;
         uint16_t *ym = y + m0 * O;
+        hipEvent_t a = m0 == 0 ? ev0 : nullptr, b = m0 + mc == M ? ev1 : nullptr;
         hipError_t e;
         switch (mc) {
-        case 4: e = launch_gemv_m<4>(codes, scales, xm, ym, O, K, exact_dev, st); break;
-        case 3: e = launch_gemv_m<3>(codes, scales, xm, ym, O, K, exact_dev, st); break;
-        case 2: e = launch_gemv_m<2>(codes, scales, xm, ym, O, K, exact_dev, st); break;
-        default: e = launch_gemv_m<1>(codes, scales, xm, ym, O, K, exact_dev, st); break;
+        case 4: e = launch_gemv_m<4>(codes, scales, xm, ym, O, K, exact_dev, a, b, st); break;
+        case 3: e = launch_gemv_m<3>(codes, scales, xm, ym, O, K, exact_dev, a, b, st); break;
+        case 2: e = launch_gemv_m<2>(codes, scales, xm, ym, O, K, exact_dev, a, b, st); break;
+        default: e = launch_gemv_m<1>(codes, scales, xm, ym, O, K, exact_dev, a, b, st); break;
         }
         if (e != hipSuccess) return e;
         m0 += mc;

@@ -338,6 +338,7 @@ extern "C" hipError_t ghip_launch_moe_decode(const GhipBank *bank,
                                              int topk, float limit,
                                              uint16_t *out,
                                              const GhipMoeDecodeWs *ws,
+                                             const hipEvent_t *ev,
                                              hipStream_t st) {
     if (!bank || !ws || !x || !out) return hipErrorInvalidValue;
     const uint32_t dim = bank->dim, inter = bank->inter;
@@ -352,15 +353,17 @@ extern "C" hipError_t ghip_launch_moe_decode(const GhipBank *bank,
         return hipErrorInvalidValue;
     const size_t lds_gu = (size_t)dim * 2, lds_dn = (size_t)topk * inter * 2;
     if (lds_gu > 64 * 1024 || lds_dn > 64 * 1024) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(64), 0, st, logits, idx, w, topk,
-                       (int)bank->n_experts, ws->route, ws->err);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_moe_gateup, dim3((uint32_t)topk * (inter / MD_T)),
-                       dim3(MD_NW * 64), lds_gu, st, *bank, x, ws->route, limit, ws->h);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_moe_down, dim3(dim / MD_T), dim3(MD_NW * 64), lds_dn, st,
-                       *bank, ws->h, ws->route, out);
+    hipEvent_t e0 = ev ? ev[0] : nullptr, e1 = ev ? ev[1] : nullptr;
+    hipEvent_t e2 = ev ? ev[2] : nullptr, e3 = ev ? ev[3] : nullptr;
+    hipEvent_t e4 = ev ? ev[4] : nullptr, e5 = ev ? ev[5] : nullptr;
+    hipError_t e;
+    GHIP_LAUNCH(e0, e1, k_moe_route, dim3(1), dim3(64), 0, st, logits, idx, w, topk,
+                (int)bank->n_experts, ws->route, ws->err);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    GHIP_LAUNCH(e2, e3, k_moe_gateup, dim3((uint32_t)topk * (inter / MD_T)),
+                dim3(MD_NW * 64), lds_gu, st, *bank, x, ws->route, limit, ws->h);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    GHIP_LAUNCH(e4, e5, k_moe_down, dim3(dim / MD_T), dim3(MD_NW * 64), lds_dn, st,
+                *bank, ws->h, ws->route, out);
     return hipGetLastError();
 }

@@ -57,6 +57,24 @@ def traffic_from_profiles(kernel):
     return v.get("hbm_bytes_per_launch") if isinstance(v, dict) else None
 
 
+def kernel_times(lib, rt, step, first, steps, n_ev, pairs):
+    """Average duration (ms) of chosen launches, from start/stop HIP events
+    carried by the launches' own dispatch packets on the launch stream
+    (apus_ghip_set_trace_events), over a second pass of `steps` steps right
+    after the timed region.
+    pairs: {name: (i, j)} -> mean elapsed(events[i], events[j])."""
+    evs = [[rt.Event() for _ in range(n_ev)] for _ in range(steps)]
+    arr_t = ctypes.c_void_p * n_ev
+    for i in range(steps):
+        arr = arr_t(*[e.handle for e in evs[i]])
+        lib.apus_ghip_set_trace_events(arr, n_ev)
+        step(first + i)
+    lib.apus_ghip_set_trace_events(None, 0)
+    evs[-1][-1].synchronize()
+    return {name: sum(evs[i][a].elapsed_ms(evs[i][b]) for i in range(steps)) / steps
+            for name, (a, b) in pairs.items()}
+
+
 # --------------------------------------------------------------------------
 # config 2: MoE decode
 # --------------------------------------------------------------------------
@@ -65,10 +83,14 @@ MOE = dict(E=288, k=8, dim=4096, inter=2048, seed=0xC2, limit=10.0)
 
 
 def moe_algorithmic_bytes(E, k, dim, inter):
+    """(step bytes, step flops, gate/up launch bytes). Step: k expert slabs
+    (FP8 codes + F32 block scales) + x + out + logits. Gate/up launch: the k
+    gate and up members + x + the k*inter BF16 h rows it writes."""
     nb = lambda n: (n + 127) // 128  # noqa: E731
-    slab = 2 * (inter * dim + nb(inter) * nb(dim) * 4) + dim * inter \
-        + nb(dim) * nb(inter) * 4
-    return k * slab + dim * 2 + dim * 2 + E * 4, 2 * k * 3 * inter * dim
+    gu = 2 * (inter * dim + nb(inter) * nb(dim) * 4)
+    slab = gu + dim * inter + nb(dim) * nb(inter) * 4
+    return (k * slab + dim * 2 + dim * 2 + E * 4, 2 * k * 3 * inter * dim,
+            k * gu + dim * 2 + k * inter * 2)
 
 
 def bench_moe_decode(lib, pkg, rt, steps, warmup, rotate=64):
@@ -111,12 +133,18 @@ def bench_moe_decode(lib, pkg, rt, steps, warmup, rotate=64):
     e1.synchronize()
     wall = time.perf_counter() - t0
     ms = e0.elapsed_ms(e1) / steps
-    nbytes, flops = moe_algorithmic_bytes(E, k, dim, inter)
+    kt = kernel_times(lib, rt, step, warmup + steps, steps, 6,
+                      {"k_moe_route": (0, 1), "k_moe_gateup": (2, 3),
+                       "k_moe_down": (4, 5)})
+    nbytes, flops, gu_bytes = moe_algorithmic_bytes(E, k, dim, inter)
     gbs = nbytes / (ms * 1e-3) / 1e9
     lib.apus_ghip_store_close(store)
     return {
         "ms_per_step": ms, "value": gbs, "wall_s": wall,
-        "bytes": nbytes, "flops": flops, "kernel": "k_moe_decode",
+        "bytes": nbytes, "flops": flops, "kernel": "k_moe_gateup",
+        "kernel_ms": kt["k_moe_gateup"], "kernel_bytes": gu_bytes,
+        "kernel_flops": 2 * k * 2 * inter * dim,
+        "launch_ms": {n: round(v, 5) for n, v in kt.items()},
         "config": {"workload": "moe_decode (BASELINE config 2)", "experts": E,
                    "topk": k, "dim": dim, "inter": inter, "tokens": 1,
                    "rotated_tokens": rotate, "weights": "fp8-e4m3 128x128 blocks",
@@ -177,7 +205,7 @@ def cpu_moe_decode(lib, budget_s=12.0):
             y = O.bf16_to_f32(O.f32_to_bf16(y + c))
         t_tok += time.perf_counter() - t0
         ntok += 1
-    nbytes, _ = moe_algorithmic_bytes(E, k, dim, inter)
+    nbytes = moe_algorithmic_bytes(E, k, dim, inter)[0]
     per_tok = t_tok / ntok
     return {
         "value": nbytes / per_tok / 1e9, "unit": "GB/s",
@@ -232,9 +260,14 @@ def bench_dense_gemv(lib, pkg, rt, steps, warmup, M=1, copies=12):
     e1.record(st)
     e1.synchronize()
     ms = e0.elapsed_ms(e1) / steps
+    kt = kernel_times(lib, rt, step, warmup + steps, steps, 2,
+                      {"k_fp8_gemv": (0, 1)})
     nbytes = N * K + nsb * 4 + M * K * 2 + M * N * 2
     return {"ms_per_step": ms, "value": nbytes / (ms * 1e-3) / 1e9,
             "bytes": nbytes, "flops": 2 * M * N * K, "kernel": "k_fp8_gemv",
+            "kernel_ms": kt["k_fp8_gemv"], "kernel_bytes": nbytes,
+            "kernel_flops": 2 * M * N * K,
+            "launch_ms": {n: round(v, 5) for n, v in kt.items()},
             "config": {"workload": "dense_gemv (BASELINE config 1)", "N": N, "K": K,
                        "M": M, "weight_copies": copies}}
 
@@ -293,6 +326,8 @@ def bench_copy(rt, steps, warmup, nbytes=256 << 20):
     ms = e0.elapsed_ms(e1) / steps
     return {"ms_per_step": ms, "value": 2 * nbytes / (ms * 1e-3) / 1e9,
             "bytes": 2 * nbytes, "flops": 0, "kernel": "copy",
+            "kernel_ms": ms, "kernel_bytes": 2 * nbytes, "kernel_flops": 0,
+            "launch_ms": {"copy": round(ms, 5)},
             "config": {"workload": "copy (FETCH/WRITE calibration)",
                        "bytes_read": nbytes, "bytes_written": nbytes}}
 
@@ -333,6 +368,7 @@ def main():
         metric = "device copy HBM GB/s (read + write)"
         cpu = None
     traffic = traffic_from_profiles(r["kernel"])
+    achieved = r["kernel_bytes"] / (r["kernel_ms"] * 1e-3) / 1e9
     line = {
         "metric": metric,
         "value": round(r["value"], 2),
@@ -350,13 +386,15 @@ def main():
         "roofline": {
             "bound": "hbm",
             "kernel": r["kernel"],
-            "achieved": round(r["value"], 2),
+            "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(r["value"] / HBM_PEAK_GBS, 4),
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "algorithmic_bytes_per_launch": r["bytes"],
-            "mfma_tflops": round(r["flops"] / (r["ms_per_step"] * 1e-3) / 1e12, 3),
+            "algorithmic_bytes_per_launch": r["kernel_bytes"],
+            "avg_launch_ms": round(r["kernel_ms"], 6),
+            "launch_ms": r["launch_ms"],
+            "mfma_tflops": round(r["kernel_flops"] / (r["kernel_ms"] * 1e-3) / 1e12, 3),
         },
         "cpu_baseline": cpu,
     }

@@ -188,6 +188,17 @@ int apus_ghip_moe_decode_dev(ApusGhipStore *s, const uint16_t *x,
                              const float *w, int topk, uint16_t *out,
                              void *stream);
 
+/* --- timing (no reference counterpart; for benchmarks and profilers).
+ * events: n caller-created hipEvent_t handles, NULL/0 turns it off. While
+ * set, launches carry start/stop events in their dispatch packets
+ * (hipExtLaunchKernelGGL), so an event pair spans exactly one kernel:
+ * apus_ghip_moe_decode_dev (n >= 6) times routing with events[0..1], the
+ * gate/up launch with events[2..3] and the down launch with events[4..5];
+ * apus_ghip_fp8blk_linear_dev (n >= 2) starts events[0] with its first
+ * GEMV launch and stops events[1] with its last. Process-wide, not
+ * thread-safe; the events must outlive their use. */
+void apus_ghip_set_trace_events(void *const *events, int n);
+
 #ifdef __cplusplus
 }
 #endif
