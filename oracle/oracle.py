@@ -26,6 +26,12 @@ c_float = ctypes.c_float
 c_u8 = ctypes.c_uint8
 c_u16 = ctypes.c_uint16
 
+class SlabLayout(ctypes.Structure):
+    """ApoSlabLayout: byte offsets of the six slab members and the size."""
+    _fields_ = [(n, c_size) for n in ("gw", "gs", "uw", "us", "dw", "ds",
+                                      "bytes")]
+
+
 _ORACLE_SIGS = {
     "apo_e4m3_f32": (c_float, [c_u8]),
     "apo_bf16_bits": (c_u16, [c_float]),
@@ -45,6 +51,7 @@ _ORACLE_SIGS = {
     "apo_topk_stable": (None, [c_vp, c_int, c_int, c_vp]),
     "apo_swiglu_expert": (c_int, [c_vp, c_vp, c_vp, c_vp, c_size, c_size,
                                   c_float, c_vp, c_vp, c_vp, c_vp, c_int]),
+    "apo_slab_layout": (SlabLayout, [c_size, c_size]),
     "apo_slab_dequant": (None, [c_vp, c_size, c_size, c_vp, c_int]),
     "apo_moe_forward": (c_int, [c_vp, c_int, c_size, c_size, c_float, c_vp,
                                 c_size, c_vp, c_vp, c_int, c_vp, c_vp, c_int]),

@@ -175,3 +175,18 @@ def test_expert_vs_reference_build_real_shape():
     assert R.ref_gmoe_expert(O.ptr(pl[0]), O.ptr(pl[1]), O.ptr(pl[2]), O.ptr(x),
                              dim, inter, 10.0, O.ptr(out_ref)) == 0
     assert np.array_equal(O.swiglu_expert(*pl, x, threads=8)[0], out_ref)
+
+
+def test_slab_layout_arithmetic():
+    """Slab = gate.w | gate.s | up.w | up.s | down.w | down.s
+    (c/gcache.h:852-861); 25,171,968 B at dim 4096 / inter 2048
+    (tests/m1/README.md:77-78 of the reference); ragged scale grids use
+    ceil(n/128)."""
+    L = O.lib().apo_slab_layout(4096, 2048)
+    assert L.bytes == 25_171_968
+    assert (L.gw, L.gs, L.uw) == (0, 8_388_608, 8_388_608 + 2048)
+    assert L.us == L.uw + 8_388_608 and L.dw == L.us + 2048
+    assert L.ds == L.dw + 8_388_608 and L.bytes == L.ds + 2048
+    r = O.lib().apo_slab_layout(200, 136)       # inter 136 -> 2 blocks, dim 2
+    nb = 2 * 2 * 4
+    assert r.bytes == 2 * (136 * 200 + nb) + 200 * 136 + nb
