@@ -61,6 +61,11 @@ SIGNATURES = {
     "apus_ghip_moe_decode": (c_int, [c_vp, c_vp, c_vp, c_vp, c_int, c_vp]),
     "apus_ghip_moe_decode_dev": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_int,
                                          c_vp, c_vp]),
+    "apus_ghip_moe_prefill_reserve": (c_int, [c_vp, c_size, c_int]),
+    "apus_ghip_moe_prefill": (c_int, [c_vp, c_vp, c_size, c_vp, c_vp, c_int,
+                                      c_vp]),
+    "apus_ghip_moe_prefill_dev": (c_int, [c_vp, c_vp, c_size, c_vp, c_vp,
+                                          c_int, c_vp, c_vp]),
     "apus_ghip_set_trace_events": (None, [ctypes.POINTER(c_vp), c_int]),
     # include/apus_synth.h
     "apus_synth_mix64": (c_u64, [c_u64]),

@@ -18,7 +18,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 
 C_SRCS = ["ghip_backend.c", "ghip_synth.c"]
-HIP_SRCS = ["k_linear.hip", "k_moe.hip", "k_synth.hip"]
+HIP_SRCS = ["k_linear.hip", "k_moe.hip", "k_moe_prefill.hip", "k_synth.hip"]
 
 INC = ["-I" + os.path.join(ROOT, "include"), "-I" + CSRC]
 CFLAGS = ["-std=c11", "-O2", "-Wall", "-Wextra", "-fPIC", "-ffp-contract=off",

@@ -66,8 +66,14 @@ static struct {
     uint64_t bytes_wrapped, bytes_pinned, dispatches, off_bf16, off_fp8;
     uint64_t h2d, d2h;
     /* caller-owned timing events (apus_ghip_set_trace_events), n = 0: off */
-    hipEvent_t trace_ev[6];
+    hipEvent_t trace_ev[8];
     int trace_n;
+    /* K4 prefill workspace (process-wide, grow-only) and host staging */
+    GhipMoePrefillWs pf;
+    size_t pf_cap[8];
+    void *pf_x, *pf_idx, *pf_w, *pf_out;
+    size_t pf_cap_x, pf_cap_idx, pf_cap_w, pf_cap_out;
+    int pf_inited;
 } G;
 
 static _Thread_local char g_err[512];
@@ -447,7 +453,7 @@ int apus_ghip_fp8blk_linear_dev(const uint8_t *codes, const float *scales,
 void apus_ghip_set_trace_events(void *const *events, int n) {
     G.trace_n = 0;
     if (!events || n <= 0) return;
-    if (n > 6) n = 6;
+    if (n > 8) n = 8;
     for (int i = 0; i < n; i++) G.trace_ev[i] = (hipEvent_t)events[i];
     G.trace_n = n;
 }
@@ -781,6 +787,127 @@ int apus_ghip_moe_decode(ApusGhipStore *s, const uint16_t *x,
     if (err) {
         ghip_seterr("moe_decode: invalid expert id in routing (code %u)", err);
         hipMemset(s->ws.err, 0, 4);
+        return 1;
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* K4: routed MoE prefill                                                   */
+/* ------------------------------------------------------------------------ */
+
+/* Grow one prefill workspace buffer; the caller has drained the device. */
+static int pf_grow(void **p, size_t *cap, size_t need) {
+    if (need <= *cap) return 0;
+    need = (need + 4095) & ~(size_t)4095;
+    if (*p) HIPCHK(hipFree(*p));
+    *p = NULL;
+    *cap = 0;
+    HIPCHK(hipMalloc(p, need));
+    *cap = need;
+    return 0;
+}
+
+int apus_ghip_moe_prefill_reserve(const ApusGhipStore *s, size_t tokens,
+                                  int topk) {
+    if (ghip_init()) return 1;
+    if (!s || topk <= 0 || topk > GHIP_MAX_TOPK) {
+        ghip_seterr("moe_prefill_reserve: bad store or topk %d", topk);
+        return 1;
+    }
+    if (!G.pf_inited) {
+        HIPCHK(ghip_moe_prefill_init());
+        G.pf_inited = 1;
+    }
+    const size_t P = tokens * (size_t)topk;
+    if (P == 0) return 0;
+    const uint32_t E = (uint32_t)s->n_experts;
+    const size_t need[8] = {
+        16 * sizeof(uint32_t),
+        ghip_moe_prefill_chunks(P) * E * sizeof(uint32_t),
+        ghip_moe_prefill_max_tiles(P, E) * 4 * sizeof(uint32_t),
+        P * sizeof(int32_t), P * sizeof(int32_t), P * sizeof(int32_t),
+        P * s->inter * 2, P * s->dim * 2};
+    int grow_any = 0;
+    for (int i = 0; i < 8; i++) grow_any |= need[i] > G.pf_cap[i];
+    if (grow_any) {
+        HIPCHK(hipDeviceSynchronize());
+        void **bufs[8] = {(void **)&G.pf.hdr, (void **)&G.pf.cnt,
+                          (void **)&G.pf.tiles, (void **)&G.pf.eid,
+                          (void **)&G.pf.perm, (void **)&G.pf.pos,
+                          (void **)&G.pf.h, (void **)&G.pf.o};
+        for (int i = 0; i < 8; i++)
+            if (pf_grow(bufs[i], &G.pf_cap[i], need[i])) return 1;
+    }
+    /* every buffer now holds this shape's P pairs (the chunk and tile
+     * arrays depend on P and E, so the limit is per call, not a max) */
+    G.pf.cap_pairs = P;
+    return 0;
+}
+
+int apus_ghip_moe_prefill_dev(ApusGhipStore *s, const uint16_t *x, size_t T,
+                              const int32_t *idx, const float *w, int topk,
+                              uint16_t *out, void *stream) {
+    if (!s) { ghip_seterr("moe_prefill: no store"); return 1; }
+    if (topk <= 0 || topk > GHIP_MAX_TOPK) {
+        ghip_seterr("moe_prefill: topk %d outside 1..%d", topk, GHIP_MAX_TOPK);
+        return 1;
+    }
+    if (T == 0) return 0;
+    if (s->dim % 256 || s->inter % 128 || s->n_experts > 1024) {
+        ghip_seterr("moe_prefill: needs dim %% 256 == 0, inter %% 128 == 0 and "
+                    "<= 1024 experts (dim=%zu inter=%zu E=%d)", s->dim, s->inter,
+                    s->n_experts);
+        return 1;
+    }
+    if (apus_ghip_moe_prefill_reserve(s, T, topk)) return 1;
+    GhipBank bk;
+    store_bank(s, &bk);
+    hipError_t e = ghip_launch_moe_prefill(&bk, x, T, idx, w, topk, s->limit, out,
+                                           &G.pf,
+                                           G.trace_n >= 8 ? G.trace_ev : NULL,
+                                           (hipStream_t)stream);
+    if (e != hipSuccess) {
+        ghip_seterr("moe_prefill launch: %s", hipGetErrorString(e));
+        return 1;
+    }
+    G.dispatches++;
+    return 0;
+}
+
+int apus_ghip_moe_prefill(ApusGhipStore *s, const uint16_t *x, size_t T,
+                          const int32_t *idx, const float *w, int topk,
+                          uint16_t *out) {
+    if (!s) { ghip_seterr("moe_prefill: no store"); return 1; }
+    if (topk <= 0 || topk > GHIP_MAX_TOPK) {
+        ghip_seterr("moe_prefill: topk %d outside 1..%d", topk, GHIP_MAX_TOPK);
+        return 1;
+    }
+    if (T == 0) return 0;
+    const size_t P = T * (size_t)topk;
+    for (size_t p = 0; p < P; p++)
+        if (idx[p] < 0 || idx[p] >= s->n_experts) {
+            ghip_seterr("moe_prefill: expert id %d out of range (pair %zu)",
+                        idx[p], p);
+            return 1;
+        }
+    if (grow(&G.pf_x, &G.pf_cap_x, T * s->dim * 2)
+        || grow(&G.pf_idx, &G.pf_cap_idx, P * 4)
+        || grow(&G.pf_w, &G.pf_cap_w, P * 4)
+        || grow(&G.pf_out, &G.pf_cap_out, T * s->dim * 2))
+        return 1;
+    if (h2d(G.pf_x, x, T * s->dim * 2) || h2d(G.pf_idx, idx, P * 4)
+        || h2d(G.pf_w, w, P * 4))
+        return 1;
+    if (apus_ghip_moe_prefill_dev(s, (const uint16_t *)G.pf_x, T,
+                                  (const int32_t *)G.pf_idx, (const float *)G.pf_w,
+                                  topk, (uint16_t *)G.pf_out, G.stream))
+        return 1;
+    if (sync_out(out, G.pf_out, T * s->dim * 2)) return 1;
+    uint32_t hdr[PF_HDR_WORDS];
+    HIPCHK(hipMemcpy(hdr, G.pf.hdr, sizeof hdr, hipMemcpyDeviceToHost));
+    if (hdr[PF_HDR_ERR]) {
+        ghip_seterr("moe_prefill: invalid expert id in routing");
         return 1;
     }
     return 0;

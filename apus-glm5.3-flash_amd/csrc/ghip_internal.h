@@ -70,6 +70,38 @@ hipError_t ghip_launch_moe_decode(const GhipBank *bank, const uint16_t *x,
                                   uint16_t *out, const GhipMoeDecodeWs *ws,
                                   const hipEvent_t *ev, hipStream_t st);
 
+/* K4 prefill workspace (device; sized for cap_pairs = T * topk pairs). */
+#define PF_HDR_NTILES 0
+#define PF_HDR_NPAIRS 1
+#define PF_HDR_ERR 2
+#define PF_HDR_WORDS 4
+typedef struct {
+    uint32_t *hdr;        /* PF_HDR_WORDS u32: tiles, kept pairs, error */
+    uint32_t *cnt;        /* [chunks, n_experts] histograms -> offsets */
+    uint32_t *tiles;      /* [max_tiles] x {expert, row0, rows, 0} */
+    int32_t *eid;         /* [pairs] expert of a kept pair, else -1 */
+    int32_t *perm;        /* [pairs] sorted row -> pair */
+    int32_t *pos;         /* [pairs] pair -> sorted row, -1 if dropped */
+    uint16_t *h;          /* [pairs, inter] bf16 SwiGLU activations */
+    uint16_t *o;          /* [pairs, dim] bf16 expert outputs */
+    size_t cap_pairs;
+} GhipMoePrefillWs;
+
+size_t ghip_moe_prefill_max_tiles(size_t pairs, uint32_t n_experts);
+size_t ghip_moe_prefill_chunks(size_t pairs);
+/* Raise the GEMM kernels' dynamic-LDS limit (once per process). */
+hipError_t ghip_moe_prefill_init(void);
+
+/* K4: routed MoE prefill for T tokens: permutation, grouped gate/up GEMM
+ * with the SwiGLU epilogue, grouped down GEMM, ordered combine (stream
+ * ordered on st). x [T, dim], idx/w [T, topk], out [T, dim], all device.
+ * ev: NULL or 8 events (permutation, gate/up, down, combine start/stop). */
+hipError_t ghip_launch_moe_prefill(const GhipBank *bank, const uint16_t *x,
+                                   size_t T, const int32_t *idx, const float *w,
+                                   int topk, float limit, uint16_t *out,
+                                   const GhipMoePrefillWs *ws,
+                                   const hipEvent_t *ev, hipStream_t st);
+
 /* Fill n u32 words with value (a kernel, not a memset, so callers may
  * capture it in a graph). */
 hipError_t ghip_launch_fill_u32(uint32_t *p, size_t n, uint32_t value,

@@ -188,6 +188,30 @@ int apus_ghip_moe_decode_dev(ApusGhipStore *s, const uint16_t *x,
                              const float *w, int topk, uint16_t *out,
                              void *stream);
 
+/* --- routed MoE prefill (T tokens): the reference runs, per token, the
+ * selected experts and the ordered combine (c/gmoe.h:278-320, expert body
+ * c/gmoe.h:210-227); here the same result is computed as grouped GEMMs over
+ * expert-sorted (token, expert) pairs: a GPU stable counting sort of the
+ * pairs, one gate/up GEMM launch with the SwiGLU epilogue and one down GEMM
+ * launch over all experts (FP8 tiles dequantized bit-exactly in registers,
+ * BF16 MFMA, fp32 accumulation), then the ascending-expert bf16-per-add
+ * combine. idx/w [T, topk] row-major (token t's slots at t*topk). A repeated
+ * id inside one token counts once, with its first slot's weight, as the
+ * reference loop. Needs dim % 256 == 0, inter % 128 == 0, <= 1024 experts,
+ * topk <= 16. Tolerance class as the GEMV (floor = sum_e |contrib_e|).
+ * The device variant is stream-ordered; ids out of range are dropped from
+ * the sum (the host variant rejects them before launching). All prefill
+ * calls share one process-wide workspace (grown on demand; reserve to size
+ * it up front), so calls on different streams must not overlap in time. */
+int apus_ghip_moe_prefill_reserve(const ApusGhipStore *s, size_t tokens,
+                                  int topk);
+int apus_ghip_moe_prefill(ApusGhipStore *s, const uint16_t *x, size_t T,
+                          const int32_t *idx, const float *w, int topk,
+                          uint16_t *out);
+int apus_ghip_moe_prefill_dev(ApusGhipStore *s, const uint16_t *x, size_t T,
+                              const int32_t *idx, const float *w, int topk,
+                              uint16_t *out, void *stream);
+
 /* --- timing (no reference counterpart; for benchmarks and profilers).
  * events: n caller-created hipEvent_t handles, NULL/0 turns it off. While
  * set, launches carry start/stop events in their dispatch packets
@@ -195,7 +219,10 @@ int apus_ghip_moe_decode_dev(ApusGhipStore *s, const uint16_t *x,
  * apus_ghip_moe_decode_dev (n >= 6) times routing with events[0..1], the
  * gate/up launch with events[2..3] and the down launch with events[4..5];
  * apus_ghip_fp8blk_linear_dev (n >= 2) starts events[0] with its first
- * GEMV launch and stops events[1] with its last. Process-wide, not
+ * GEMV launch and stops events[1] with its last; apus_ghip_moe_prefill_dev
+ * (n >= 8) times the permutation with events[0..1], the gate/up GEMM with
+ * events[2..3], the down GEMM with events[4..5] and the combine with
+ * events[6..7]. Process-wide, not
  * thread-safe; the events must outlive their use. */
 void apus_ghip_set_trace_events(void *const *events, int n);
 

@@ -32,3 +32,15 @@ def vp(buf):
 
 def stream():
     return None          # the null stream
+
+
+def download_ptr(ptr, dtype, shape):
+    """Copy from a raw device address (e.g. a store slab) to numpy."""
+    import ctypes
+    r = rt()
+    r.synchronize()
+    out = np.empty(shape, dtype)
+    r.check(r.hip().hipMemcpy(out.ctypes.data_as(ctypes.c_void_p),
+                              ctypes.c_void_p(ptr), out.nbytes, r.D2H),
+            "hipMemcpy D2H")
+    return out

@@ -12,7 +12,7 @@ import pytest
 
 import oracle as O
 import gpu_util as G
-from tolerance import assert_close
+from tolerance import assert_close, assert_close_combined
 
 pytestmark = pytest.mark.gpu
 GOLD = os.path.join(os.path.dirname(__file__), "golden")
@@ -89,7 +89,7 @@ def test_moe_decode_vs_oracle(small, k):
         assert rc == 0, ghip.apus_ghip_last_error()
         want, eo = O.moe_forward(slabs, dim, inter, x, idx[None], w[None],
                                  want_expert_out=True)
-        assert_close(out, want[0], moe_floor(eo, w[None], idx[None])[0],
+        assert_close_combined(out, want[0], moe_floor(eo, w[None], idx[None])[0],
                      "k=%d trial %d" % (k, trial))
         out2 = np.empty(dim, np.uint16)
         assert ghip.apus_ghip_moe_decode(s, O.ptr(x), O.ptr(idx), O.ptr(w), idx.size,
@@ -108,7 +108,7 @@ def test_moe_decode_duplicate_ids_first_slot(small):
     want, eo = O.moe_forward(slabs, dim, inter, x, idx[None], w[None],
                              want_expert_out=True)
     fl = moe_floor(eo[:, [0, 1, 3]], w[None, [0, 1, 3]], None)[0]
-    assert_close(out, want[0], fl, "duplicate ids")
+    assert_close_combined(out, want[0], fl, "duplicate ids")
 
 
 def test_moe_decode_dev_logits(small):
@@ -124,7 +124,7 @@ def test_moe_decode_dev_logits(small):
     dx, dl, dout = G.dev(x), G.dev(logits), G.empty(dim * 2)
     assert ghip.apus_ghip_moe_decode_dev(s, G.vp(dx), G.vp(dl), None, None, 8,
                                          G.vp(dout), G.stream()) == 0
-    assert_close(G.host(dout, np.uint16, (dim,)), want[0],
+    assert_close_combined(G.host(dout, np.uint16, (dim,)), want[0],
                  moe_floor(eo, w[None], idx[None])[0], "device routing")
 
 
@@ -149,12 +149,12 @@ def test_config2_golden(ghip, pkg):
         dx, dl, dout = G.dev(x), G.dev(logits), G.empty(dim * 2)
         assert ghip.apus_ghip_moe_decode_dev(s, G.vp(dx), G.vp(dl), None, None, k,
                                              G.vp(dout), G.stream()) == 0
-        st = assert_close(G.host(dout, np.uint16, (dim,)), fx["cfg2_out"], fl,
+        st = assert_close_combined(G.host(dout, np.uint16, (dim,)), fx["cfg2_out"], fl,
                           "config2 device routing")
         print("config2", st)
         out = np.empty(dim, np.uint16)
         assert ghip.apus_ghip_moe_decode(s, O.ptr(x), O.ptr(idx), O.ptr(w), k,
                                          O.ptr(out)) == 0
-        assert_close(out, fx["cfg2_out"], fl, "config2 host routing")
+        assert_close_combined(out, fx["cfg2_out"], fl, "config2 host routing")
     finally:
         ghip.apus_ghip_store_close(s)

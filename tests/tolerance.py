@@ -6,9 +6,14 @@ bf16 code (sign-magnitude folded to two's complement; +0 == -0).
 relative error: |a - b| / max(|b|, floor). The floor makes the bound
 meaningful where the exact result cancels to ~0:
   GEMV/GEMM output   floor = 2^-8 * sum_k |w_k * x_k|  (f64, oracle)
+  expert output      floor = sum_i |h_i * wd_i|         (the down GEMM's
+                     terms: h comes out of the GPU's own gate/up GEMM, so an
+                     ulp step of one h_i is a legitimate input difference)
   MoE combine output floor = sum_e |contrib_e|         (the combined terms)
 An fp32 reordering moves a sum by ~sqrt(K)*2^-24*sum|terms|, far below the
 floor; a wrong term or index moves it by O(|term|), far above 1e-2.
+GEMV/GEMM outputs (and a single expert's output) take the ulp test as is;
+the MoE combine takes it at its cancellation scale (compare_combined).
 """
 import numpy as np
 
@@ -51,5 +56,39 @@ def compare(got, ref, floor):
 def assert_close(got, ref, floor, what=""):
     st = compare(got, ref, floor)
     assert st["frac_le1ulp"] >= ULP_FRAC_MIN and st["max_rel"] <= REL_MAX, \
+        "%s: %s" % (what, st)
+    return st
+
+
+def bf16_ulp_at(v):
+    """bf16 ulp at magnitude v: 2^(floor(log2 v) - 7) (8 significant bits);
+    0 where v == 0."""
+    v = np.asarray(v, np.float64)
+    with np.errstate(divide="ignore"):
+        e = np.floor(np.log2(np.where(v > 0, v, 1.0)))
+    return np.where(v > 0, np.exp2(e - 7), 0.0)
+
+
+def compare_combined(got, ref, floor):
+    """compare() plus the ulp test at the output's cancellation scale, for
+    sums of bf16-rounded terms (the MoE combine, floor = sum_e |contrib_e|):
+    |got - ref| <= one bf16 ulp of max(|ref|, floor). A one-ulp change of
+    one expert output -- the GEMM contract -- moves the combined value by
+    up to one ulp of that scale, however far the sum cancels; the raw ulp
+    distance of a cancelling sum is unbounded for any summation order,
+    including an exact one."""
+    st = compare(got, ref, floor)
+    g = bf16_f32(np.asarray(got, np.uint16).ravel()).astype(np.float64)
+    r = bf16_f32(np.asarray(ref, np.uint16).ravel()).astype(np.float64)
+    fl = np.asarray(floor, np.float64)
+    fl = np.full(r.shape, float(fl)) if fl.size == 1 else fl.ravel()
+    unit = bf16_ulp_at(np.maximum(np.abs(r), fl))
+    st["frac_le1ulp_scaled"] = float(np.mean(np.abs(g - r) <= unit)) if r.size else 1.0
+    return st
+
+
+def assert_close_combined(got, ref, floor, what=""):
+    st = compare_combined(got, ref, floor)
+    assert st["frac_le1ulp_scaled"] >= ULP_FRAC_MIN and st["max_rel"] <= REL_MAX, \
         "%s: %s" % (what, st)
     return st
