@@ -817,6 +817,11 @@ int apus_ghip_moe_prefill_reserve(const ApusGhipStore *s, size_t tokens,
     }
     if (!G.pf_inited) {
         HIPCHK(ghip_moe_prefill_init());
+        int ncu = 0;
+        HIPCHK(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount,
+                                     G.device));
+        if (ncu <= 0) { ghip_seterr("moe_prefill: no compute units"); return 1; }
+        G.pf.n_cu = (uint32_t)((ncu + 7) / 8 * 8);
         G.pf_inited = 1;
     }
     const size_t P = tokens * (size_t)topk;

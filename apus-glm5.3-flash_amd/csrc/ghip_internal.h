@@ -85,6 +85,7 @@ typedef struct {
     uint16_t *h;          /* [pairs, inter] bf16 SwiGLU activations */
     uint16_t *o;          /* [pairs, dim] bf16 expert outputs */
     size_t cap_pairs;
+    uint32_t n_cu;        /* persistent GEMM grid: the device's CU count */
 } GhipMoePrefillWs;
 
 size_t ghip_moe_prefill_max_tiles(size_t pairs, uint32_t n_experts);

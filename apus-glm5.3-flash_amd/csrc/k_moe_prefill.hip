@@ -33,11 +33,13 @@
  * 128-block, identical for A and B. 32-row blocks past the tile's row count
  * skip their MFMAs, so ragged experts cost what their rows need.
  *
- * Workgroup -> work mapping is XCD-aware: hardware deals workgroups to the
- * 8 XCDs round-robin, so block b is remapped to logical id
- * (b % 8) * (G / 8) + b / 8 and logical ids enumerate column blocks fastest:
- * the column blocks of one tile (same gathered activation rows) run on one
- * XCD and share its L2.
+ * The GEMM grid is persistent and XCD-aware: one workgroup per CU;
+ * hardware deals workgroups to the 8 XCDs round-robin, so workgroup b
+ * (XCD b % 8) works on tiles b % 8, b % 8 + 8, ... and the XCD's
+ * workgroups split each tile's column blocks: the column blocks of one tile
+ * (same gathered activation rows) run on one XCD and share its L2, and the
+ * worst-case tile count sizes nothing (the real count is read on the
+ * device).
  */
 #include "ghip_device.h"
 #include "ghip_internal.h"
@@ -47,8 +49,11 @@ typedef float ghip_f32x16 __attribute__((ext_vector_type(16)));
 #define PF_CHUNK 1024            /* pairs per permutation workgroup */
 #define PF_BM 256                /* rows per GEMM tile */
 #define PF_RB (PF_BM / 32)       /* 32-row MFMA blocks per tile */
-#define PF_PITCH 136             /* LDS row pitch (bf16): 128 + 8 pad */
-#define PF_BUF (PF_BM * PF_PITCH)
+#define PF_BK 64                 /* k per pipeline stage */
+#define PF_A_STAGE (PF_BM * PF_BK * 2)          /* 32 KB activation tile */
+#define PF_W_STAGE (256 * PF_BK)                /* 16 KB FP8 weight rows */
+#define PF_STAGE (PF_A_STAGE + PF_W_STAGE)
+#define PF_LDS (3 * PF_STAGE)                   /* 144 KB ring */
 #define PF_MAXK 16               /* max top-k per token */
 #define PF_MAXE 1024             /* max experts in a bank */
 
@@ -182,46 +187,204 @@ __global__ __launch_bounds__(1024) void k_pf_scatter(
 /* grouped GEMM                                                             */
 /* ------------------------------------------------------------------------ */
 
-/* 8 codes (two dwords) -> one bf16x8 MFMA operand. `exact` (wave-uniform:
- * the expert holds NaN codes) selects the integer decode; a branch per
- * operand keeps one copy of the MFMA loop and its registers. */
-__device__ __forceinline__ ghip_bf16x8 pf_deq8(uint32_t d0, uint32_t d1, float s,
-                                               bool exact) {
-    ghip_u32x2 a, b;
-    if (exact) {
-        a = ghip_deq4<true>(d0, s);
-        b = ghip_deq4<true>(d1, s);
-    } else {
-        a = ghip_deq4<false>(d0, s);
-        b = ghip_deq4<false>(d1, s);
-    }
+/* 8 codes (two dwords) -> one bf16x8 MFMA operand. */
+template <bool EXACT>
+__device__ __forceinline__ ghip_bf16x8 pf_deq8(uint32_t d0, uint32_t d1, float s) {
+    ghip_u32x2 a = ghip_deq4<EXACT>(d0, s), b = ghip_deq4<EXACT>(d1, s);
     ghip_u32x4 v = {a[0], a[1], b[0], b[1]};
     return __builtin_bit_cast(ghip_bf16x8, v);
 }
 
-/* One 128-wide k step of a wave: 8 MFMA k-slices x (up to) 8 row blocks x
- * 2 weight slots. */
-__device__ __forceinline__ void pf_step(const uint16_t *__restrict__ ab,
-                                        const ghip_u32x4 (&c0)[4],
-                                        const ghip_u32x4 (&c1)[4], float s0,
-                                        float s1, uint32_t nrb, uint32_t n,
-                                        uint32_t h, bool exact,
-                                        ghip_f32x16 (&a0)[PF_RB],
-                                        ghip_f32x16 (&a1)[PF_RB]) {
+typedef __attribute__((address_space(3))) void pf_lds_t;
+typedef __attribute__((address_space(1))) void pf_glb_t;
+
+/* 16 bytes global -> LDS, bypassing registers (gfx950
+ * global_load_lds_dwordx4): lane l of the wave writes lds_wave + 16*l. */
+__device__ __forceinline__ void pf_dma16(const void *src, void *lds_wave) {
+    __builtin_amdgcn_global_load_lds((pf_glb_t *)src, (pf_lds_t *)lds_wave, 16, 0, 0);
+}
+
+/* s_waitcnt vmcnt(N), other counters untouched. */
+#define PF_VMCNT(N) __builtin_amdgcn_s_waitcnt(((N) & 15) | (((N) >> 4) << 14) | 0x0F70)
+
+/* s_waitcnt vmcnt(LPS * min(m, M)): wait until at most min(m, M) stages of
+ * LPS loads each are still in flight (m wave-uniform). */
+template <uint32_t LPS, uint32_t M>
+__device__ __forceinline__ void pf_wait(uint32_t m) {
+    if constexpr (M == 0) {
+        PF_VMCNT(0);
+    } else {
+        if (m >= M) PF_VMCNT(LPS * M);
+        else pf_wait<LPS, M - 1>(m);
+    }
+}
+
+/* What one workgroup computes (see k_pf_gemm). */
+struct PfTile {
+    const uint16_t *act;          /* activation matrix (x or H), K wide */
+    const int32_t *perm;          /* sorted row -> pair (mode 0 gather) */
+    const uint8_t *w0, *w1;       /* weight matrices of the two slots */
+    const float *sr0, *sr1;       /* scale rows of the two slots */
+    uint16_t *out;
+    uint32_t K, N, row0, rows, cb0, cb1, topk;  /* cbX: slot X column base */
+    float limit;
+};
+
+/* The tile body for tiles of at most NRB 32-row blocks (rows past NRB*32
+ * are neither loaded nor computed; rows past `rows` inside the last block
+ * repeat the last row: computed, never stored).
+ *
+ * K advances in stages of 64 through a 3-deep LDS ring filled by direct
+ * global->LDS loads (no register staging): stage load j+2 is in flight
+ * while stage j is computed. Stage layout, 16-byte pieces XOR-swizzled so
+ * the MFMA operand reads hit distinct banks:
+ *   A  [256 rows][8 pieces]  piece p of row r at (p ^ ((r >> 1) & 7))
+ *   W  [256 rows][4 pieces]  weight row wr = 64*wave + 32*slot + n,
+ *                            piece p at (p ^ ((wr >> 2) & 3))
+ * Inside a stage, lane half h owns k in [32h, 32h+32); MFMA step s takes
+ * k = 32h + 8s + [0, 8) from both operands. */
+template <int MODE, int NRB, bool EXACT>
+__device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds) {
+    constexpr uint32_t LPS = NRB + 4;            /* DMA loads per thread per stage */
+    /* ring depth: as many stages as the LDS holds, so tiles with few rows
+     * keep more weight bytes in flight (3, 4, 6, 7 stages for 8, 4, 2, 1
+     * row blocks) */
+    constexpr uint32_t ASTG = NRB * 32 * PF_BK * 2;
+    constexpr uint32_t STG = ASTG + PF_W_STAGE;
+    constexpr uint32_t NS = PF_LDS / STG < 8 ? PF_LDS / STG : 8;
+    static_assert(NS >= 3 && LPS * (NS - 2) <= 63, "ring depth vs vmcnt range");
+    /* opaque thread id: keeps the lane-derived address math of this body
+     * inside the persistent item loop instead of hoisted and held live
+     * across items for every body */
+    uint32_t tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const uint32_t wv = tid >> 6, lane = tid & 63;
+    const uint32_t n = lane & 31, h = lane >> 5;
+    const uint32_t K = t.K, nst = K / PF_BK;
+
+    /* --- DMA source addresses (stage 0); stage j adds j*64 elements ---- */
+    const uint8_t *asrc[NRB];
 #pragma unroll
-    for (int s = 0; s < 8; s++) {
-        const ghip_u32x4 q0 = c0[s >> 1], q1 = c1[s >> 1];
-        const int o = (s & 1) * 2;
-        const ghip_bf16x8 b0 = pf_deq8(q0[o], q0[o + 1], s0, exact);
-        const ghip_bf16x8 b1 = pf_deq8(q1[o], q1[o + 1], s1, exact);
-        const uint16_t *ar = ab + n * PF_PITCH + 64 * h + 8 * s;
+    for (int i = 0; i < NRB; i++) {
+        const uint32_t r = 32 * i + 8 * wv + (lane >> 3);
+        const uint32_t rc = r < t.rows ? r : t.rows - 1;
+        const uint32_t src = MODE == 0 ? (uint32_t)t.perm[t.row0 + rc] / t.topk
+                                       : t.row0 + rc;
+        const uint32_t p = (lane & 7) ^ ((r >> 1) & 7);
+        asrc[i] = (const uint8_t *)(t.act + (size_t)src * K) + 16 * p;
+    }
+    const uint8_t *wsrc[4];
 #pragma unroll
-        for (int rb = 0; rb < PF_RB; rb++) {
-            if ((uint32_t)rb < nrb) {
-                const ghip_bf16x8 a =
-                    *(const ghip_bf16x8 *)(ar + (size_t)rb * 32 * PF_PITCH);
-                a0[rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b0, a0[rb], 0, 0, 0);
-                a1[rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b1, a1[rb], 0, 0, 0);
+    for (int i = 0; i < 4; i++) {
+        const uint32_t wr = 64 * i + 16 * wv + (lane >> 2);
+        const uint32_t w = wr >> 6, j = (wr >> 5) & 1, nn = wr & 31;
+        const uint32_t col = (j ? t.cb1 : t.cb0) + 32 * w + nn;
+        const uint32_t p = (lane & 3) ^ ((wr >> 2) & 3);
+        wsrc[i] = (j ? t.w1 : t.w0) + (size_t)col * K + 16 * p;
+    }
+    auto issue = [&](uint32_t j) {
+        uint8_t *st = lds + (j % NS) * STG;
+#pragma unroll
+        for (int i = 0; i < NRB; i++)
+            pf_dma16(asrc[i] + (size_t)j * PF_BK * 2, st + (4 * i + wv) * 1024);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            pf_dma16(wsrc[i] + (size_t)j * PF_BK, st + ASTG + (4 * i + wv) * 1024);
+    };
+
+    /* --- operand read offsets inside a stage --------------------------- */
+    uint32_t aoff[4], boff0[2], boff1[2];
+#pragma unroll
+    for (int s = 0; s < 4; s++)
+        aoff[s] = n * 128 + 16 * (((4 * h) | s) ^ ((n >> 1) & 7));
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const uint32_t ph = ((2 * h + u) ^ ((n >> 2) & 3)) * 16;
+        boff0[u] = ASTG + (64 * wv + n) * 64 + ph;
+        boff1[u] = ASTG + (64 * wv + 32 + n) * 64 + ph;
+    }
+
+    ghip_f32x16 a0[NRB], a1[NRB];
+#pragma unroll
+    for (int rb = 0; rb < NRB; rb++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) { a0[rb][i] = 0.0f; a1[rb][i] = 0.0f; }
+
+#pragma unroll
+    for (uint32_t i = 0; i + 1 < NS; i++)
+        if (i < nst) issue(i);
+    for (uint32_t j = 0; j < nst; j++) {
+        /* own DMA for stage j done (later stages may stay in flight), then a
+         * bare barrier: every wave's stage-j writes have landed and every
+         * wave is done reading buffer (j-1) % NS, refilled next. No fence:
+         * a fence would drain the whole DMA stream at each stage. */
+        const uint32_t later = nst - 1 - j;
+        pf_wait<LPS, NS - 2>(later);
+        __builtin_amdgcn_s_barrier();
+        if (j + NS - 1 < nst) issue(j + NS - 1);
+        const uint8_t *st = lds + (j % NS) * STG;
+        /* wave-uniform scale reads through the constant address space:
+         * scalar loads (lgkmcnt), so they never wait behind the DMA stream */
+        const float sc0 = ((const __attribute__((address_space(4))) float *)t.sr0)[j >> 1];
+        const float sc1 = ((const __attribute__((address_space(4))) float *)t.sr1)[j >> 1];
+        /* operands one MFMA step ahead: A rows of step s+1 and the dequant
+         * of B for step s+1 are in flight while step s's MFMAs run */
+        ghip_u32x4 q0[2], q1[2];
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            q0[u] = *(const ghip_u32x4 *)(st + boff0[u]);
+            q1[u] = *(const ghip_u32x4 *)(st + boff1[u]);
+        }
+        ghip_bf16x8 av[NRB], an[NRB];
+#pragma unroll
+        for (int rb = 0; rb < NRB; rb++)
+            av[rb] = *(const ghip_bf16x8 *)(st + rb * 32 * 128 + aoff[0]);
+        ghip_bf16x8 b0 = pf_deq8<EXACT>(q0[0][0], q0[0][1], sc0);
+        ghip_bf16x8 b1 = pf_deq8<EXACT>(q1[0][0], q1[0][1], sc1);
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            ghip_bf16x8 nb0 = b0, nb1 = b1;
+            if (s < 3) {
+                const int u = (s + 1) >> 1, v = 2 * ((s + 1) & 1);
+#pragma unroll
+                for (int rb = 0; rb < NRB; rb++)
+                    an[rb] = *(const ghip_bf16x8 *)(st + rb * 32 * 128 + aoff[s + 1]);
+                nb0 = pf_deq8<EXACT>(q0[u][v], q0[u][v + 1], sc0);
+                nb1 = pf_deq8<EXACT>(q1[u][v], q1[u][v + 1], sc1);
+            }
+#pragma unroll
+            for (int rb = 0; rb < NRB; rb++) {
+                a0[rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[rb], b0, a0[rb], 0, 0, 0);
+                a1[rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[rb], b1, a1[rb], 0, 0, 0);
+            }
+            /* let the scheduler interleave the LDS reads of step s+1 with
+             * step s's MFMAs (small-GEMM interleave strategy) */
+            __builtin_amdgcn_iglp_opt(0);
+#pragma unroll
+            for (int rb = 0; rb < NRB; rb++) av[rb] = an[rb];
+            b0 = nb0;
+            b1 = nb1;
+        }
+    }
+
+    /* epilogue: lane (n, h), register i of row block rb holds output row
+     * rb*32 + 8*(i/4) + 4*h + i%4, column n of each slot */
+    const uint32_t c0 = t.cb0 + 32 * wv + n, c1 = t.cb1 + 32 * wv + n;
+#pragma unroll
+    for (int rb = 0; rb < NRB; rb++) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const uint32_t r = rb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+            if (r < t.rows) {
+                uint16_t *o = t.out + (size_t)(t.row0 + r) * t.N;
+                if (MODE == 0) {
+                    const float g = ghip_bf16_round(a0[rb][i]);
+                    const float u = ghip_bf16_round(a1[rb][i]);
+                    o[c0] = (uint16_t)ghip_swiglu(g, u, t.limit);
+                } else {
+                    o[c0] = (uint16_t)ghip_bf16_bits(a0[rb][i]);
+                    o[c1] = (uint16_t)ghip_bf16_bits(a1[rb][i]);
+                }
             }
         }
     }
@@ -231,133 +394,62 @@ __device__ __forceinline__ void pf_step(const uint16_t *__restrict__ ab,
  *         out = H [P, inter] (sorted rows), SwiGLU epilogue.
  * MODE 1: act = H [P, inter] (sorted rows); out = O [P, dim] (sorted rows),
  *         bf16 expert outputs.
- * Grid: G (multiple of 8) >= tiles * nblk; 256 threads. */
+ * Grid: G (multiple of 8) >= tiles * nblk; 256 threads. The body is chosen
+ * once per tile: 8, 4, 2 or 1 row blocks (the smallest that holds the
+ * tile), or the exact-decode body for an expert with NaN codes. */
 template <int MODE>
 __global__ __launch_bounds__(256, 1) void k_pf_gemm(
     GhipBank bank, const uint16_t *__restrict__ act,
     const int32_t *__restrict__ perm, const uint4 *__restrict__ tiles,
     const uint32_t *__restrict__ hdr, uint32_t nblk, uint32_t topk,
     float limit, uint16_t *__restrict__ out) {
-    extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
-    const uint32_t G = gridDim.x, b = blockIdx.x;
-    const uint32_t L = (b & 7u) * (G >> 3) + (b >> 3);
-    const uint32_t tile = L / nblk, nb = L - tile * nblk;
-    if (tile >= hdr[PF_HDR_NTILES]) return;
-    const uint4 td = tiles[tile];
-    const uint32_t e = td.x, row0 = td.y, rows = td.z;
+    extern __shared__ __attribute__((aligned(1024))) uint8_t pf_lds[];
+    /* persistent: one workgroup per CU; workgroup b runs on XCD b % 8 and
+     * that XCD takes tiles x, x+8, ...; its workgroups share each tile's
+     * column blocks (same activation rows, one L2) */
+    const uint32_t ntiles = hdr[PF_HDR_NTILES];
+    const uint32_t x = blockIdx.x & 7u, c = blockIdx.x >> 3, per = gridDim.x >> 3;
+    const uint32_t ntx = ntiles > x ? (ntiles - x + 7) >> 3 : 0;
+    const uint32_t items = ntx * nblk;
     const uint32_t K = MODE == 0 ? bank.dim : bank.inter;
     const uint32_t nkb = K >> 7;
-    const uint8_t *slab = bank.base + (size_t)e * bank.stride;
-    const uint32_t tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
-    const uint32_t n = lane & 31, h = lane >> 5;
-    uint32_t col0, col1;
-    const uint8_t *w0, *w1;
-    const float *s0, *s1;
-    if (MODE == 0) {
-        col0 = col1 = nb * 128 + 32 * wv;
-        w0 = slab + bank.off_gw;
-        w1 = slab + bank.off_uw;
-        s0 = (const float *)(slab + bank.off_gs);
-        s1 = (const float *)(slab + bank.off_us);
-    } else {
-        col0 = nb * 256 + 32 * wv;
-        col1 = col0 + 128;
-        w0 = w1 = slab + bank.off_dw;
-        s0 = s1 = (const float *)(slab + bank.off_ds);
-    }
-    const uint8_t *wr0 = w0 + (size_t)(col0 + n) * K + 64 * h;
-    const uint8_t *wr1 = w1 + (size_t)(col1 + n) * K + 64 * h;
-    const float *sr0 = s0 + (size_t)(col0 >> 7) * nkb;
-    const float *sr1 = s1 + (size_t)(col1 >> 7) * nkb;
-    const bool exact = bank.nan_flags && bank.nan_flags[e];
-    const uint32_t nrb = (rows + 31) >> 5;
-
-    /* activation rows of this thread's 16 loads: tile row i*16 + tid/16,
-     * 16-byte piece tid%16 of the 128-wide step; rows past the tile clamp
-     * to its last row (computed, never stored). */
-    uint32_t arow[16];
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-        uint32_t r = i * 16 + (tid >> 4);
-        r = r < rows ? r : rows - 1;
-        arow[i] = MODE == 0 ? (uint32_t)perm[row0 + r] / topk : row0 + r;
-    }
-    const uint32_t pc = (tid & 15) * 8;
-    const uint32_t nld = nrb * 2;         /* 16-row groups that hold rows */
-
-    ghip_u32x4 areg[16];
-    ghip_u32x4 c0[4], c1[4], n0[4], n1[4];
-#pragma unroll
-    for (int i = 0; i < 16; i++)
-        if ((uint32_t)i < nld)
-            areg[i] = *(const ghip_u32x4 *)(act + (size_t)arow[i] * K + pc);
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-        c0[q] = __builtin_nontemporal_load((const ghip_u32x4 *)(wr0 + 16 * q));
-        c1[q] = __builtin_nontemporal_load((const ghip_u32x4 *)(wr1 + 16 * q));
-    }
-#pragma unroll
-    for (int i = 0; i < 16; i++)
-        if ((uint32_t)i < nld)
-            *(ghip_u32x4 *)(lds + (i * 16 + (tid >> 4)) * PF_PITCH + pc) = areg[i];
-    __syncthreads();
-
-    ghip_f32x16 a0[PF_RB], a1[PF_RB];
-#pragma unroll
-    for (int rb = 0; rb < PF_RB; rb++)
-#pragma unroll
-        for (int i = 0; i < 16; i++) { a0[rb][i] = 0.0f; a1[rb][i] = 0.0f; }
-
-    for (uint32_t kb = 0; kb < nkb; kb++) {
-        const uint32_t kn = kb + 1 < nkb ? kb + 1 : kb;   /* clamped prefetch */
-#pragma unroll
-        for (int i = 0; i < 16; i++)
-            if ((uint32_t)i < nld)
-                areg[i] = *(const ghip_u32x4 *)(act + (size_t)arow[i] * K +
-                                                 (size_t)kn * 128 + pc);
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            n0[q] = __builtin_nontemporal_load(
-                (const ghip_u32x4 *)(wr0 + (size_t)kn * 128 + 16 * q));
-            n1[q] = __builtin_nontemporal_load(
-                (const ghip_u32x4 *)(wr1 + (size_t)kn * 128 + 16 * q));
+    for (uint32_t k = c; k < items; k += per) {
+        const uint32_t tile = x + 8 * (k / nblk), nb = k % nblk;
+        const uint4 td = tiles[tile];
+        const uint32_t e = td.x;
+        PfTile t;
+        t.act = act;
+        t.perm = perm;
+        t.out = out;
+        t.row0 = td.y;
+        t.rows = td.z;
+        t.topk = topk;
+        t.limit = limit;
+        t.K = K;
+        t.N = MODE == 0 ? bank.inter : bank.dim;
+        const uint8_t *slab = bank.base + (size_t)e * bank.stride;
+        if (MODE == 0) {
+            t.cb0 = t.cb1 = nb * 128;
+            t.w0 = slab + bank.off_gw;
+            t.w1 = slab + bank.off_uw;
+            t.sr0 = (const float *)(slab + bank.off_gs) + (size_t)nb * nkb;
+            t.sr1 = (const float *)(slab + bank.off_us) + (size_t)nb * nkb;
+        } else {
+            t.cb0 = nb * 256;
+            t.cb1 = nb * 256 + 128;
+            t.w0 = t.w1 = slab + bank.off_dw;
+            t.sr0 = (const float *)(slab + bank.off_ds) + (size_t)(2 * nb) * nkb;
+            t.sr1 = (const float *)(slab + bank.off_ds) + (size_t)(2 * nb + 1) * nkb;
         }
-        const float sc0 = sr0[kb], sc1 = sr1[kb];
-        const uint16_t *ab = lds + (kb & 1) * PF_BUF;
-        pf_step(ab, c0, c1, sc0, sc1, nrb, n, h, exact, a0, a1);
-        if (kb + 1 < nkb) {
-            uint16_t *nbuf = lds + ((kb + 1) & 1) * PF_BUF;
-#pragma unroll
-            for (int i = 0; i < 16; i++)
-                if ((uint32_t)i < nld)
-                    *(ghip_u32x4 *)(nbuf + (i * 16 + (tid >> 4)) * PF_PITCH + pc) = areg[i];
-        }
-#pragma unroll
-        for (int q = 0; q < 4; q++) { c0[q] = n0[q]; c1[q] = n1[q]; }
-        __syncthreads();
-    }
-
-    /* epilogue: lane (n, h), register i of row block rb holds output row
-     * rb*32 + 8*(i/4) + 4*h + i%4, column n of each slot */
-    const uint32_t N = MODE == 0 ? bank.inter : bank.dim;
-#pragma unroll
-    for (int rb = 0; rb < PF_RB; rb++) {
-        if ((uint32_t)rb >= nrb) break;
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const uint32_t r = rb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
-            if (r < rows) {
-                uint16_t *o = out + (size_t)(row0 + r) * N;
-                if (MODE == 0) {
-                    const float g = ghip_bf16_round(a0[rb][i]);
-                    const float u = ghip_bf16_round(a1[rb][i]);
-                    o[col0 + n] = (uint16_t)ghip_swiglu(g, u, limit);
-                } else {
-                    o[col0 + n] = (uint16_t)ghip_bf16_bits(a0[rb][i]);
-                    o[col1 + n] = (uint16_t)ghip_bf16_bits(a1[rb][i]);
-                }
-            }
-        }
+        const uint32_t nrb = (t.rows + 31) >> 5;
+        if (bank.nan_flags && bank.nan_flags[e]) pf_tile<MODE, PF_RB, true>(t, pf_lds);
+        else if (nrb > 4) pf_tile<MODE, 8, false>(t, pf_lds);
+        else if (nrb > 2) pf_tile<MODE, 4, false>(t, pf_lds);
+        else if (nrb > 1) pf_tile<MODE, 2, false>(t, pf_lds);
+        else              pf_tile<MODE, 1, false>(t, pf_lds);
+        /* every wave is done with the LDS ring before the next item's
+         * prologue refills it */
+        __builtin_amdgcn_s_barrier();
     }
 }
 
@@ -425,8 +517,6 @@ extern "C" size_t ghip_moe_prefill_chunks(size_t pairs) {
     return (pairs + PF_CHUNK - 1) / PF_CHUNK;
 }
 
-static size_t round8(size_t v) { return (v + 7) & ~(size_t)7; }
-
 extern "C" hipError_t ghip_launch_moe_prefill(const GhipBank *bank,
                                               const uint16_t *x, size_t T,
                                               const int32_t *idx, const float *w,
@@ -442,6 +532,7 @@ extern "C" hipError_t ghip_launch_moe_prefill(const GhipBank *bank,
     if (dim == 0 || inter == 0 || dim % 256 || inter % 128) return hipErrorInvalidValue;
     const size_t P = T * (size_t)topk;
     if (P > ws->cap_pairs || P > 0x7fffffffu) return hipErrorInvalidValue;
+    if (ws->n_cu == 0 || ws->n_cu % 8) return hipErrorInvalidValue;
     if (((uintptr_t)x & 15) || ((uintptr_t)out & 15) || ((uintptr_t)bank->base & 15)
         || (bank->stride & 15) || (bank->off_gw & 15) || (bank->off_uw & 15)
         || (bank->off_dw & 15) || (bank->off_gs & 3) || (bank->off_us & 3)
@@ -464,14 +555,14 @@ extern "C" hipError_t ghip_launch_moe_prefill(const GhipBank *bank,
     GHIP_LAUNCH(nullptr, e1, k_pf_scatter, dim3(nch), dim3(1024), 16 * E * 4, st,
                 ws->eid, (uint32_t)P, E, ws->cnt, ws->perm, ws->pos);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    const size_t lds = 2 * (size_t)PF_BUF * 2;
-    const size_t g0 = round8(mt * (inter / 128)), g1 = round8(mt * (dim / 256));
-    if (g0 > 0x7fffffffu || g1 > 0x7fffffffu) return hipErrorInvalidValue;
-    GHIP_LAUNCH(e2, e3, k_pf_gemm<0>, dim3((uint32_t)g0), dim3(256), lds, st, *bank,
+    const size_t lds = PF_LDS;
+    (void)mt;
+    const uint32_t g0 = ws->n_cu, g1 = ws->n_cu;
+    GHIP_LAUNCH(e2, e3, k_pf_gemm<0>, dim3(g0), dim3(256), lds, st, *bank,
                 x, ws->perm, (const uint4 *)ws->tiles, ws->hdr, inter / 128,
                 (uint32_t)topk, limit, ws->h);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    GHIP_LAUNCH(e4, e5, k_pf_gemm<1>, dim3((uint32_t)g1), dim3(256), lds, st, *bank,
+    GHIP_LAUNCH(e4, e5, k_pf_gemm<1>, dim3(g1), dim3(256), lds, st, *bank,
                 ws->h, ws->perm, (const uint4 *)ws->tiles, ws->hdr, dim / 256,
                 (uint32_t)topk, limit, ws->o);
     if ((e = hipGetLastError()) != hipSuccess) return e;
@@ -482,7 +573,7 @@ extern "C" hipError_t ghip_launch_moe_prefill(const GhipBank *bank,
 }
 
 extern "C" hipError_t ghip_moe_prefill_init(void) {
-    const int lds = 2 * PF_BUF * 2;
+    const int lds = PF_LDS;
     hipError_t e = hipFuncSetAttribute((const void *)k_pf_gemm<0>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (e != hipSuccess) return e;

@@ -304,6 +304,123 @@ def cpu_dense_gemv(lib, M=1, budget_s=10.0):
 
 
 # --------------------------------------------------------------------------
+# configs 3 / 4: routed-MoE prefill (grouped GEMM, MFMA path)
+# --------------------------------------------------------------------------
+
+PREFILL = {
+    "prefill_zipf": dict(layers=1, T=2048, zipf=1.1, seed=0xC3,
+                         desc="BASELINE config 3: 288 experts, T=2048, Zipf(1.1) top-8"),
+    "prefill_stack": dict(layers=16, T=8192, zipf=0.0, seed=0xC4,
+                          desc="BASELINE config 4: 16 layers x 288 experts, "
+                               "T=8192 per layer, uniform top-8"),
+}
+
+
+def bench_prefill(lib, pkg, rt, steps, warmup, name):
+    """One step = the MoE prefill of every layer back to back (one
+    apus_ghip_moe_prefill_dev call per layer, each on its own 288-expert
+    bank, tokens and routing). FLOPs = pairs x 2*(2*inter*dim + dim*inter);
+    algorithmic bytes = the touched experts' FP8 slabs + x + out + routing."""
+    cfg = PREFILL[name]
+    E, k, dim, inter = 288, 8, 4096, 2048
+    L, T, seed = cfg["layers"], cfg["T"], cfg["seed"]
+    err = ctypes.create_string_buffer(256)
+    stores, xs, idxs, ws, outs, touched = [], [], [], [], [], []
+    slab = moe_algorithmic_bytes(E, 1, dim, inter)[0] - 2 * dim * 2 - E * 4
+    for l in range(L):
+        st_ = ctypes.c_void_p()
+        pkg.check(lib.apus_ghip_store_open(ctypes.byref(st_), E, dim, inter,
+                                           MOE["limit"], err, 256), "store_open")
+        pkg.check(lib.apus_ghip_store_synth(st_, seed + l, l, 1e-4, 1e-2), "store_synth")
+        stores.append(st_)
+        idx = np.empty((T, k), np.int32)
+        w = np.empty((T, k), np.float32)
+        pkg.check(lib.apus_synth_route(idx.ctypes.data_as(ctypes.c_void_p),
+                                       w.ctypes.data_as(ctypes.c_void_p), T, E, k,
+                                       cfg["zipf"], seed + l), "synth_route")
+        touched.append(int(np.unique(idx).size))
+        d_x = rt.DevBuf(T * dim * 2)
+        pkg.check(lib.apus_synth_bf16_normal_dev(d_x.vp, T * dim, seed + l, 40, 0,
+                                                 None), "synth x")
+        xs.append(d_x)
+        idxs.append(rt.DevBuf.of(idx))
+        ws.append(rt.DevBuf.of(w))
+        outs.append(rt.DevBuf(T * dim * 2))
+    pkg.check(lib.apus_ghip_moe_prefill_reserve(stores[0], T, k), "prefill_reserve")
+    st = rt.Stream()
+    rt.synchronize()
+
+    def step(_i):
+        for l in range(L):
+            rc = lib.apus_ghip_moe_prefill_dev(stores[l], xs[l].vp, T, idxs[l].vp,
+                                               ws[l].vp, k, outs[l].vp, st.vp)
+            if rc:
+                pkg.check(rc, "moe_prefill_dev")
+
+    for i in range(warmup):
+        step(i)
+    st.synchronize()
+    e0, e1 = rt.Event(), rt.Event()
+    e0.record(st)
+    for i in range(steps):
+        step(warmup + i)
+    e1.record(st)
+    e1.synchronize()
+    ms = e0.elapsed_ms(e1) / steps
+    # per-launch timing: 8 dispatch-packet events per layer call
+    evs = [[rt.Event() for _ in range(8)] for _ in range(L * steps)]
+    arr_t = ctypes.c_void_p * 8
+    for i in range(steps):
+        for l in range(L):
+            lib.apus_ghip_set_trace_events(arr_t(*[e.handle for e in evs[i * L + l]]), 8)
+            rc = lib.apus_ghip_moe_prefill_dev(stores[l], xs[l].vp, T, idxs[l].vp,
+                                               ws[l].vp, k, outs[l].vp, st.vp)
+            if rc:
+                pkg.check(rc, "moe_prefill_dev")
+    lib.apus_ghip_set_trace_events(None, 0)
+    evs[-1][-1].synchronize()
+    n = len(evs)
+    kt = {nm: sum(ev[a].elapsed_ms(ev[b]) for ev in evs) / n
+          for nm, (a, b) in {"k_pf_permute": (0, 1), "k_pf_gemm_gateup": (2, 3),
+                             "k_pf_gemm_down": (4, 5), "k_pf_combine": (6, 7)}.items()}
+    for s_ in stores:
+        lib.apus_ghip_store_close(s_)
+    P = T * k
+    flops = L * P * 2 * 3 * inter * dim
+    nbytes = sum(touched) * slab + L * (2 * T * dim * 2 + P * 8)
+    gu_flops = P * 2 * 2 * inter * dim
+    return {
+        "ms_per_step": ms, "value": flops / (ms * 1e-3) / 1e12, "unit": "TFLOP/s",
+        "bytes": nbytes, "flops": flops, "kernel": "k_pf_gemm_gateup",
+        "kernel_ms": kt["k_pf_gemm_gateup"], "kernel_flops": gu_flops,
+        "kernel_bytes": None, "launch_ms": {n_: round(v, 5) for n_, v in kt.items()},
+        "hbm_gbs": nbytes / (ms * 1e-3) / 1e9,
+        "config": {"workload": "%s (%s)" % (name, cfg["desc"]), "layers": L,
+                   "experts": E, "topk": k, "dim": dim, "inter": inter,
+                   "tokens_per_layer": T,
+                   "routing": "Zipf(%.1f)" % cfg["zipf"] if cfg["zipf"] > 0 else "uniform",
+                   "experts_touched_per_layer": touched[0] if L == 1 else
+                   [min(touched), max(touched)],
+                   "weights": "fp8-e4m3 128x128 blocks"},
+    }
+
+
+def cpu_moe_prefill(lib, L, T):
+    """The reference has no grouped GEMM: its prefill is the per-token loop
+    (c/gmoe.h:278-320), 8 experts per token on BF16 payloads -- the same
+    per-token work as a decode step. Timed on a bounded token sample and
+    reported as TFLOP/s (50,331,648 FLOP per (token, expert))."""
+    r = cpu_moe_decode(lib)
+    tflops = 8 * 50_331_648 / (r["ms_per_token"] * 1e-3) / 1e12
+    r = dict(r)
+    r["value"], r["unit"] = tflops, "TFLOP/s"
+    r["sample"] = (r["sample"] + "; the reference prefill runs this loop once per "
+                   "token, so %d x %d tokens would take %.1f s"
+                   % (L, T, L * T * r["ms_per_token"] * 1e-3))
+    return r
+
+
+# --------------------------------------------------------------------------
 # calibration: a plain device-to-device copy of known size
 # --------------------------------------------------------------------------
 
@@ -340,7 +457,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="moe_decode",
-                    choices=["moe_decode", "dense_gemv", "copy"])
+                    choices=["moe_decode", "dense_gemv", "prefill_zipf",
+                             "prefill_stack", "copy"])
     ap.add_argument("--m", type=int, default=1, help="dense_gemv rows (1, 2, 4)")
     ap.add_argument("--no-cpu", action="store_true",
                     help="skip the CPU baseline leg")
@@ -363,16 +481,25 @@ def main():
         r = bench_dense_gemv(lib, pkg, rt, args.steps, args.warmup, M=args.m)
         metric = "FP8 dense decode GEMV HBM GB/s"
         cpu = None if args.no_cpu else cpu_dense_gemv(lib, M=args.m)
+    elif args.workload in PREFILL:
+        r = bench_prefill(lib, pkg, rt, args.steps, args.warmup, args.workload)
+        metric = "prefill grouped-GEMM TFLOP/s"
+        cpu = None if args.no_cpu else cpu_moe_prefill(
+            lib, PREFILL[args.workload]["layers"], PREFILL[args.workload]["T"])
     else:
         r = bench_copy(rt, args.steps, args.warmup)
         metric = "device copy HBM GB/s (read + write)"
         cpu = None
     traffic = traffic_from_profiles(r["kernel"])
-    achieved = r["kernel_bytes"] / (r["kernel_ms"] * 1e-3) / 1e9
+    mfma = r.get("unit") == "TFLOP/s"
+    if mfma:
+        achieved = r["kernel_flops"] / (r["kernel_ms"] * 1e-3) / 1e12
+    else:
+        achieved = r["kernel_bytes"] / (r["kernel_ms"] * 1e-3) / 1e9
     line = {
         "metric": metric,
         "value": round(r["value"], 2),
-        "unit": "GB/s",
+        "unit": r.get("unit", "GB/s"),
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
@@ -384,20 +511,25 @@ def main():
         "data": "synthetic (include/apus_synth.h generator, seeded)",
         "config": r["config"],
         "roofline": {
-            "bound": "hbm",
+            "bound": "mfma" if mfma else "hbm",
             "kernel": r["kernel"],
             "achieved": round(achieved, 2),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "peak": BF16_PEAK_TFLOPS if mfma else HBM_PEAK_GBS,
+            "unit": "TFLOP/s" if mfma else "GB/s",
+            "frac": round(achieved / (BF16_PEAK_TFLOPS if mfma else HBM_PEAK_GBS), 4),
             "traffic": traffic,
             "algorithmic_bytes_per_launch": r["kernel_bytes"],
+            "algorithmic_flops_per_launch": r["kernel_flops"],
             "avg_launch_ms": round(r["kernel_ms"], 6),
             "launch_ms": r["launch_ms"],
             "mfma_tflops": round(r["kernel_flops"] / (r["kernel_ms"] * 1e-3) / 1e12, 3),
         },
         "cpu_baseline": cpu,
     }
+    if "hbm_gbs" in r:
+        line["hbm"] = {"achieved": round(r["hbm_gbs"], 2), "peak": HBM_PEAK_GBS,
+                       "unit": "GB/s", "frac": round(r["hbm_gbs"] / HBM_PEAK_GBS, 4),
+                       "algorithmic_bytes_per_step": r["bytes"]}
     print(json.dumps(line))
 
 
