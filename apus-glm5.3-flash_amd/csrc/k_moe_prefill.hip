@@ -187,6 +187,20 @@ __global__ __launch_bounds__(1024) void k_pf_scatter(
 /* grouped GEMM                                                             */
 /* ------------------------------------------------------------------------ */
 
+/* SwiGLU of the prefill epilogue: the clamp order and bf16 roundings of
+ * c/gmoe.h:217-225 with the numpy-stable sigmoid (c/gmhc.h:157-160) on the
+ * hardware exp2 and reciprocal (a few f32 ulps, far below the bf16 step
+ * that follows; a tolerance-class result like every GEMM output). */
+__device__ __forceinline__ uint32_t pf_swiglu(float g, float u, float limit) {
+    if (g > limit) g = limit;
+    if (u > limit) u = limit;
+    else if (u < -limit) u = -limit;
+    const float e = __expf(-fabsf(g));
+    const float r = __frcp_rn(1.0f + e);
+    const float sg = g >= 0.0f ? r : e * r;
+    return ghip_bf16_bits(ghip_bf16_round(g * sg) * u);
+}
+
 /* 8 codes (two dwords) -> one bf16x8 MFMA operand. */
 template <bool EXACT>
 __device__ __forceinline__ ghip_bf16x8 pf_deq8(uint32_t d0, uint32_t d1, float s) {
@@ -380,7 +394,7 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds) {
                 if (MODE == 0) {
                     const float g = ghip_bf16_round(a0[rb][i]);
                     const float u = ghip_bf16_round(a1[rb][i]);
-                    o[c0] = (uint16_t)ghip_swiglu(g, u, t.limit);
+                    o[c0] = (uint16_t)pf_swiglu(g, u, t.limit);
                 } else {
                     o[c0] = (uint16_t)ghip_bf16_bits(a0[rb][i]);
                     o[c1] = (uint16_t)ghip_bf16_bits(a1[rb][i]);
