@@ -49,6 +49,7 @@ typedef struct {
 
 static struct {
     int inited, enabled, device;
+    uint32_t n_cu;               /* CU count rounded up to the 8 XCDs */
     hipStream_t stream;
     /* grow-only staging (device) */
     void *d_w, *d_s, *d_x, *d_y;
@@ -127,6 +128,14 @@ static int ghip_init(void) {
     }
     HIPCHK(hipSetDevice(dev));
     HIPCHK(hipStreamCreate(&G.stream));
+    int ncu = 0;
+    HIPCHK(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev));
+    if (ncu <= 0) {
+        ghip_seterr("device %d reports no compute units", dev);
+        return 1;
+    }
+    G.n_cu = (uint32_t)((ncu + 7) / 8 * 8);
+    HIPCHK(ghip_moe_decode_init());
     HIPCHK(hipMalloc((void **)&G.d_flag, 256));
     HIPCHK(hipMalloc((void **)&G.d_flags, GHIP_SCAN_SLOTS * sizeof(uint32_t)));
     HIPCHK(hipMemset(G.d_flags, 0, GHIP_SCAN_SLOTS * sizeof(uint32_t)));
@@ -551,6 +560,7 @@ int apus_ghip_store_open(ApusGhipStore **out, int n_experts, size_t dim,
            || hipMemset(s->ws.route, 0, GHIP_MOE_ROUTE_WORDS * 4) != hipSuccess
            || hipMalloc((void **)&s->ws.err, 4) != hipSuccess
            || hipMemset(s->ws.err, 0, 4) != hipSuccess
+           || (s->ws.n_cu = G.n_cu) == 0
            || hipMalloc((void **)&s->ws.h, GHIP_MAX_TOPK * inter * 2) != hipSuccess
            || hipMalloc((void **)&s->d_x, dim * 2) != hipSuccess
            || hipMalloc((void **)&s->d_out, dim * 2) != hipSuccess
@@ -752,7 +762,7 @@ int apus_ghip_moe_decode_dev(ApusGhipStore *s, const uint16_t *x,
     store_bank(s, &bk);
     hipError_t e = ghip_launch_moe_decode(&bk, x, logits, idx, w, topk,
                                           s->limit, out, &s->ws,
-                                          G.trace_n >= 6 ? G.trace_ev : NULL,
+                                          G.trace_n >= 4 ? G.trace_ev : NULL,
                                           (hipStream_t)stream);
     if (e != hipSuccess) {
         ghip_seterr("moe_decode launch: %s", hipGetErrorString(e));
@@ -817,11 +827,7 @@ int apus_ghip_moe_prefill_reserve(const ApusGhipStore *s, size_t tokens,
     }
     if (!G.pf_inited) {
         HIPCHK(ghip_moe_prefill_init());
-        int ncu = 0;
-        HIPCHK(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount,
-                                     G.device));
-        if (ncu <= 0) { ghip_seterr("moe_prefill: no compute units"); return 1; }
-        G.pf.n_cu = (uint32_t)((ncu + 7) / 8 * 8);
+        G.pf.n_cu = G.n_cu;
         G.pf_inited = 1;
     }
     const size_t P = tokens * (size_t)topk;

@@ -236,6 +236,36 @@ __device__ __forceinline__ void ghip_wcopy(uint16_t *dst, const uint16_t *src,
     __builtin_amdgcn_wave_barrier();
 }
 
+/* ---- direct global -> LDS loads (gfx950 global_load_lds_dwordx4) -------
+ * Lane l of the wave writes its 16 bytes to lds_wave + 16*l, bypassing
+ * registers; completion is tracked by vmcnt like any vector load. */
+typedef __attribute__((address_space(3))) void ghip_lds_t;
+typedef __attribute__((address_space(1))) void ghip_glb_t;
+__device__ __forceinline__ void ghip_dma16(const void *src, void *lds_wave) {
+    __builtin_amdgcn_global_load_lds((ghip_glb_t *)src, (ghip_lds_t *)lds_wave, 16, 0, 0);
+}
+
+/* s_waitcnt vmcnt(N), other counters untouched. */
+#define GHIP_VMCNT(N) __builtin_amdgcn_s_waitcnt(((N) & 15) | (((N) >> 4) << 14) | 0x0F70)
+
+/* vmcnt(LPS * min(m, M)): wait until at most min(m, M) stages of LPS loads
+ * each are still in flight (m wave-uniform). */
+template <uint32_t LPS, uint32_t M>
+__device__ __forceinline__ void ghip_wait_stages(uint32_t m) {
+    if constexpr (M == 0) {
+        GHIP_VMCNT(0);
+    } else {
+        if (m >= M) GHIP_VMCNT(LPS * M);
+        else ghip_wait_stages<LPS, M - 1>(m);
+    }
+}
+
+/* Wave-uniform F32 read through the constant address space: a scalar load
+ * (lgkmcnt), so it never waits behind a stream of vector loads. */
+__device__ __forceinline__ float ghip_sload(const float *p, uint32_t i) {
+    return ((const __attribute__((address_space(4))) float *)p)[i];
+}
+
 /* numpy-stable sigmoid (c/gmhc.h:157-160) with the device expf. */
 __device__ __forceinline__ float ghip_sigmoid_np(float x) {
     float e = expf(-fabsf(x));

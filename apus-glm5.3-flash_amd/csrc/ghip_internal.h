@@ -46,7 +46,11 @@ typedef struct {
     uint32_t *route;      /* device, GHIP_MOE_ROUTE_WORDS u32 */
     uint16_t *h;          /* device [max topk, inter] bf16 */
     uint32_t *err;        /* device u32: nonzero after an invalid expert id */
+    uint32_t n_cu;        /* persistent grid bound: the device's CU count */
 } GhipMoeDecodeWs;
+
+/* Raise the decode kernels' dynamic-LDS limit (once per process). */
+hipError_t ghip_moe_decode_init(void);
 
 #define GHIP_MOE_ROUTE_WORDS 64
 
@@ -60,8 +64,8 @@ typedef struct {
     const uint32_t *nan_flags;   /* device [n_experts] u32 or NULL */
 } GhipBank;
 
-/* K3: routed MoE decode for one token (routing, gate/up + SwiGLU, down +
- * ordered combine: three launches on st). Either logits (device f32
+/* K3: routed MoE decode for one token (routing + gate/up + SwiGLU, down +
+ * ordered combine: two launches on st; ev: NULL or 4 events timing them). Either logits (device f32
  * [n_experts]; top-k + softmax on the device) or idx/w (device [topk]) must
  * be given. out: device [dim] bf16. */
 hipError_t ghip_launch_moe_decode(const GhipBank *bank, const uint16_t *x,

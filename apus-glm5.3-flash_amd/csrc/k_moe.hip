@@ -1,31 +1,31 @@
 /*
- * k_moe.hip — K3: routed-MoE decode for one token (gfx950), three launches
- * on one stream, no inter-workgroup waits:
+ * k_moe.hip — K3: routed-MoE decode for one token (gfx950), two launches on
+ * one stream, no inter-workgroup waits:
  *
- *   k_moe_route   one wave: routing -> workspace (nsel, expert ids ascending,
- *                 weights). Either the harness routing on the device (stable
- *                 top-k of f32 logits, ties -> lower id, softmax over the k
- *                 selected) or given idx/w, deduplicated keeping the first
- *                 slot of a repeated id (c/gmoe.h:309-312) and sorted by id.
- *   k_moe_gateup  one workgroup per (slot q, 16 rows): g and u GEMVs over
- *                 dim with the FP8 dequant fused (bit-exact weights), the
- *                 SwiGLU epilogue of c/gmoe.h:217-225 -> h[q] (bf16).
+ *   k_moe_gateup  routing first (one wave per workgroup: the harness
+ *                 routing -- stable top-k of f32 logits, ties -> lower id,
+ *                 softmax over the k selected -- or given idx/w,
+ *                 deduplicated keeping the first slot of a repeated id,
+ *                 c/gmoe.h:309-312, sorted by id; workgroup 0 publishes the
+ *                 record), then per (slot q, 16 rows) the g and u GEMVs
+ *                 over dim with the FP8 dequant fused (bit-exact weights)
+ *                 and the SwiGLU epilogue of c/gmoe.h:217-225 -> h[q].
  *   k_moe_down    one workgroup per 16 output rows: wave q computes expert
  *                 q's down GEMV (h[q] . Wd^T, full inter in-wave), then the
  *                 ascending-expert combine y = bf16(y + bf16(bf16(o)*w))
- *                 (c/gmoe.h:307-320) runs in-workgroup — no atomics, no
+ *                 (c/gmoe.h:307-320) runs in-workgroup -- no atomics, no
  *                 cross-workgroup reduction, deterministic.
  *
  * A single persistent launch with completion counters was tried first: its
  * agent-scope release/acquire fences (an L2 write-back / invalidate per wave
- * per tile) cost ~10x the weight streaming, so the phases are split at
- * kernel boundaries, which order the h and routing handoffs for free.
+ * per tile) cost ~10x the weight streaming, so the phases are split at a
+ * kernel boundary, which orders the h and routing handoff for free.
  *
- * GEMV inner loop (ghip_chunk_*, as k_linear.hip): 16 rows per MFMA group,
- * 128-wide k chunks (one scale block, two 16-byte code loads per lane, full
- * 128-byte lines per wave), dequant in registers, x (or h) as the A operand
- * from LDS; weight loads are issued before the activation is staged so the
- * two latencies overlap.
+ * Weight streaming: each wave pulls its 16-row chunks (128-wide k, one
+ * scale block) through a wave-private LDS ring with direct global->LDS
+ * loads, so the bytes in flight are not bounded by registers; the GEMV
+ * inner step (ghip_chunk_mfma) dequantizes in registers and reduces over k
+ * on MFMA with the activation (x or h) from LDS as the A operand.
  */
 #include "ghip_device.h"
 #include "ghip_internal.h"
@@ -33,7 +33,7 @@
 #define MD_NW 8                  /* waves per workgroup */
 #define MD_T 16                  /* rows per tile (one MFMA group) */
 #define MD_MAXK 16               /* max routed slots */
-#define MD_LOADS 16              /* 16-byte loads in flight per lane */
+#define MD_LDS_MAX (144 * 1024)  /* dynamic LDS limit set for both GEMV kernels */
 
 /* routing workspace (u32 words): [0] nsel, [1..16] ids, [17..32] weights */
 #define RT_NSEL 0
@@ -66,15 +66,19 @@ __device__ __forceinline__ uint64_t rt_wave_max(uint64_t k) {
     return k;
 }
 
-/* One wave. Logits live in registers (RT_REG per lane); each of the k
- * rounds takes the lane-local best key and one 64-bit wave max. */
-__global__ __launch_bounds__(64) void k_moe_route(
-    const float *__restrict__ logits, const int32_t *__restrict__ idx,
-    const float *__restrict__ w, int topk, int E, uint32_t *__restrict__ route,
-    uint32_t *__restrict__ err) {
-    __shared__ int32_t te[MD_MAXK];
-    __shared__ float tw[MD_MAXK];
-    const int lane = threadIdx.x;
+/* Routing by one wave into rt[] (an LDS route record: RT_NSEL, RT_IDS,
+ * RT_W words). Either the harness routing (stable top-k of f32 logits,
+ * ties -> lower id, softmax over the k selected, in slot order) or given
+ * idx/w; a repeated id keeps its first slot (c/gmoe.h:309-312), kept slots
+ * are placed by ascending expert id (the combine order). Logits live in
+ * registers (RT_REG per lane); each of the k rounds takes the lane-local
+ * best key and one 64-bit wave max. */
+__device__ __forceinline__ void md_route(const float *__restrict__ logits,
+                                         const int32_t *__restrict__ idx,
+                                         const float *__restrict__ w, int topk, int E,
+                                         uint32_t *rt, int32_t *te, float *tw,
+                                         uint32_t *__restrict__ err) {
+    const int lane = threadIdx.x & 63;
     if (logits) {
         uint64_t key[RT_REG];
 #pragma unroll
@@ -110,14 +114,15 @@ __global__ __launch_bounds__(64) void k_moe_route(
         te[lane] = idx[lane];
         tw[lane] = w[lane];
     }
-    __syncthreads();
-    /* lane j < topk owns slot j: dropped if its id repeats an earlier slot
-     * (first-match slot, c/gmoe.h:309-312) or is out of range; kept slots
-     * are placed by ascending expert id (the combine order). */
+    __builtin_amdgcn_s_waitcnt(0xc07f);           /* lgkmcnt(0) */
+    __builtin_amdgcn_wave_barrier();
     const int e = lane < topk ? te[lane] : -1;
     const float wj = lane < topk ? tw[lane] : 0.0f;
     bool keep = lane < topk;
-    if (keep && (e < 0 || e >= E)) { keep = false; atomicOr(err, 2u); }
+    if (keep && (e < 0 || e >= E)) {
+        keep = false;
+        if (err) atomicOr(err, 2u);
+    }
     for (int q = 0; q < MD_MAXK; q++) {
         const int eq = __shfl(e, q, 64);
         if (q < lane && q < topk && eq == e) keep = false;
@@ -129,103 +134,163 @@ __global__ __launch_bounds__(64) void k_moe_route(
         pos += (kq && eq < e);
     }
     const uint64_t kept = __ballot(keep);
-    if (keep) {
-        route[RT_IDS + pos] = (uint32_t)e;
-        route[RT_W + pos] = __float_as_uint(wj);
-    }
     const uint32_t nsel = (uint32_t)__popcll(kept);
-    if (lane == 0) route[RT_NSEL] = nsel;
-    if (lane >= (int)nsel && lane < MD_MAXK) {
-        route[RT_IDS + lane] = 0u;
-        route[RT_W + lane] = 0u;
+    if (lane < MD_MAXK) {                 /* clear, then place kept slots */
+        rt[RT_IDS + lane] = 0u;
+        rt[RT_W + lane] = 0u;
     }
+    __builtin_amdgcn_wave_barrier();
+    if (keep) {
+        rt[RT_IDS + pos] = (uint32_t)e;
+        rt[RT_W + pos] = __float_as_uint(wj);
+    }
+    if (lane == 0) rt[RT_NSEL] = nsel;
+    __builtin_amdgcn_s_waitcnt(0xc07f);           /* lgkmcnt(0) */
+    __builtin_amdgcn_wave_barrier();
+}
+
+/* ------------------------------------------------------------------------ */
+/* weight streaming (both GEMV kernels)                                     */
+/* ------------------------------------------------------------------------ */
+
+/* A chunk (16 weight rows x 128 codes = 2 KB, one scale block) lives in
+ * LDS as [16 rows][8 pieces of 16 B] with piece p of row r at
+ * (p ^ ((r >> 1) & 7)), so the MFMA-layout reads (lane 16g + n: row n,
+ * pieces 2g and 2g+1) hit distinct banks. Two DMA instructions fill it:
+ * instruction i, lane l -> row 8i + l/8, stored slot l % 8. */
+struct MdDma {
+    uint32_t off0, off1;          /* global byte offsets (row * K + piece) */
+};
+
+__device__ __forceinline__ MdDma md_dma_offsets(uint32_t lane, uint32_t K) {
+    MdDma d;
+    const uint32_t r0 = lane >> 3, r1 = 8 + (lane >> 3);
+    d.off0 = r0 * K + 16u * ((lane & 7u) ^ ((r0 >> 1) & 7u));
+    d.off1 = r1 * K + 16u * ((lane & 7u) ^ ((r1 >> 1) & 7u));
+    return d;
+}
+
+/* chunk c of the 16 rows at `rows` (row stride K) -> LDS chunk buffer */
+__device__ __forceinline__ void md_issue_chunk(const uint8_t *rows, uint32_t c,
+                                               const MdDma &d, uint8_t *buf) {
+    ghip_dma16(rows + (size_t)c * 128u + d.off0, buf);
+    ghip_dma16(rows + (size_t)c * 128u + d.off1, buf + 1024);
+}
+
+/* this lane's 32 codes of a chunk in LDS (row n, pieces 2g, 2g+1) */
+__device__ __forceinline__ ghip_chunk md_read_chunk(const uint8_t *buf, uint32_t n,
+                                                    uint32_t g) {
+    const uint32_t sw = (n >> 1) & 7u;
+    ghip_chunk c;
+    c.lo = *(const ghip_u32x4 *)(buf + n * 128u + 16u * ((2u * g) ^ sw));
+    c.hi = *(const ghip_u32x4 *)(buf + n * 128u + 16u * ((2u * g + 1u) ^ sw));
+    return c;
 }
 
 /* ------------------------------------------------------------------------ */
 /* gate/up + SwiGLU                                                         */
 /* ------------------------------------------------------------------------ */
 
-#define GU_U 4                   /* chunks per matrix per batch (16 loads) */
+#define GU_NW 8                  /* waves per workgroup (two per SIMD) */
+#define GU_IPW 4                 /* items per workgroup pass (2 waves each) */
+#define GU_R 4                   /* ring stages per wave (gate + up chunk) */
+#define GU_STG 4096              /* bytes per stage */
 
-/* buf / scg / scu hold the first batch on entry (issued before x was
- * staged) and are refilled in place, so one set of registers streams. */
-template <bool EXACT>
-__device__ __forceinline__ void gateup_tile(const uint8_t *wg, const uint8_t *wu,
-                                            const float *sg, const float *su,
-                                            const uint16_t *xa, uint32_t nch,
-                                            uint32_t wv, ghip_chunk (&buf)[2 * GU_U],
-                                            float (&scg)[GU_U], float (&scu)[GU_U],
-                                            ghip_f32x4 &ag, ghip_f32x4 &au) {
-    for (uint32_t c0 = wv; c0 < nch; c0 += MD_NW * GU_U) {
-        if (c0 != wv) {
-#pragma unroll
-            for (int u = 0; u < GU_U; u++) {
-                uint32_t c = min(c0 + u * MD_NW, nch - 1u);
-                buf[2 * u] = ghip_chunk_load(wg + (size_t)c * 128);
-                buf[2 * u + 1] = ghip_chunk_load(wu + (size_t)c * 128);
-                scg[u] = sg[c];
-                scu[u] = su[c];
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < GU_U; u++) {
-            uint32_t c = c0 + u * MD_NW;
-            if (c < nch) {
-                ghip_chunk_mfma<EXACT>(buf[2 * u], scg[u], xa + c * 128, ag);
-                ghip_chunk_mfma<EXACT>(buf[2 * u + 1], scu[u], xa + c * 128, au);
-            }
-        }
-    }
-}
-
-__global__ __launch_bounds__(MD_NW * 64, 2) void k_moe_gateup(
-    GhipBank bank, const uint16_t *__restrict__ x, const uint32_t *__restrict__ route,
-    float limit, uint16_t *__restrict__ h) {
-    extern __shared__ __align__(16) uint16_t xs[];      /* x [dim] */
-    __shared__ float red[2][MD_NW][16];
+/* Routing first (wave 0; workgroup 0 publishes the record for the down
+ * launch), then items = (slot q, 16 rows): gate and up GEMVs over dim and
+ * the SwiGLU -> h[q]. Persistent: workgroup b takes item groups b, b + G,
+ * ... of GU_IPW items; wave w streams item (w / 2)'s half (w % 2) of K
+ * through a wave-private GU_R-stage LDS ring filled by direct DMA (no
+ * registers hold loads in flight, no barriers inside the stream); the two
+ * halves are summed in LDS in a fixed order (deterministic). x is staged
+ * once per workgroup. */
+__global__ __launch_bounds__(GU_NW * 64, 1) void k_moe_gateup(
+    GhipBank bank, const uint16_t *__restrict__ x, const float *__restrict__ logits,
+    const int32_t *__restrict__ idx, const float *__restrict__ w, int topk,
+    float limit, uint16_t *__restrict__ h, uint32_t *__restrict__ route_out,
+    uint32_t *__restrict__ err) {
+    extern __shared__ __attribute__((aligned(1024))) uint8_t gl[];
+    __shared__ uint32_t rt[GHIP_MOE_ROUTE_WORDS];
+    __shared__ int32_t te[MD_MAXK];
+    __shared__ float tw[MD_MAXK];
+    __shared__ float red[GU_IPW][2][2][16];
+    const uint32_t dim = bank.dim, inter = bank.inter;
+    uint16_t *xs = (uint16_t *)gl;
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t n = lane & 15u, g = lane >> 4;
-    const uint32_t dim = bank.dim, inter = bank.inter;
-    const uint32_t tiles = inter / MD_T;
-    const uint32_t q = blockIdx.x / tiles, r0 = (blockIdx.x - q * tiles) * MD_T;
-    const uint32_t nsel = __builtin_amdgcn_readfirstlane(route[RT_NSEL]);
-    if (q >= nsel) return;
-    const uint32_t e = __builtin_amdgcn_readfirstlane(route[RT_IDS + q]);
-    const uint8_t *slab = bank.base + (size_t)e * bank.stride;
-    const bool exact = bank.nan_flags && bank.nan_flags[e];
-    const uint8_t *wg = slab + bank.off_gw + (size_t)(r0 + n) * dim + 32u * g;
-    const uint8_t *wu = slab + bank.off_uw + (size_t)(r0 + n) * dim + 32u * g;
-    const uint32_t nkb = dim >> 7;
-    const float *sg = (const float *)(slab + bank.off_gs) + (size_t)(r0 >> 7) * nkb;
-    const float *su = (const float *)(slab + bank.off_us) + (size_t)(r0 >> 7) * nkb;
-    const uint32_t nch = dim >> 7;
-    /* this wave's x slices first, then the first batch of weights, then
-     * the slices into LDS (wave-local: no workgroup barrier) */
-    ghip_stage stx;
-    ghip_wstage_load(stx, x, 1u, dim, nch, wv, MD_NW, lane);
-    ghip_chunk pre[2 * GU_U];
-    float scg[GU_U], scu[GU_U];
-#pragma unroll
-    for (int u = 0; u < GU_U; u++) {
-        uint32_t c = min(wv + u * MD_NW, nch - 1u);     /* unconditional */
-        pre[2 * u] = ghip_chunk_load(wg + (size_t)c * 128);
-        pre[2 * u + 1] = ghip_chunk_load(wu + (size_t)c * 128);
-        scg[u] = sg[c];
-        scu[u] = su[c];
-    }
-    ghip_wstage_store(stx, xs, x, 1u, dim, nch, wv, MD_NW, lane);
-    ghip_f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
-    if (exact) gateup_tile<true>(wg, wu, sg, su, xs + 32u * g, nch, wv, pre, scg, scu, ag, au);
-    else gateup_tile<false>(wg, wu, sg, su, xs + 32u * g, nch, wv, pre, scg, scu, ag, au);
-    if (g == 0) { red[0][wv][n] = ag[0]; red[1][wv][n] = au[0]; }
+    if (wv == 0)
+        md_route(logits, idx, w, topk, (int)bank.n_experts, rt, te, tw,
+                 blockIdx.x == 0 ? err : nullptr);
+    for (uint32_t i = tid; i < (dim >> 3); i += GU_NW * 64)
+        ((ghip_u32x4 *)xs)[i] = ((const ghip_u32x4 *)x)[i];
     __syncthreads();
-    if (tid < 16) {
-        float gs = 0.0f, us = 0.0f;
+    if (blockIdx.x == 0 && tid < GHIP_MOE_ROUTE_WORDS) route_out[tid] = rt[tid];
+    const uint32_t nsel = __builtin_amdgcn_readfirstlane(rt[RT_NSEL]);
+    const uint32_t tiles = inter / MD_T, items = nsel * tiles;
+    const uint32_t groups = (items + GU_IPW - 1) / GU_IPW;
+    uint8_t *ring = gl + ((dim * 2u + 1023u) & ~1023u) + wv * (GU_R * GU_STG);
+    const uint32_t nch = dim >> 7, nkb = dim >> 7;
+    const uint32_t half = wv & 1u, slot = wv >> 1;
+    const uint32_t c0 = half ? nch / 2 : 0u, c1 = half ? nch : nch / 2;
+    const uint32_t nc = c1 - c0;
+    const MdDma d = md_dma_offsets(lane, dim);
+    const uint32_t n = lane & 15u, g = lane >> 4;
+
+    for (uint32_t grp = blockIdx.x; grp < groups; grp += gridDim.x) {
+        const uint32_t it = grp * GU_IPW + slot;
+        const bool live = it < items;
+        uint32_t q = 0, r0 = 0;
+        if (live) {
+            q = it / tiles;
+            r0 = (it - q * tiles) * MD_T;
+            const uint32_t e = __builtin_amdgcn_readfirstlane(rt[RT_IDS + q]);
+            const uint8_t *slab = bank.base + (size_t)e * bank.stride;
+            const uint8_t *wg = slab + bank.off_gw + (size_t)r0 * dim;
+            const uint8_t *wu = slab + bank.off_uw + (size_t)r0 * dim;
+            const float *sg = (const float *)(slab + bank.off_gs) + (size_t)(r0 >> 7) * nkb;
+            const float *su = (const float *)(slab + bank.off_us) + (size_t)(r0 >> 7) * nkb;
+            const bool exact = bank.nan_flags && bank.nan_flags[e];
+            auto issue = [&](uint32_t t) {
+                uint8_t *buf = ring + (t % GU_R) * GU_STG;
+                md_issue_chunk(wg, c0 + t, d, buf);
+                md_issue_chunk(wu, c0 + t, d, buf + 2048);
+            };
 #pragma unroll
-        for (int w2 = 0; w2 < MD_NW; w2++) { gs += red[0][w2][tid]; us += red[1][w2][tid]; }
-        h[(size_t)q * inter + r0 + tid] =
-            (uint16_t)ghip_swiglu(ghip_bf16_round(gs), ghip_bf16_round(us), limit);
+            for (uint32_t i = 0; i + 1 < GU_R; i++)
+                if (i < nc) issue(i);
+            ghip_f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
+            for (uint32_t t = 0; t < nc; t++) {
+                /* own DMA of stage t landed; stage t-1's buffer is free
+                 * (its reads fed stage t-1's MFMAs) */
+                ghip_wait_stages<4, GU_R - 2>(nc - 1 - t);
+                if (t + GU_R - 1 < nc) issue(t + GU_R - 1);
+                const uint8_t *buf = ring + (t % GU_R) * GU_STG;
+                const ghip_chunk cg = md_read_chunk(buf, n, g);
+                const ghip_chunk cu = md_read_chunk(buf + 2048, n, g);
+                const uint32_t c = c0 + t;
+                const float scg = ghip_sload(sg, c), scu = ghip_sload(su, c);
+                const uint16_t *xa = xs + c * 128u + 32u * g;
+                if (exact) {
+                    ghip_chunk_mfma<true>(cg, scg, xa, ag);
+                    ghip_chunk_mfma<true>(cu, scu, xa, au);
+                } else {
+                    ghip_chunk_mfma<false>(cg, scg, xa, ag);
+                    ghip_chunk_mfma<false>(cu, scu, xa, au);
+                }
+            }
+            if (g == 0) {
+                red[slot][half][0][n] = ag[0];
+                red[slot][half][1][n] = au[0];
+            }
+        }
+        __syncthreads();
+        if (live && half == 0 && lane < 16) {     /* fixed order: half 0 + half 1 */
+            const float gs = red[slot][0][0][lane] + red[slot][1][0][lane];
+            const float us = red[slot][0][1][lane] + red[slot][1][1][lane];
+            h[(size_t)q * inter + r0 + lane] = (uint16_t)ghip_swiglu(
+                ghip_bf16_round(gs), ghip_bf16_round(us), limit);
+        }
+        __syncthreads();
     }
 }
 
@@ -233,37 +298,19 @@ __global__ __launch_bounds__(MD_NW * 64, 2) void k_moe_gateup(
 /* down + ordered combine                                                   */
 /* ------------------------------------------------------------------------ */
 
-#define DN_U 8                   /* chunks in flight per lane (16 loads) */
+#define DN_R 6                   /* ring stages per wave (one chunk each) */
+#define DN_STG 2048
 
-/* buf / sc hold the first DN_U chunks on entry and are refilled in place. */
-template <bool EXACT>
-__device__ __forceinline__ ghip_f32x4 down_rows(const uint8_t *wr, const float *srow,
-                                                const uint16_t *ha, uint32_t nch,
-                                                ghip_chunk (&buf)[DN_U],
-                                                float (&sc)[DN_U]) {
-    ghip_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (uint32_t c0 = 0; c0 < nch; c0 += DN_U) {
-        if (c0 != 0) {
-#pragma unroll
-            for (int u = 0; u < DN_U; u++) {
-                uint32_t c = min(c0 + u, nch - 1u);
-                buf[u] = ghip_chunk_load(wr + (size_t)c * 128);
-                sc[u] = srow[c];
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < DN_U; u++) {
-            uint32_t c = c0 + u;
-            if (c < nch) ghip_chunk_mfma<EXACT>(buf[u], sc[u], ha + c * 128, acc);
-        }
-    }
-    return acc;
-}
-
-__global__ __launch_bounds__(MD_NW * 64, 2) void k_moe_down(
+/* One workgroup per 16 output rows; wave q streams expert slot q's 16 rows
+ * of Wd over inter through its own DN_R-stage DMA ring (h[q] staged into
+ * the wave's own LDS region as the A operand, restaged for a second slot
+ * q + 8), then the ascending-expert combine
+ * y = bf16(y + bf16(bf16(o) * w)) (c/gmoe.h:307-320) runs in-workgroup:
+ * no atomics, no cross-workgroup reduction, deterministic. */
+__global__ __launch_bounds__(MD_NW * 64, 1) void k_moe_down(
     GhipBank bank, const uint16_t *__restrict__ h, const uint32_t *__restrict__ route,
     uint16_t *__restrict__ out) {
-    extern __shared__ __align__(16) uint16_t hs[];      /* h [nsel][inter] */
+    extern __shared__ __attribute__((aligned(1024))) uint8_t dl[];
     __shared__ float oq[MD_MAXK][16];
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -271,51 +318,53 @@ __global__ __launch_bounds__(MD_NW * 64, 2) void k_moe_down(
     const uint32_t inter = bank.inter;
     const uint32_t r0 = blockIdx.x * MD_T;
     const uint32_t nsel = __builtin_amdgcn_readfirstlane(route[RT_NSEL]);
-    const uint32_t nch = inter >> 7;
-    const uint32_t nkb = inter >> 7;
-    /* this wave's h[q] first (wave-local), then its weights, then h[q]
-     * into LDS; a wave holds one expert's full K */
-    const uint32_t q0 = wv < nsel ? wv : 0u;
-    ghip_stage sth;
-    ghip_wstage_load(sth, h + (size_t)q0 * inter, 1u, inter, nch, 0u, 1u, lane);
-    ghip_chunk pre[DN_U];
-    float sc[DN_U];
-    {
-        /* unconditional (a wave without a slot reloads slot 0's rows and
-         * discards them) so the waitcnt pass sees a fixed load count */
-        const uint32_t e = __builtin_amdgcn_readfirstlane(
-            route[RT_IDS + (wv < nsel ? wv : 0u)]);
-        const uint8_t *slab = bank.base + (size_t)e * bank.stride;
-        const uint8_t *wr0 = slab + bank.off_dw + (size_t)(r0 + n) * inter + 32u * g;
-        const float *sr0 = (const float *)(slab + bank.off_ds) + (size_t)(r0 >> 7) * nkb;
-#pragma unroll
-        for (int u = 0; u < DN_U; u++) {
-            const uint32_t c = min((uint32_t)u, nch - 1u);
-            pre[u] = ghip_chunk_load(wr0 + (size_t)c * 128);
-            sc[u] = sr0[c];
-        }
-    }
-    ghip_wstage_store(sth, hs + (size_t)q0 * inter, h + (size_t)q0 * inter, 1u, inter,
-                      nch, 0u, 1u, lane);
-    for (uint32_t q = wv; q < nsel; q += MD_NW) {
+    const uint32_t nch = inter >> 7, nkb = inter >> 7;
+    uint16_t *hs = (uint16_t *)dl + (size_t)wv * inter;  /* this wave's h */
+    uint8_t *ring = dl + (size_t)MD_NW * inter * 2u + wv * (DN_R * DN_STG);
+    const MdDma d = md_dma_offsets(lane, inter);
+    const uint32_t T = nch * ((nsel > wv ? nsel - wv + MD_NW - 1 : 0u) / MD_NW);
+
+    auto slot_rows = [&](uint32_t k) {
+        const uint32_t q = wv + k * MD_NW;
         const uint32_t e = __builtin_amdgcn_readfirstlane(route[RT_IDS + q]);
-        const uint8_t *slab = bank.base + (size_t)e * bank.stride;
-        const uint8_t *wr = slab + bank.off_dw + (size_t)(r0 + n) * inter + 32u * g;
-        const float *srow = (const float *)(slab + bank.off_ds) + (size_t)(r0 >> 7) * nkb;
-        if (q != wv) {          /* second slot of this wave (topk > 8) */
+        return bank.base + (size_t)e * bank.stride + bank.off_dw + (size_t)r0 * inter;
+    };
+    auto issue = [&](uint32_t t) {
+        const uint32_t k = t / nch, c = t - k * nch;
+        md_issue_chunk(slot_rows(k), c, d, ring + (t % DN_R) * DN_STG);
+    };
+    /* h of the first slot before any DMA is in flight (its vector loads
+     * and the LDS writes wait with vmcnt / lgkmcnt of their own) */
+    if (wv < nsel) ghip_wcopy(hs, h + (size_t)wv * inter, inter >> 3, lane);
 #pragma unroll
-            for (int u = 0; u < DN_U; u++) {
-                const uint32_t c = min((uint32_t)u, nch - 1u);
-                pre[u] = ghip_chunk_load(wr + (size_t)c * 128);
-                sc[u] = srow[c];
-            }
-            ghip_wcopy(hs + (size_t)q * inter, h + (size_t)q * inter, inter >> 3, lane);
+    for (uint32_t i = 0; i + 1 < DN_R; i++)
+        if (i < T) issue(i);
+
+    ghip_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    const float *srow = nullptr;
+    bool exact = false;
+    for (uint32_t t = 0; t < T; t++) {
+        const uint32_t k = t / nch, c = t - k * nch, q = wv + k * MD_NW;
+        if (c == 0) {
+            const uint32_t e = __builtin_amdgcn_readfirstlane(route[RT_IDS + q]);
+            const uint8_t *slab = bank.base + (size_t)e * bank.stride;
+            srow = (const float *)(slab + bank.off_ds) + (size_t)(r0 >> 7) * nkb;
+            exact = bank.nan_flags && bank.nan_flags[e];
+            /* a second slot (topk > 8): restage; the copy's loads wait for
+             * the DMA already in flight, a bubble only for such routings */
+            if (k > 0) ghip_wcopy(hs, h + (size_t)q * inter, inter >> 3, lane);
         }
-        const bool exact = bank.nan_flags && bank.nan_flags[e];
-        const uint16_t *ha = hs + (size_t)q * inter + 32u * g;
-        ghip_f32x4 acc = exact ? down_rows<true>(wr, srow, ha, nch, pre, sc)
-                               : down_rows<false>(wr, srow, ha, nch, pre, sc);
-        if (g == 0) oq[q][n] = acc[0];
+        ghip_wait_stages<2, DN_R - 2>(T - 1 - t);
+        if (t + DN_R - 1 < T) issue(t + DN_R - 1);
+        const ghip_chunk cw = md_read_chunk(ring + (t % DN_R) * DN_STG, n, g);
+        const float sc = ghip_sload(srow, c);
+        const uint16_t *ha = hs + c * 128u + 32u * g;
+        if (exact) ghip_chunk_mfma<true>(cw, sc, ha, acc);
+        else ghip_chunk_mfma<false>(cw, sc, ha, acc);
+        if (c == nch - 1) {
+            if (g == 0) oq[q][n] = acc[0];
+            acc = (ghip_f32x4){0.f, 0.f, 0.f, 0.f};
+        }
     }
     __syncthreads();
     if (tid < 16) {
@@ -351,19 +400,28 @@ extern "C" hipError_t ghip_launch_moe_decode(const GhipBank *bank,
         || (bank->off_gw & 15) || (bank->off_uw & 15) || (bank->off_dw & 15)
         || (bank->off_gs & 3) || (bank->off_us & 3) || (bank->off_ds & 3))
         return hipErrorInvalidValue;
-    const size_t lds_gu = (size_t)dim * 2, lds_dn = (size_t)topk * inter * 2;
-    if (lds_gu > 64 * 1024 || lds_dn > 64 * 1024) return hipErrorInvalidValue;
+    const size_t lds_gu = (((size_t)dim * 2 + 1023) & ~(size_t)1023) + GU_NW * GU_R * GU_STG;
+    const size_t lds_dn = (size_t)MD_NW * inter * 2 + MD_NW * DN_R * DN_STG;
+    if (lds_gu > MD_LDS_MAX || lds_dn > MD_LDS_MAX || ws->n_cu == 0)
+        return hipErrorInvalidValue;
     hipEvent_t e0 = ev ? ev[0] : nullptr, e1 = ev ? ev[1] : nullptr;
     hipEvent_t e2 = ev ? ev[2] : nullptr, e3 = ev ? ev[3] : nullptr;
-    hipEvent_t e4 = ev ? ev[4] : nullptr, e5 = ev ? ev[5] : nullptr;
     hipError_t e;
-    GHIP_LAUNCH(e0, e1, k_moe_route, dim3(1), dim3(64), 0, st, logits, idx, w, topk,
-                (int)bank->n_experts, ws->route, ws->err);
+    uint32_t groups = ((uint32_t)topk * (inter / MD_T) + GU_IPW - 1) / GU_IPW;
+    if (groups > ws->n_cu) groups = ws->n_cu;             /* persistent */
+    GHIP_LAUNCH(e0, e1, k_moe_gateup, dim3(groups), dim3(GU_NW * 64), lds_gu, st, *bank,
+                x, logits, idx, w, topk, limit, ws->h, ws->route, ws->err);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    GHIP_LAUNCH(e2, e3, k_moe_gateup, dim3((uint32_t)topk * (inter / MD_T)),
-                dim3(MD_NW * 64), lds_gu, st, *bank, x, ws->route, limit, ws->h);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    GHIP_LAUNCH(e4, e5, k_moe_down, dim3(dim / MD_T), dim3(MD_NW * 64), lds_dn, st,
+    GHIP_LAUNCH(e2, e3, k_moe_down, dim3(dim / MD_T), dim3(MD_NW * 64), lds_dn, st,
                 *bank, ws->h, ws->route, out);
     return hipGetLastError();
+}
+
+extern "C" hipError_t ghip_moe_decode_init(void) {
+    hipError_t e = hipFuncSetAttribute((const void *)k_moe_gateup,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       MD_LDS_MAX);
+    if (e != hipSuccess) return e;
+    return hipFuncSetAttribute((const void *)k_moe_down,
+                               hipFuncAttributeMaxDynamicSharedMemorySize, MD_LDS_MAX);
 }

@@ -209,30 +209,6 @@ __device__ __forceinline__ ghip_bf16x8 pf_deq8(uint32_t d0, uint32_t d1, float s
     return __builtin_bit_cast(ghip_bf16x8, v);
 }
 
-typedef __attribute__((address_space(3))) void pf_lds_t;
-typedef __attribute__((address_space(1))) void pf_glb_t;
-
-/* 16 bytes global -> LDS, bypassing registers (gfx950
- * global_load_lds_dwordx4): lane l of the wave writes lds_wave + 16*l. */
-__device__ __forceinline__ void pf_dma16(const void *src, void *lds_wave) {
-    __builtin_amdgcn_global_load_lds((pf_glb_t *)src, (pf_lds_t *)lds_wave, 16, 0, 0);
-}
-
-/* s_waitcnt vmcnt(N), other counters untouched. */
-#define PF_VMCNT(N) __builtin_amdgcn_s_waitcnt(((N) & 15) | (((N) >> 4) << 14) | 0x0F70)
-
-/* s_waitcnt vmcnt(LPS * min(m, M)): wait until at most min(m, M) stages of
- * LPS loads each are still in flight (m wave-uniform). */
-template <uint32_t LPS, uint32_t M>
-__device__ __forceinline__ void pf_wait(uint32_t m) {
-    if constexpr (M == 0) {
-        PF_VMCNT(0);
-    } else {
-        if (m >= M) PF_VMCNT(LPS * M);
-        else pf_wait<LPS, M - 1>(m);
-    }
-}
-
 /* What one workgroup computes (see k_pf_gemm). */
 struct PfTile {
     const uint16_t *act;          /* activation matrix (x or H), K wide */
@@ -300,10 +276,10 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds) {
         uint8_t *st = lds + (j % NS) * STG;
 #pragma unroll
         for (int i = 0; i < NRB; i++)
-            pf_dma16(asrc[i] + (size_t)j * PF_BK * 2, st + (4 * i + wv) * 1024);
+            ghip_dma16(asrc[i] + (size_t)j * PF_BK * 2, st + (4 * i + wv) * 1024);
 #pragma unroll
         for (int i = 0; i < 4; i++)
-            pf_dma16(wsrc[i] + (size_t)j * PF_BK, st + ASTG + (4 * i + wv) * 1024);
+            ghip_dma16(wsrc[i] + (size_t)j * PF_BK, st + ASTG + (4 * i + wv) * 1024);
     };
 
     /* --- operand read offsets inside a stage --------------------------- */
@@ -333,7 +309,7 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds) {
          * wave is done reading buffer (j-1) % NS, refilled next. No fence:
          * a fence would drain the whole DMA stream at each stage. */
         const uint32_t later = nst - 1 - j;
-        pf_wait<LPS, NS - 2>(later);
+        ghip_wait_stages<LPS, NS - 2>(later);
         __builtin_amdgcn_s_barrier();
         if (j + NS - 1 < nst) issue(j + NS - 1);
         const uint8_t *st = lds + (j % NS) * STG;

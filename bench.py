@@ -84,13 +84,14 @@ MOE = dict(E=288, k=8, dim=4096, inter=2048, seed=0xC2, limit=10.0)
 
 def moe_algorithmic_bytes(E, k, dim, inter):
     """(step bytes, step flops, gate/up launch bytes). Step: k expert slabs
-    (FP8 codes + F32 block scales) + x + out + logits. Gate/up launch: the k
-    gate and up members + x + the k*inter BF16 h rows it writes."""
+    (FP8 codes + F32 block scales) + x + out + logits. Gate/up launch (it also
+    routes): the k gate and up members + x + logits + the k*inter BF16 h
+    rows it writes."""
     nb = lambda n: (n + 127) // 128  # noqa: E731
     gu = 2 * (inter * dim + nb(inter) * nb(dim) * 4)
     slab = gu + dim * inter + nb(dim) * nb(inter) * 4
     return (k * slab + dim * 2 + dim * 2 + E * 4, 2 * k * 3 * inter * dim,
-            k * gu + dim * 2 + k * inter * 2)
+            k * gu + dim * 2 + E * 4 + k * inter * 2)
 
 
 def bench_moe_decode(lib, pkg, rt, steps, warmup, rotate=64):
@@ -133,9 +134,8 @@ def bench_moe_decode(lib, pkg, rt, steps, warmup, rotate=64):
     e1.synchronize()
     wall = time.perf_counter() - t0
     ms = e0.elapsed_ms(e1) / steps
-    kt = kernel_times(lib, rt, step, warmup + steps, steps, 6,
-                      {"k_moe_route": (0, 1), "k_moe_gateup": (2, 3),
-                       "k_moe_down": (4, 5)})
+    kt = kernel_times(lib, rt, step, warmup + steps, steps, 4,
+                      {"k_moe_gateup": (0, 1), "k_moe_down": (2, 3)})
     nbytes, flops, gu_bytes = moe_algorithmic_bytes(E, k, dim, inter)
     gbs = nbytes / (ms * 1e-3) / 1e9
     lib.apus_ghip_store_close(store)

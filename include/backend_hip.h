@@ -173,10 +173,10 @@ int apus_ghip_store_expert_bf16(ApusGhipStore *s, int expert,
                                 uint16_t *payload);
 
 /* --- routed MoE decode (one token): SwiGLU experts + ordered combine,
- * c/gmoe.h:210-227 + 307-320 without the router and shared expert. Three
- * stream-ordered launches, each grouped over all routed experts: routing,
- * gate/up GEMVs with the SwiGLU epilogue, down GEMVs with the
- * ascending-expert bf16-per-add combine.
+ * c/gmoe.h:210-227 + 307-320 without the router and shared expert. Two
+ * stream-ordered launches, each grouped over all routed experts: routing
+ * with the gate/up GEMVs and their SwiGLU epilogue, then the down GEMVs
+ * with the ascending-expert bf16-per-add combine.
  * Routing either given (idx/w [topk]) or computed on the device from
  * logits [n_experts] f32: stable top-k (ties -> lower id), w = softmax over
  * the k selected logits. Host-pointer variant is synchronous. */
@@ -216,8 +216,8 @@ int apus_ghip_moe_prefill_dev(ApusGhipStore *s, const uint16_t *x, size_t T,
  * events: n caller-created hipEvent_t handles, NULL/0 turns it off. While
  * set, launches carry start/stop events in their dispatch packets
  * (hipExtLaunchKernelGGL), so an event pair spans exactly one kernel:
- * apus_ghip_moe_decode_dev (n >= 6) times routing with events[0..1], the
- * gate/up launch with events[2..3] and the down launch with events[4..5];
+ * apus_ghip_moe_decode_dev (n >= 4) times the routing + gate/up launch
+ * with events[0..1] and the down launch with events[2..3];
  * apus_ghip_fp8blk_linear_dev (n >= 2) starts events[0] with its first
  * GEMV launch and stops events[1] with its last; apus_ghip_moe_prefill_dev
  * (n >= 8) times the permutation with events[0..1], the gate/up GEMM with
