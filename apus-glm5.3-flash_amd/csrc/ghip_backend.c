@@ -503,6 +503,7 @@ struct ApusGhipStore {
     uint8_t *arena;
     uint32_t *nan_flags;                 /* device [n_experts] */
     GhipMoeDecodeWs ws;
+    uint64_t epoch;                      /* fused decode launches (ws.epoch) */
     /* decode staging for the host-pointer entry */
     uint16_t *d_x, *d_out;
     int32_t *d_idx;
@@ -561,6 +562,9 @@ int apus_ghip_store_open(ApusGhipStore **out, int n_experts, size_t dim,
            || hipMalloc((void **)&s->ws.err, 4) != hipSuccess
            || hipMemset(s->ws.err, 0, 4) != hipSuccess
            || (s->ws.n_cu = G.n_cu) == 0
+           || hipMalloc((void **)&s->ws.sync, 4) != hipSuccess
+           || hipMemset(s->ws.sync, 0, 4) != hipSuccess
+           || (s->ws.epoch = &s->epoch) == NULL
            || hipMalloc((void **)&s->ws.h, GHIP_MAX_TOPK * inter * 2) != hipSuccess
            || hipMalloc((void **)&s->d_x, dim * 2) != hipSuccess
            || hipMalloc((void **)&s->d_out, dim * 2) != hipSuccess
@@ -583,6 +587,7 @@ void apus_ghip_store_close(ApusGhipStore *s) {
     hipFree(s->nan_flags);
     hipFree(s->ws.route);
     hipFree(s->ws.err);
+    hipFree(s->ws.sync);
     hipFree(s->ws.h);
     hipFree(s->d_x);
     hipFree(s->d_out);
@@ -795,7 +800,8 @@ int apus_ghip_moe_decode(ApusGhipStore *s, const uint16_t *x,
     uint32_t err = 0;
     HIPCHK(hipMemcpy(&err, s->ws.err, 4, hipMemcpyDeviceToHost));
     if (err) {
-        ghip_seterr("moe_decode: invalid expert id in routing (code %u)", err);
+        ghip_seterr(err & 4u ? "moe_decode: device-wide phase wait timed out (code %u)"
+                             : "moe_decode: invalid expert id in routing (code %u)", err);
         hipMemset(s->ws.err, 0, 4);
         return 1;
     }

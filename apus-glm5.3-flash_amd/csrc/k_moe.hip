@@ -56,14 +56,29 @@ __device__ __forceinline__ uint64_t rt_key(float v, int i) {
     return ((uint64_t)u << 32) | (uint32_t)(0xffffffffu - (uint32_t)i);
 }
 
+/* k = max(k, k moved by a DPP pattern); lanes without a source keep k */
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ uint64_t rt_dpp_max(uint64_t k) {
+    const int lo = (int)(uint32_t)k, hi = (int)(uint32_t)(k >> 32);
+    const uint32_t olo = (uint32_t)__builtin_amdgcn_update_dpp(lo, lo, CTRL, ROWMASK, 0xf, false);
+    const uint32_t ohi = (uint32_t)__builtin_amdgcn_update_dpp(hi, hi, CTRL, ROWMASK, 0xf, false);
+    const uint64_t o = ((uint64_t)ohi << 32) | olo;
+    return o > k ? o : k;
+}
+
+/* 64-bit wave max on DPP (VALU lane moves, no LDS round trips): row shifts
+ * give each row's max in its lane 15, two row broadcasts carry it to lane
+ * 63, read back as a wave-uniform value. */
 __device__ __forceinline__ uint64_t rt_wave_max(uint64_t k) {
-    for (int off = 32; off > 0; off >>= 1) {
-        uint32_t lo = __shfl_xor((uint32_t)k, off, 64);
-        uint32_t hi = __shfl_xor((uint32_t)(k >> 32), off, 64);
-        uint64_t o = ((uint64_t)hi << 32) | lo;
-        k = o > k ? o : k;
-    }
-    return k;
+    k = rt_dpp_max<0x111, 0xf>(k);       /* row_shr:1 */
+    k = rt_dpp_max<0x112, 0xf>(k);       /* row_shr:2 */
+    k = rt_dpp_max<0x114, 0xf>(k);       /* row_shr:4 */
+    k = rt_dpp_max<0x118, 0xf>(k);       /* row_shr:8 */
+    k = rt_dpp_max<0x142, 0xa>(k);       /* row_bcast:15 */
+    k = rt_dpp_max<0x143, 0xc>(k);       /* row_bcast:31 */
+    const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)k, 63);
+    const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(k >> 32), 63);
+    return ((uint64_t)hi << 32) | lo;
 }
 
 /* Routing by one wave into rt[] (an LDS route record: RT_NSEL, RT_IDS,
@@ -86,31 +101,52 @@ __device__ __forceinline__ void md_route(const float *__restrict__ logits,
             int i = lane + 64 * s;
             key[s] = i < E ? rt_key(logits[i], i) : 0ull;
         }
+        /* slot j's (id, logit) ends in lane j */
+        int myid = -1;
+        float mylog = 0.0f;
         for (int j = 0; j < topk; j++) {
             uint64_t b = 0;
 #pragma unroll
             for (int s = 0; s < RT_REG; s++) b = key[s] > b ? key[s] : b;
             b = rt_wave_max(b);
-            const int bi = (int)(0xffffffffu - (uint32_t)b);
 #pragma unroll
             for (int s = 0; s < RT_REG; s++)
                 if (key[s] == b) key[s] = 0ull;
-            if (lane == 0) {
+            if (lane == j) {
                 /* the value is in the key: undo the monotone transform */
                 const uint32_t hi = (uint32_t)(b >> 32);
-                te[j] = bi;
-                tw[j] = __uint_as_float((hi & 0x80000000u) ? (hi & 0x7fffffffu) : ~hi);
+                myid = (int)(0xffffffffu - (uint32_t)b);
+                mylog = __uint_as_float((hi & 0x80000000u) ? (hi & 0x7fffffffu) : ~hi);
             }
         }
-        if (lane == 0) {
-            float m = tw[0], ssum = 0.0f;
-            for (int j = 0; j < topk; j++) {
-                tw[j] = expf(tw[j] - m);
-                ssum = ssum + tw[j];
-            }
-            for (int j = 0; j < topk; j++) tw[j] = tw[j] / ssum;
+        /* softmax over the k slots in slot order: m = slot 0's logit,
+         * e_j = expf(l_j - m), s = e_0 + e_1 + ... (ascending j), w = e / s */
+        const float m = __shfl(mylog, 0, 64);
+        const float ej = expf(mylog - m);
+        float ssum = 0.0f;
+        for (int j = 0; j < topk; j++)
+            ssum = ssum + __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                                         __builtin_bit_cast(int, ej), j));
+        const float wj = ej / ssum;
+        /* distinct ids: place slot j by its rank among the k ids */
+        int pos = 0;
+        for (int j = 0; j < topk; j++)
+            pos += __builtin_amdgcn_readlane(myid, j) < myid;
+        if (lane < MD_MAXK) {
+            rt[RT_IDS + lane] = 0u;
+            rt[RT_W + lane] = 0u;
         }
-    } else if (lane < topk) {
+        __builtin_amdgcn_wave_barrier();
+        if (lane < topk) {
+            rt[RT_IDS + pos] = (uint32_t)myid;
+            rt[RT_W + pos] = __float_as_uint(wj);
+        }
+        if (lane == 0) rt[RT_NSEL] = (uint32_t)topk;
+        __builtin_amdgcn_s_waitcnt(0xc07f);       /* lgkmcnt(0) */
+        __builtin_amdgcn_wave_barrier();
+        return;
+    }
+    if (lane < topk) {
         te[lane] = idx[lane];
         tw[lane] = w[lane];
     }
@@ -195,40 +231,55 @@ __device__ __forceinline__ ghip_chunk md_read_chunk(const uint8_t *buf, uint32_t
 #define GU_IPW 4                 /* items per workgroup pass (2 waves each) */
 #define GU_R 4                   /* ring stages per wave (gate + up chunk) */
 #define GU_STG 4096              /* bytes per stage */
+#define DN_R 6                   /* down ring stages per wave (one chunk each) */
+#define DN_STG 2048
+#define FU_SPIN (1u << 22)       /* bound on the fused kernel's phase wait */
 
-/* Routing first (wave 0; workgroup 0 publishes the record for the down
- * launch), then items = (slot q, 16 rows): gate and up GEMVs over dim and
- * the SwiGLU -> h[q]. Persistent: workgroup b takes item groups b, b + G,
- * ... of GU_IPW items; wave w streams item (w / 2)'s half (w % 2) of K
- * through a wave-private GU_R-stage LDS ring filled by direct DMA (no
- * registers hold loads in flight, no barriers inside the stream); the two
- * halves are summed in LDS in a fixed order (deterministic). x is staged
- * once per workgroup. */
-__global__ __launch_bounds__(GU_NW * 64, 1) void k_moe_gateup(
-    GhipBank bank, const uint16_t *__restrict__ x, const float *__restrict__ logits,
-    const int32_t *__restrict__ idx, const float *__restrict__ w, int topk,
-    float limit, uint16_t *__restrict__ h, uint32_t *__restrict__ route_out,
-    uint32_t *__restrict__ err) {
-    extern __shared__ __attribute__((aligned(1024))) uint8_t gl[];
-    __shared__ uint32_t rt[GHIP_MOE_ROUTE_WORDS];
-    __shared__ int32_t te[MD_MAXK];
-    __shared__ float tw[MD_MAXK];
-    __shared__ float red[GU_IPW][2][2][16];
-    const uint32_t dim = bank.dim, inter = bank.inter;
-    uint16_t *xs = (uint16_t *)gl;
-    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+/* LDS that both kernels share (static, per workgroup) */
+struct MdShared {
+    uint32_t rt[GHIP_MOE_ROUTE_WORDS];
+    int32_t te[MD_MAXK];
+    float tw[MD_MAXK];
+    float red[GU_IPW][2][2][16];
+    float oq[MD_MAXK][16];
+};
+
+/* Phase A: routing (wave 0 into sh.rt) and x into LDS, then a barrier. */
+__device__ __forceinline__ void md_phase_route(const GhipBank &bank,
+                                               const uint16_t *__restrict__ x,
+                                               const float *__restrict__ logits,
+                                               const int32_t *__restrict__ idx,
+                                               const float *__restrict__ w, int topk,
+                                               uint16_t *xs, MdShared &sh,
+                                               uint32_t *__restrict__ err) {
+    const uint32_t tid = threadIdx.x;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     if (wv == 0)
-        md_route(logits, idx, w, topk, (int)bank.n_experts, rt, te, tw,
+        md_route(logits, idx, w, topk, (int)bank.n_experts, sh.rt, sh.te, sh.tw,
                  blockIdx.x == 0 ? err : nullptr);
-    for (uint32_t i = tid; i < (dim >> 3); i += GU_NW * 64)
+    for (uint32_t i = tid; i < (bank.dim >> 3); i += GU_NW * 64)
         ((ghip_u32x4 *)xs)[i] = ((const ghip_u32x4 *)x)[i];
     __syncthreads();
-    if (blockIdx.x == 0 && tid < GHIP_MOE_ROUTE_WORDS) route_out[tid] = rt[tid];
-    const uint32_t nsel = __builtin_amdgcn_readfirstlane(rt[RT_NSEL]);
+}
+
+/* Phase B: items = (slot q, 16 rows): gate and up GEMVs over dim and the
+ * SwiGLU; workgroup b takes item groups b, b + G, ... of GU_IPW items; wave
+ * w streams item (w / 2)'s half (w % 2) of K through a wave-private
+ * GU_R-stage LDS ring filled by direct DMA (no registers hold loads in
+ * flight, no barriers inside the stream); the halves are summed in LDS in a
+ * fixed order (deterministic). put(q, row, hval) stores one h value (lanes
+ * 0..15 of the even wave of each item call it together). */
+template <typename Put>
+__device__ __forceinline__ void md_phase_gateup(const GhipBank &bank, const uint16_t *xs,
+                                                uint8_t *ring_base, MdShared &sh,
+                                                float limit, Put put) {
+    const uint32_t dim = bank.dim, inter = bank.inter;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t nsel = __builtin_amdgcn_readfirstlane(sh.rt[RT_NSEL]);
     const uint32_t tiles = inter / MD_T, items = nsel * tiles;
     const uint32_t groups = (items + GU_IPW - 1) / GU_IPW;
-    uint8_t *ring = gl + ((dim * 2u + 1023u) & ~1023u) + wv * (GU_R * GU_STG);
+    uint8_t *ring = ring_base + wv * (GU_R * GU_STG);
     const uint32_t nch = dim >> 7, nkb = dim >> 7;
     const uint32_t half = wv & 1u, slot = wv >> 1;
     const uint32_t c0 = half ? nch / 2 : 0u, c1 = half ? nch : nch / 2;
@@ -243,7 +294,7 @@ __global__ __launch_bounds__(GU_NW * 64, 1) void k_moe_gateup(
         if (live) {
             q = it / tiles;
             r0 = (it - q * tiles) * MD_T;
-            const uint32_t e = __builtin_amdgcn_readfirstlane(rt[RT_IDS + q]);
+            const uint32_t e = __builtin_amdgcn_readfirstlane(sh.rt[RT_IDS + q]);
             const uint8_t *slab = bank.base + (size_t)e * bank.stride;
             const uint8_t *wg = slab + bank.off_gw + (size_t)r0 * dim;
             const uint8_t *wu = slab + bank.off_uw + (size_t)r0 * dim;
@@ -279,103 +330,224 @@ __global__ __launch_bounds__(GU_NW * 64, 1) void k_moe_gateup(
                 }
             }
             if (g == 0) {
-                red[slot][half][0][n] = ag[0];
-                red[slot][half][1][n] = au[0];
+                sh.red[slot][half][0][n] = ag[0];
+                sh.red[slot][half][1][n] = au[0];
             }
         }
         __syncthreads();
         if (live && half == 0 && lane < 16) {     /* fixed order: half 0 + half 1 */
-            const float gs = red[slot][0][0][lane] + red[slot][1][0][lane];
-            const float us = red[slot][0][1][lane] + red[slot][1][1][lane];
-            h[(size_t)q * inter + r0 + lane] = (uint16_t)ghip_swiglu(
-                ghip_bf16_round(gs), ghip_bf16_round(us), limit);
+            const float gs = sh.red[slot][0][0][lane] + sh.red[slot][1][0][lane];
+            const float us = sh.red[slot][0][1][lane] + sh.red[slot][1][1][lane];
+            put(q, r0 + lane,
+                ghip_swiglu(ghip_bf16_round(gs), ghip_bf16_round(us), limit));
         }
         __syncthreads();
     }
 }
 
-/* ------------------------------------------------------------------------ */
-/* down + ordered combine                                                   */
-/* ------------------------------------------------------------------------ */
+/* Phase C, down + ordered combine for the 16 output rows at r0: wave q
+ * streams expert slot q's 16 rows of Wd over inter through its own
+ * DN_R-stage DMA ring with h of slot base + q (in LDS at hs + q * inter)
+ * as the A operand and leaves the expert output in sh.oq; md_combine then
+ * runs the ordered combine in-workgroup: no atomics, no cross-workgroup
+ * reduction, deterministic. md_down_prologue issues the first DN_R - 1
+ * stages (so they stream while the caller waits for h). */
+__device__ __forceinline__ void md_down_prologue(const GhipBank &bank, const MdShared &sh,
+                                                 uint32_t r0, uint32_t base,
+                                                 uint8_t *ring_base) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t nsel = __builtin_amdgcn_readfirstlane(sh.rt[RT_NSEL]);
+    if (base + wv >= nsel) return;
+    const uint32_t inter = bank.inter, nch = inter >> 7;
+    const uint32_t e = __builtin_amdgcn_readfirstlane(sh.rt[RT_IDS + base + wv]);
+    const uint8_t *rows = bank.base + (size_t)e * bank.stride + bank.off_dw + (size_t)r0 * inter;
+    const MdDma d = md_dma_offsets(lane, inter);
+    uint8_t *ring = ring_base + wv * (DN_R * DN_STG);
+#pragma unroll
+    for (uint32_t i = 0; i + 1 < DN_R; i++)
+        if (i < nch) md_issue_chunk(rows, i, d, ring + i * DN_STG);
+}
 
-#define DN_R 6                   /* ring stages per wave (one chunk each) */
-#define DN_STG 2048
-
-/* One workgroup per 16 output rows; wave q streams expert slot q's 16 rows
- * of Wd over inter through its own DN_R-stage DMA ring (h[q] staged into
- * the wave's own LDS region as the A operand, restaged for a second slot
- * q + 8), then the ascending-expert combine
- * y = bf16(y + bf16(bf16(o) * w)) (c/gmoe.h:307-320) runs in-workgroup:
- * no atomics, no cross-workgroup reduction, deterministic. */
-__global__ __launch_bounds__(MD_NW * 64, 1) void k_moe_down(
-    GhipBank bank, const uint16_t *__restrict__ h, const uint32_t *__restrict__ route,
-    uint16_t *__restrict__ out) {
-    extern __shared__ __attribute__((aligned(1024))) uint8_t dl[];
-    __shared__ float oq[MD_MAXK][16];
+__device__ __forceinline__ void md_phase_down(const GhipBank &bank, MdShared &sh,
+                                              uint32_t r0, uint32_t base, const uint16_t *hs,
+                                              uint8_t *ring_base) {
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t n = lane & 15u, g = lane >> 4;
-    const uint32_t inter = bank.inter;
-    const uint32_t r0 = blockIdx.x * MD_T;
-    const uint32_t nsel = __builtin_amdgcn_readfirstlane(route[RT_NSEL]);
-    const uint32_t nch = inter >> 7, nkb = inter >> 7;
-    uint16_t *hs = (uint16_t *)dl + (size_t)wv * inter;  /* this wave's h */
-    uint8_t *ring = dl + (size_t)MD_NW * inter * 2u + wv * (DN_R * DN_STG);
-    const MdDma d = md_dma_offsets(lane, inter);
-    const uint32_t T = nch * ((nsel > wv ? nsel - wv + MD_NW - 1 : 0u) / MD_NW);
-
-    auto slot_rows = [&](uint32_t k) {
-        const uint32_t q = wv + k * MD_NW;
-        const uint32_t e = __builtin_amdgcn_readfirstlane(route[RT_IDS + q]);
-        return bank.base + (size_t)e * bank.stride + bank.off_dw + (size_t)r0 * inter;
-    };
-    auto issue = [&](uint32_t t) {
-        const uint32_t k = t / nch, c = t - k * nch;
-        md_issue_chunk(slot_rows(k), c, d, ring + (t % DN_R) * DN_STG);
-    };
-    /* h of the first slot before any DMA is in flight (its vector loads
-     * and the LDS writes wait with vmcnt / lgkmcnt of their own) */
-    if (wv < nsel) ghip_wcopy(hs, h + (size_t)wv * inter, inter >> 3, lane);
-#pragma unroll
-    for (uint32_t i = 0; i + 1 < DN_R; i++)
-        if (i < T) issue(i);
-
-    ghip_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    const float *srow = nullptr;
-    bool exact = false;
-    for (uint32_t t = 0; t < T; t++) {
-        const uint32_t k = t / nch, c = t - k * nch, q = wv + k * MD_NW;
-        if (c == 0) {
-            const uint32_t e = __builtin_amdgcn_readfirstlane(route[RT_IDS + q]);
-            const uint8_t *slab = bank.base + (size_t)e * bank.stride;
-            srow = (const float *)(slab + bank.off_ds) + (size_t)(r0 >> 7) * nkb;
-            exact = bank.nan_flags && bank.nan_flags[e];
-            /* a second slot (topk > 8): restage; the copy's loads wait for
-             * the DMA already in flight, a bubble only for such routings */
-            if (k > 0) ghip_wcopy(hs, h + (size_t)q * inter, inter >> 3, lane);
+    const uint32_t inter = bank.inter, nch = inter >> 7, nkb = inter >> 7;
+    const uint32_t nsel = __builtin_amdgcn_readfirstlane(sh.rt[RT_NSEL]);
+    if (base + wv < nsel) {
+        const uint32_t e = __builtin_amdgcn_readfirstlane(sh.rt[RT_IDS + base + wv]);
+        const uint8_t *slab = bank.base + (size_t)e * bank.stride;
+        const uint8_t *rows = slab + bank.off_dw + (size_t)r0 * inter;
+        const float *srow = (const float *)(slab + bank.off_ds) + (size_t)(r0 >> 7) * nkb;
+        const bool exact = bank.nan_flags && bank.nan_flags[e];
+        const MdDma d = md_dma_offsets(lane, inter);
+        uint8_t *ring = ring_base + wv * (DN_R * DN_STG);
+        ghip_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        for (uint32_t t = 0; t < nch; t++) {
+            ghip_wait_stages<2, DN_R - 2>(nch - 1 - t);
+            if (t + DN_R - 1 < nch)
+                md_issue_chunk(rows, t + DN_R - 1, d, ring + ((t + DN_R - 1) % DN_R) * DN_STG);
+            const ghip_chunk cw = md_read_chunk(ring + (t % DN_R) * DN_STG, n, g);
+            const float sc = ghip_sload(srow, t);
+            const uint16_t *ha = hs + (size_t)wv * inter + t * 128u + 32u * g;
+            if (exact) ghip_chunk_mfma<true>(cw, sc, ha, acc);
+            else ghip_chunk_mfma<false>(cw, sc, ha, acc);
         }
-        ghip_wait_stages<2, DN_R - 2>(T - 1 - t);
-        if (t + DN_R - 1 < T) issue(t + DN_R - 1);
-        const ghip_chunk cw = md_read_chunk(ring + (t % DN_R) * DN_STG, n, g);
-        const float sc = ghip_sload(srow, c);
-        const uint16_t *ha = hs + c * 128u + 32u * g;
-        if (exact) ghip_chunk_mfma<true>(cw, sc, ha, acc);
-        else ghip_chunk_mfma<false>(cw, sc, ha, acc);
-        if (c == nch - 1) {
-            if (g == 0) oq[q][n] = acc[0];
-            acc = (ghip_f32x4){0.f, 0.f, 0.f, 0.f};
-        }
+        if (g == 0) sh.oq[base + wv][n] = acc[0];
     }
-    __syncthreads();
+}
+
+/* the ascending-expert combine of the nsel expert outputs in sh.oq (slot
+ * order = ascending expert id): y = bf16(y + bf16(bf16(o) * w)), from +0
+ * (c/gmoe.h:307-320). Call after a barrier. */
+__device__ __forceinline__ void md_combine(const MdShared &sh, uint32_t r0,
+                                           uint16_t *__restrict__ out) {
+    const uint32_t tid = threadIdx.x;
     if (tid < 16) {
+        const uint32_t nsel = sh.rt[RT_NSEL];
         float y = 0.0f;
         for (uint32_t q = 0; q < nsel; q++) {
-            float eo = ghip_bf16_round(oq[q][tid]);
-            float c = ghip_bf16_round(eo * __uint_as_float(route[RT_W + q]));
+            float eo = ghip_bf16_round(sh.oq[q][tid]);
+            float c = ghip_bf16_round(eo * __uint_as_float(sh.rt[RT_W + q]));
             y = ghip_bf16_round(y + c);
         }
         out[r0 + tid] = (uint16_t)ghip_bf16_bits(y);
     }
+}
+
+/* ------------------------------------------------------------------------ */
+/* fused decode: one persistent launch                                      */
+/* ------------------------------------------------------------------------ */
+
+/* Phases A and B, then a device-wide handoff of h, then phase C. One
+ * workgroup per CU (LDS use keeps it at one), so all workgroups are
+ * resident and the wait completes. h crosses XCDs (separate L2s) without
+ * fences: it is written and read with agent-scope atomics (coherent
+ * accesses), each workgroup waits for its h stores to complete before
+ * bumping the counter, and readers load h only after the counter reads
+ * complete. The counter is monotone per store (target = (epoch + 1) * G, the
+ * host counts launches), so it is never reset; the wait is bounded and
+ * reports a timeout in err (bit 4) instead of hanging. Each workgroup
+ * issues its down weights' first ring stages before waiting. nsel <= 8. */
+__global__ __launch_bounds__(GU_NW * 64, 1) void k_moe_fused(
+    GhipBank bank, const uint16_t *__restrict__ x, const float *__restrict__ logits,
+    const int32_t *__restrict__ idx, const float *__restrict__ w, int topk, float limit,
+    uint32_t *__restrict__ hw, uint32_t *__restrict__ route_out, uint32_t *__restrict__ err,
+    uint32_t *__restrict__ sync, uint32_t target, uint16_t *__restrict__ out) {
+    extern __shared__ __attribute__((aligned(1024))) uint8_t gl[];
+    __shared__ MdShared sh;
+    const uint32_t dim = bank.dim, inter = bank.inter;
+    const uint32_t tid = threadIdx.x;
+    uint16_t *xs = (uint16_t *)gl;
+    uint8_t *gu_ring = gl + ((dim * 2u + 1023u) & ~1023u);
+    md_phase_route(bank, x, logits, idx, w, topk, xs, sh, err);
+    if (blockIdx.x == 0 && tid < GHIP_MOE_ROUTE_WORDS) route_out[tid] = sh.rt[tid];
+    /* h pairs packed by adjacent lanes into agent-scope 32-bit stores */
+    md_phase_gateup(bank, xs, gu_ring, sh, limit, [&](uint32_t q, uint32_t row, uint32_t hv) {
+        const uint32_t hi = __shfl_down(hv, 1, 64);
+        if ((row & 1u) == 0)
+            __hip_atomic_store(hw + (((size_t)q * inter + row) >> 1), hv | (hi << 16),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    });
+    /* this workgroup's h stores are complete before it is counted */
+    GHIP_VMCNT(0);
+    __syncthreads();
+    if (tid == 0) __hip_atomic_fetch_add(sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    /* down: this workgroup's row groups; the first one's weights start
+     * streaming before the wait */
+    const uint32_t rgs = dim / MD_T;
+    uint8_t *hsb = gl;                                       /* h [8][inter] */
+    uint8_t *dn_ring = gl + (size_t)MD_NW * inter * 2u;
+    if (blockIdx.x < rgs) md_down_prologue(bank, sh, blockIdx.x * MD_T, 0u, dn_ring);
+    if (tid == 0) {
+        uint32_t spins = 0;
+        while (__hip_atomic_load(sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+            __builtin_amdgcn_s_sleep(1);
+            if (++spins == FU_SPIN) {
+                atomicOr(err, 4u);
+                break;
+            }
+        }
+    }
+    __syncthreads();
+    const uint32_t nsel = __builtin_amdgcn_readfirstlane(sh.rt[RT_NSEL]);
+    /* h of all slots: 64-bit coherent loads, all issued before any use */
+    const uint32_t dwords = nsel * inter / 4;
+    for (uint32_t i0 = tid; i0 < dwords; i0 += GU_NW * 64 * 8) {
+        uint64_t v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const uint32_t i = i0 + u * GU_NW * 64;
+            v[u] = i < dwords ? __hip_atomic_load((const uint64_t *)hw + i, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT)
+                              : 0ull;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const uint32_t i = i0 + u * GU_NW * 64;
+            if (i < dwords) ((uint64_t *)hsb)[i] = v[u];
+        }
+    }
+    __syncthreads();
+    for (uint32_t rg = blockIdx.x; rg < rgs; rg += gridDim.x) {
+        if (rg != blockIdx.x) md_down_prologue(bank, sh, rg * MD_T, 0u, dn_ring);
+        md_phase_down(bank, sh, rg * MD_T, 0u, (const uint16_t *)hsb, dn_ring);
+        __syncthreads();
+        md_combine(sh, rg * MD_T, out);
+        __syncthreads();
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* two-launch decode (routings with more than 8 kept slots)                 */
+/* ------------------------------------------------------------------------ */
+
+__global__ __launch_bounds__(GU_NW * 64, 1) void k_moe_gateup(
+    GhipBank bank, const uint16_t *__restrict__ x, const float *__restrict__ logits,
+    const int32_t *__restrict__ idx, const float *__restrict__ w, int topk,
+    float limit, uint16_t *__restrict__ h, uint32_t *__restrict__ route_out,
+    uint32_t *__restrict__ err) {
+    extern __shared__ __attribute__((aligned(1024))) uint8_t gl[];
+    __shared__ MdShared sh;
+    const uint32_t dim = bank.dim, inter = bank.inter;
+    uint16_t *xs = (uint16_t *)gl;
+    md_phase_route(bank, x, logits, idx, w, topk, xs, sh, err);
+    if (blockIdx.x == 0 && threadIdx.x < GHIP_MOE_ROUTE_WORDS)
+        route_out[threadIdx.x] = sh.rt[threadIdx.x];
+    md_phase_gateup(bank, xs, gl + ((dim * 2u + 1023u) & ~1023u), sh, limit,
+                    [&](uint32_t q, uint32_t row, uint32_t hv) {
+                        h[(size_t)q * inter + row] = (uint16_t)hv;
+                    });
+}
+
+/* One workgroup per 16 output rows; h of up to 8 slots in LDS per pass
+ * (slots past 8 run in a second pass with h restaged), then the combine
+ * over all slots. */
+__global__ __launch_bounds__(MD_NW * 64, 1) void k_moe_down(
+    GhipBank bank, const uint16_t *__restrict__ h, const uint32_t *__restrict__ route,
+    uint16_t *__restrict__ out) {
+    extern __shared__ __attribute__((aligned(1024))) uint8_t dl[];
+    __shared__ MdShared sh;
+    const uint32_t tid = threadIdx.x, inter = bank.inter;
+    if (tid < GHIP_MOE_ROUTE_WORDS) sh.rt[tid] = route[tid];
+    __syncthreads();
+    const uint32_t nsel = sh.rt[RT_NSEL];
+    uint16_t *hs = (uint16_t *)dl;
+    uint8_t *ring = dl + (size_t)MD_NW * inter * 2u;
+    const uint32_t r0 = blockIdx.x * MD_T;
+    for (uint32_t base = 0; base < nsel; base += MD_NW) {
+        const uint32_t m = nsel - base < MD_NW ? nsel - base : MD_NW;
+        for (uint32_t i = tid; i < m * inter / 8; i += MD_NW * 64)
+            ((ghip_u32x4 *)hs)[i] = ((const ghip_u32x4 *)(h + (size_t)base * inter))[i];
+        __syncthreads();
+        md_down_prologue(bank, sh, r0, base, ring);
+        md_phase_down(bank, sh, r0, base, hs, ring);
+        __syncthreads();
+    }
+    md_combine(sh, r0, out);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -407,6 +579,22 @@ extern "C" hipError_t ghip_launch_moe_decode(const GhipBank *bank,
     hipEvent_t e0 = ev ? ev[0] : nullptr, e1 = ev ? ev[1] : nullptr;
     hipEvent_t e2 = ev ? ev[2] : nullptr, e3 = ev ? ev[3] : nullptr;
     hipError_t e;
+    if (topk <= MD_NW && ws->sync && ws->epoch) {
+        /* one persistent launch: grid = CUs (all resident) */
+        const size_t lds = lds_gu > lds_dn ? lds_gu : lds_dn;
+        const uint32_t G = ws->n_cu;
+        const uint32_t target = (uint32_t)((*ws->epoch + 1) * G);
+        GHIP_LAUNCH(e0, e1, k_moe_fused, dim3(G), dim3(GU_NW * 64), lds, st, *bank, x,
+                    logits, idx, w, topk, limit, (uint32_t *)ws->h, ws->route, ws->err,
+                    ws->sync, target, out);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        (*ws->epoch)++;
+        if (e2) {                     /* nothing separate to time */
+            if ((e = hipEventRecord(e2, st)) != hipSuccess) return e;
+            if ((e = hipEventRecord(e3, st)) != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
     uint32_t groups = ((uint32_t)topk * (inter / MD_T) + GU_IPW - 1) / GU_IPW;
     if (groups > ws->n_cu) groups = ws->n_cu;             /* persistent */
     GHIP_LAUNCH(e0, e1, k_moe_gateup, dim3(groups), dim3(GU_NW * 64), lds_gu, st, *bank,
@@ -418,10 +606,12 @@ extern "C" hipError_t ghip_launch_moe_decode(const GhipBank *bank,
 }
 
 extern "C" hipError_t ghip_moe_decode_init(void) {
-    hipError_t e = hipFuncSetAttribute((const void *)k_moe_gateup,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       MD_LDS_MAX);
-    if (e != hipSuccess) return e;
-    return hipFuncSetAttribute((const void *)k_moe_down,
-                               hipFuncAttributeMaxDynamicSharedMemorySize, MD_LDS_MAX);
+    const void *ks[3] = {(const void *)k_moe_gateup, (const void *)k_moe_down,
+                         (const void *)k_moe_fused};
+    for (int i = 0; i < 3; i++) {
+        hipError_t e = hipFuncSetAttribute(ks[i], hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           MD_LDS_MAX);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }

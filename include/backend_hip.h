@@ -173,10 +173,11 @@ int apus_ghip_store_expert_bf16(ApusGhipStore *s, int expert,
                                 uint16_t *payload);
 
 /* --- routed MoE decode (one token): SwiGLU experts + ordered combine,
- * c/gmoe.h:210-227 + 307-320 without the router and shared expert. Two
- * stream-ordered launches, each grouped over all routed experts: routing
- * with the gate/up GEMVs and their SwiGLU epilogue, then the down GEMVs
- * with the ascending-expert bf16-per-add combine.
+ * c/gmoe.h:210-227 + 307-320 without the router and shared expert. Up to 8
+ * kept slots: one persistent launch (routing, gate/up GEMVs with the
+ * SwiGLU epilogue, a device-wide handoff of the activations, down GEMVs
+ * with the ascending-expert bf16-per-add combine); more slots: two
+ * stream-ordered launches split at the handoff.
  * Routing either given (idx/w [topk]) or computed on the device from
  * logits [n_experts] f32: stable top-k (ties -> lower id), w = softmax over
  * the k selected logits. Host-pointer variant is synchronous. */
@@ -217,7 +218,9 @@ int apus_ghip_moe_prefill_dev(ApusGhipStore *s, const uint16_t *x, size_t T,
  * set, launches carry start/stop events in their dispatch packets
  * (hipExtLaunchKernelGGL), so an event pair spans exactly one kernel:
  * apus_ghip_moe_decode_dev (n >= 4) times the routing + gate/up launch
- * with events[0..1] and the down launch with events[2..3];
+ * with events[0..1] and the down launch with events[2..3] (when it runs as
+ * one fused launch, top-k <= 8, events[0..1] time that launch and
+ * events[2..3] are recorded back to back);
  * apus_ghip_fp8blk_linear_dev (n >= 2) starts events[0] with its first
  * GEMV launch and stops events[1] with its last; apus_ghip_moe_prefill_dev
  * (n >= 8) times the permutation with events[0..1], the gate/up GEMM with
