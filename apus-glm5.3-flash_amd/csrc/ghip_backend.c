@@ -136,6 +136,7 @@ static int ghip_init(void) {
     }
     G.n_cu = (uint32_t)((ncu + 7) / 8 * 8);
     HIPCHK(ghip_moe_decode_init());
+    HIPCHK(ghip_linear_init(G.n_cu));
     HIPCHK(hipMalloc((void **)&G.d_flag, 256));
     HIPCHK(hipMalloc((void **)&G.d_flags, GHIP_SCAN_SLOTS * sizeof(uint32_t)));
     HIPCHK(hipMemset(G.d_flags, 0, GHIP_SCAN_SLOTS * sizeof(uint32_t)));

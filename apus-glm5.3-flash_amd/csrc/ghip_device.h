@@ -266,6 +266,43 @@ __device__ __forceinline__ float ghip_sload(const float *p, uint32_t i) {
     return ((const __attribute__((address_space(4))) float *)p)[i];
 }
 
+/* ---- streaming 16-row GEMV chunks through LDS ---------------------------
+ * A chunk (16 weight rows x 128 codes = 2 KB, one scale block) lives in
+ * LDS as [16 rows][8 pieces of 16 B] with piece p of row r at
+ * (p ^ ((r >> 1) & 7)), so the MFMA-layout reads (lane 16g + n: row n,
+ * pieces 2g and 2g+1) hit distinct banks. Two DMA instructions fill it:
+ * instruction i, lane l -> row 8i + l/8, stored slot l % 8. */
+struct ghip_cdma {
+    uint32_t off0, off1;          /* global byte offsets (row * K + piece) */
+};
+
+/* rmax: rows past it (a partial last group) re-read row rmax */
+__device__ __forceinline__ ghip_cdma ghip_cdma_offsets(uint32_t lane, uint32_t K,
+                                                       uint32_t rmax = 15u) {
+    ghip_cdma d;
+    const uint32_t r0 = min(lane >> 3, rmax), r1 = min(8u + (lane >> 3), rmax);
+    d.off0 = r0 * K + 16u * ((lane & 7u) ^ ((r0 >> 1) & 7u));
+    d.off1 = r1 * K + 16u * ((lane & 7u) ^ ((r1 >> 1) & 7u));
+    return d;
+}
+
+/* chunk c of the 16 rows at `rows` (row stride K) -> LDS chunk buffer */
+__device__ __forceinline__ void ghip_cdma_issue(const uint8_t *rows, uint32_t c,
+                                               const ghip_cdma &d, uint8_t *buf) {
+    ghip_dma16(rows + (size_t)c * 128u + d.off0, buf);
+    ghip_dma16(rows + (size_t)c * 128u + d.off1, buf + 1024);
+}
+
+/* this lane's 32 codes of a chunk in LDS (row n, pieces 2g, 2g+1) */
+__device__ __forceinline__ ghip_chunk ghip_cdma_read(const uint8_t *buf, uint32_t n,
+                                                    uint32_t g) {
+    const uint32_t sw = (n >> 1) & 7u;
+    ghip_chunk c;
+    c.lo = *(const ghip_u32x4 *)(buf + n * 128u + 16u * ((2u * g) ^ sw));
+    c.hi = *(const ghip_u32x4 *)(buf + n * 128u + 16u * ((2u * g + 1u) ^ sw));
+    return c;
+}
+
 /* numpy-stable sigmoid (c/gmhc.h:157-160) with the device expf. */
 __device__ __forceinline__ float ghip_sigmoid_np(float x) {
     float e = expf(-fabsf(x));

@@ -51,6 +51,9 @@ typedef struct {
     uint64_t *epoch;      /* host: fused launches so far on this workspace */
 } GhipMoeDecodeWs;
 
+/* Streaming GEMV set-up (dynamic-LDS limits, persistent grid bound). */
+hipError_t ghip_linear_init(uint32_t n_cu);
+
 /* Raise the decode kernels' dynamic-LDS limit (once per process). */
 hipError_t ghip_moe_decode_init(void);
 

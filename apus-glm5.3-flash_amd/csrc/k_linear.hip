@@ -266,14 +266,123 @@ extern "C" hipError_t ghip_launch_nan_scan(const uint8_t *codes, size_t n,
     return hipGetLastError();
 }
 
+/* ------------------------------------------------------------------------ */
+/* K2 streaming: persistent FP8 GEMV through per-wave DMA rings             */
+/* ------------------------------------------------------------------------ */
+
+#define GS_NW 8                  /* waves per workgroup */
+#define GS_R 6                   /* ring stages per wave (one chunk each) */
+#define GS_LDS (144u * 1024u)    /* dynamic LDS limit of the streaming GEMV */
+
+/* Y[m, rows] for M <= 4 token rows. A row group (16 weight rows) is split
+ * over KS waves along K (KS in {2, 8}); a workgroup pass covers 8 / KS row
+ * groups, passes run over the groups persistently (grid <= CUs). Each wave
+ * streams its chunks (16 rows x 128 codes, one scale block) through a
+ * wave-private GS_R-stage LDS ring filled by direct DMA, dequantizes in
+ * registers and reduces on MFMA with the token rows of x (staged once per
+ * workgroup) as the A operand: A row i = lane % 16 is token min(i, M-1),
+ * rows past M feed output rows that are discarded. The KS partial sums of a
+ * group are added in LDS in a fixed order (deterministic). */
+template <int M, int KS>
+__global__ __launch_bounds__(GS_NW * 64, 1) void k_fp8_gemv_stream(
+    const uint8_t *__restrict__ W, const float *__restrict__ S,
+    const uint16_t *__restrict__ X, uint16_t *__restrict__ Y, uint32_t O,
+    uint32_t K, const uint32_t *__restrict__ exact_flag) {
+    constexpr uint32_t GPP = GS_NW / KS;             /* row groups per pass */
+    extern __shared__ __attribute__((aligned(1024))) uint8_t gsl[];
+    __shared__ float red[GPP][KS][M][16];
+    uint16_t *xs = (uint16_t *)gsl;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t n = lane & 15u, g = lane >> 4;
+    for (uint32_t i = tid; i < (uint32_t)M * (K >> 3); i += GS_NW * 64)
+        ((ghip_u32x4 *)xs)[i] = ((const ghip_u32x4 *)X)[i];
+    __syncthreads();
+    const bool exact = exact_flag != nullptr && *exact_flag != 0u;
+    uint8_t *ring = gsl + (((size_t)M * K * 2u + 1023u) & ~(size_t)1023u) +
+                    wv * (GS_R * 2048u);
+    const uint32_t nch = K >> 7, nkb = nch;
+    const uint32_t part = wv % KS, slot = wv / KS;
+    const uint32_t c0 = part * nch / KS, c1 = (part + 1) * nch / KS, nc = c1 - c0;
+    const uint32_t groups = (O + 15) / 16, passes = (groups + GPP - 1) / GPP;
+    const uint16_t *xa = xs + (size_t)min(n, (uint32_t)M - 1u) * K + 32u * g;
+    for (uint32_t ps = blockIdx.x; ps < passes; ps += gridDim.x) {
+        const uint32_t grp = ps * GPP + slot;
+        const bool live = grp < groups;
+        if (live) {
+            /* a wave with no chunks (K < KS * 128) contributes zeros */
+            const uint32_t row0 = grp * 16;
+            const uint8_t *rows = W + (size_t)row0 * K;
+            /* a partial last group re-reads row O-1 (outputs discarded) */
+            const ghip_cdma d = ghip_cdma_offsets(lane, K, min(15u, O - 1u - row0));
+            const float *srow = S + (size_t)(row0 >> 7) * nkb;
+#pragma unroll
+            for (uint32_t i = 0; i + 1 < GS_R; i++)
+                if (i < nc) ghip_cdma_issue(rows, c0 + i, d, ring + i * 2048u);
+            ghip_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            for (uint32_t t = 0; t < nc; t++) {
+                ghip_wait_stages<2, GS_R - 2>(nc - 1 - t);
+                if (t + GS_R - 1 < nc)
+                    ghip_cdma_issue(rows, c0 + t + GS_R - 1, d,
+                                    ring + ((t + GS_R - 1) % GS_R) * 2048u);
+                const ghip_chunk cw = ghip_cdma_read(ring + (t % GS_R) * 2048u, n, g);
+                const uint32_t c = c0 + t;
+                const float sc = ghip_sload(srow, c);
+                if (exact) ghip_chunk_mfma<true>(cw, sc, xa + c * 128u, acc);
+                else ghip_chunk_mfma<false>(cw, sc, xa + c * 128u, acc);
+            }
+            if (g == 0) {
+#pragma unroll
+                for (int i = 0; i < M; i++) red[slot][part][i][n] = acc[i];
+            }
+        }
+        __syncthreads();
+        if (tid < GPP * M * 16u) {
+            const uint32_t sl = tid / (M * 16u), rem = tid - sl * (M * 16u);
+            const uint32_t m = rem >> 4, nn = rem & 15u;
+            const uint32_t gp = ps * GPP + sl;
+            if (gp < groups && gp * 16 + nn < O) {
+                float s = 0.0f;
+#pragma unroll
+                for (int k = 0; k < KS; k++) s += red[sl][k][m][nn];
+                Y[(size_t)m * O + gp * 16 + nn] = (uint16_t)ghip_bf16_bits(s);
+            }
+        }
+        __syncthreads();
+    }
+}
+
+static uint32_t g_gs_ncu;                 /* CUs: the streaming grid bound */
+
+/* LDS the streaming GEMV needs for M token rows of length K */
+static size_t gs_lds(size_t M, size_t K) {
+    return ((M * K * 2 + 1023) & ~(size_t)1023) + (size_t)GS_NW * GS_R * 2048;
+}
+
 template <int M>
 static hipError_t launch_gemv_m(const uint8_t *codes, const float *scales,
                                 const uint16_t *x, uint16_t *y, size_t O,
                                 size_t K, const uint32_t *exact_dev,
                                 hipEvent_t ev0, hipEvent_t ev1, hipStream_t st) {
+    const size_t groups = (O + 15) / 16;
+    if (g_gs_ncu && gs_lds(M, K) <= GS_LDS) {
+        const size_t lds = gs_lds(M, K);
+        if ((groups + 3) / 4 >= g_gs_ncu) {          /* KS = 2: 4 groups a pass */
+            uint32_t g = (uint32_t)((groups + 3) / 4);
+            if (g > g_gs_ncu) g = g_gs_ncu;
+            GHIP_LAUNCH(ev0, ev1, (k_fp8_gemv_stream<M, 2>), dim3(g), dim3(GS_NW * 64),
+                        lds, st, codes, scales, x, y, (uint32_t)O, (uint32_t)K, exact_dev);
+        } else {                                       /* KS = 8: 1 group a pass */
+            uint32_t g = (uint32_t)groups;
+            if (g > g_gs_ncu) g = g_gs_ncu;
+            GHIP_LAUNCH(ev0, ev1, (k_fp8_gemv_stream<M, 8>), dim3(g), dim3(GS_NW * 64),
+                        lds, st, codes, scales, x, y, (uint32_t)O, (uint32_t)K, exact_dev);
+        }
+        return hipGetLastError();
+    }
     size_t lds = (size_t)M * K * 2;
     uint32_t nkb = (uint32_t)((K + 127) / 128);
-    uint32_t g = (uint32_t)((O + 15) / 16);
+    uint32_t g = (uint32_t)groups;
     GHIP_LAUNCH(ev0, ev1, k_fp8_gemv<M>, dim3(g), dim3(GEMV_NW * 64), lds, st,
                 codes, scales, x, y, (uint32_t)O, (uint32_t)K, nkb, exact_dev);
     return hipGetLastError();
@@ -340,4 +449,22 @@ extern "C" hipError_t ghip_launch_bf16_linear(const uint16_t *w,
                        dim3(256), 0, st, w, x, y, (uint32_t)M, (uint32_t)O,
                        (uint32_t)K);
     return hipGetLastError();
+}
+
+template <int M>
+static hipError_t gs_attr(void) {
+    hipError_t e = hipFuncSetAttribute((const void *)k_fp8_gemv_stream<M, 2>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, GS_LDS);
+    if (e != hipSuccess) return e;
+    return hipFuncSetAttribute((const void *)k_fp8_gemv_stream<M, 8>,
+                               hipFuncAttributeMaxDynamicSharedMemorySize, GS_LDS);
+}
+
+extern "C" hipError_t ghip_linear_init(uint32_t n_cu) {
+    hipError_t e;
+    if ((e = gs_attr<1>()) != hipSuccess || (e = gs_attr<2>()) != hipSuccess
+        || (e = gs_attr<3>()) != hipSuccess || (e = gs_attr<4>()) != hipSuccess)
+        return e;
+    g_gs_ncu = n_cu;
+    return hipSuccess;
 }

@@ -189,40 +189,6 @@ __device__ __forceinline__ void md_route(const float *__restrict__ logits,
 /* weight streaming (both GEMV kernels)                                     */
 /* ------------------------------------------------------------------------ */
 
-/* A chunk (16 weight rows x 128 codes = 2 KB, one scale block) lives in
- * LDS as [16 rows][8 pieces of 16 B] with piece p of row r at
- * (p ^ ((r >> 1) & 7)), so the MFMA-layout reads (lane 16g + n: row n,
- * pieces 2g and 2g+1) hit distinct banks. Two DMA instructions fill it:
- * instruction i, lane l -> row 8i + l/8, stored slot l % 8. */
-struct MdDma {
-    uint32_t off0, off1;          /* global byte offsets (row * K + piece) */
-};
-
-__device__ __forceinline__ MdDma md_dma_offsets(uint32_t lane, uint32_t K) {
-    MdDma d;
-    const uint32_t r0 = lane >> 3, r1 = 8 + (lane >> 3);
-    d.off0 = r0 * K + 16u * ((lane & 7u) ^ ((r0 >> 1) & 7u));
-    d.off1 = r1 * K + 16u * ((lane & 7u) ^ ((r1 >> 1) & 7u));
-    return d;
-}
-
-/* chunk c of the 16 rows at `rows` (row stride K) -> LDS chunk buffer */
-__device__ __forceinline__ void md_issue_chunk(const uint8_t *rows, uint32_t c,
-                                               const MdDma &d, uint8_t *buf) {
-    ghip_dma16(rows + (size_t)c * 128u + d.off0, buf);
-    ghip_dma16(rows + (size_t)c * 128u + d.off1, buf + 1024);
-}
-
-/* this lane's 32 codes of a chunk in LDS (row n, pieces 2g, 2g+1) */
-__device__ __forceinline__ ghip_chunk md_read_chunk(const uint8_t *buf, uint32_t n,
-                                                    uint32_t g) {
-    const uint32_t sw = (n >> 1) & 7u;
-    ghip_chunk c;
-    c.lo = *(const ghip_u32x4 *)(buf + n * 128u + 16u * ((2u * g) ^ sw));
-    c.hi = *(const ghip_u32x4 *)(buf + n * 128u + 16u * ((2u * g + 1u) ^ sw));
-    return c;
-}
-
 /* ------------------------------------------------------------------------ */
 /* gate/up + SwiGLU                                                         */
 /* ------------------------------------------------------------------------ */
@@ -284,7 +250,7 @@ __device__ __forceinline__ void md_phase_gateup(const GhipBank &bank, const uint
     const uint32_t half = wv & 1u, slot = wv >> 1;
     const uint32_t c0 = half ? nch / 2 : 0u, c1 = half ? nch : nch / 2;
     const uint32_t nc = c1 - c0;
-    const MdDma d = md_dma_offsets(lane, dim);
+    const ghip_cdma d = ghip_cdma_offsets(lane, dim);
     const uint32_t n = lane & 15u, g = lane >> 4;
 
     for (uint32_t grp = blockIdx.x; grp < groups; grp += gridDim.x) {
@@ -303,8 +269,8 @@ __device__ __forceinline__ void md_phase_gateup(const GhipBank &bank, const uint
             const bool exact = bank.nan_flags && bank.nan_flags[e];
             auto issue = [&](uint32_t t) {
                 uint8_t *buf = ring + (t % GU_R) * GU_STG;
-                md_issue_chunk(wg, c0 + t, d, buf);
-                md_issue_chunk(wu, c0 + t, d, buf + 2048);
+                ghip_cdma_issue(wg, c0 + t, d, buf);
+                ghip_cdma_issue(wu, c0 + t, d, buf + 2048);
             };
 #pragma unroll
             for (uint32_t i = 0; i + 1 < GU_R; i++)
@@ -316,8 +282,8 @@ __device__ __forceinline__ void md_phase_gateup(const GhipBank &bank, const uint
                 ghip_wait_stages<4, GU_R - 2>(nc - 1 - t);
                 if (t + GU_R - 1 < nc) issue(t + GU_R - 1);
                 const uint8_t *buf = ring + (t % GU_R) * GU_STG;
-                const ghip_chunk cg = md_read_chunk(buf, n, g);
-                const ghip_chunk cu = md_read_chunk(buf + 2048, n, g);
+                const ghip_chunk cg = ghip_cdma_read(buf, n, g);
+                const ghip_chunk cu = ghip_cdma_read(buf + 2048, n, g);
                 const uint32_t c = c0 + t;
                 const float scg = ghip_sload(sg, c), scu = ghip_sload(su, c);
                 const uint16_t *xa = xs + c * 128u + 32u * g;
@@ -362,11 +328,11 @@ __device__ __forceinline__ void md_down_prologue(const GhipBank &bank, const MdS
     const uint32_t inter = bank.inter, nch = inter >> 7;
     const uint32_t e = __builtin_amdgcn_readfirstlane(sh.rt[RT_IDS + base + wv]);
     const uint8_t *rows = bank.base + (size_t)e * bank.stride + bank.off_dw + (size_t)r0 * inter;
-    const MdDma d = md_dma_offsets(lane, inter);
+    const ghip_cdma d = ghip_cdma_offsets(lane, inter);
     uint8_t *ring = ring_base + wv * (DN_R * DN_STG);
 #pragma unroll
     for (uint32_t i = 0; i + 1 < DN_R; i++)
-        if (i < nch) md_issue_chunk(rows, i, d, ring + i * DN_STG);
+        if (i < nch) ghip_cdma_issue(rows, i, d, ring + i * DN_STG);
 }
 
 __device__ __forceinline__ void md_phase_down(const GhipBank &bank, MdShared &sh,
@@ -383,14 +349,14 @@ __device__ __forceinline__ void md_phase_down(const GhipBank &bank, MdShared &sh
         const uint8_t *rows = slab + bank.off_dw + (size_t)r0 * inter;
         const float *srow = (const float *)(slab + bank.off_ds) + (size_t)(r0 >> 7) * nkb;
         const bool exact = bank.nan_flags && bank.nan_flags[e];
-        const MdDma d = md_dma_offsets(lane, inter);
+        const ghip_cdma d = ghip_cdma_offsets(lane, inter);
         uint8_t *ring = ring_base + wv * (DN_R * DN_STG);
         ghip_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
         for (uint32_t t = 0; t < nch; t++) {
             ghip_wait_stages<2, DN_R - 2>(nch - 1 - t);
             if (t + DN_R - 1 < nch)
-                md_issue_chunk(rows, t + DN_R - 1, d, ring + ((t + DN_R - 1) % DN_R) * DN_STG);
-            const ghip_chunk cw = md_read_chunk(ring + (t % DN_R) * DN_STG, n, g);
+                ghip_cdma_issue(rows, t + DN_R - 1, d, ring + ((t + DN_R - 1) % DN_R) * DN_STG);
+            const ghip_chunk cw = ghip_cdma_read(ring + (t % DN_R) * DN_STG, n, g);
             const float sc = ghip_sload(srow, t);
             const uint16_t *ha = hs + (size_t)wv * inter + t * 128u + 32u * g;
             if (exact) ghip_chunk_mfma<true>(cw, sc, ha, acc);
@@ -589,10 +555,6 @@ extern "C" hipError_t ghip_launch_moe_decode(const GhipBank *bank,
                     ws->sync, target, out);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         (*ws->epoch)++;
-        if (e2) {                     /* nothing separate to time */
-            if ((e = hipEventRecord(e2, st)) != hipSuccess) return e;
-            if ((e = hipEventRecord(e3, st)) != hipSuccess) return e;
-        }
         return hipSuccess;
     }
     uint32_t groups = ((uint32_t)topk * (inter / MD_T) + GU_IPW - 1) / GU_IPW;
