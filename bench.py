@@ -134,17 +134,18 @@ def bench_moe_decode(lib, pkg, rt, steps, warmup, rotate=64):
     e1.synchronize()
     wall = time.perf_counter() - t0
     ms = e0.elapsed_ms(e1) / steps
+    fused = k <= 8          # top-k <= 8 runs as one fused launch (backend_hip.h)
     kt = kernel_times(lib, rt, step, warmup + steps, steps, 4,
+                      {"k_moe_fused": (0, 1)} if fused else
                       {"k_moe_gateup": (0, 1), "k_moe_down": (2, 3)})
     nbytes, flops, gu_bytes = moe_algorithmic_bytes(E, k, dim, inter)
     gbs = nbytes / (ms * 1e-3) / 1e9
     lib.apus_ghip_store_close(store)
-    if kt["k_moe_down"] < 1e-3:
-        # top-k <= 8 runs as one fused launch (events 2..3 recorded back to
-        # back): the whole step is that launch
-        kern = {"kernel": "k_moe_fused", "kernel_ms": kt["k_moe_gateup"],
+    if fused:
+        # the whole step is that launch
+        kern = {"kernel": "k_moe_fused", "kernel_ms": kt["k_moe_fused"],
                 "kernel_bytes": nbytes, "kernel_flops": flops,
-                "launch_ms": {"k_moe_fused": round(kt["k_moe_gateup"], 5)}}
+                "launch_ms": {"k_moe_fused": round(kt["k_moe_fused"], 5)}}
     else:
         kern = {"kernel": "k_moe_gateup", "kernel_ms": kt["k_moe_gateup"],
                 "kernel_bytes": gu_bytes, "kernel_flops": 2 * k * 2 * inter * dim,

@@ -220,7 +220,7 @@ int apus_ghip_moe_prefill_dev(ApusGhipStore *s, const uint16_t *x, size_t T,
  * apus_ghip_moe_decode_dev (n >= 4) times the routing + gate/up launch
  * with events[0..1] and the down launch with events[2..3] (when it runs as
  * one fused launch, top-k <= 8, events[0..1] time that launch and
- * events[2..3] are recorded back to back);
+ * events[2..3] are not recorded);
  * apus_ghip_fp8blk_linear_dev (n >= 2) starts events[0] with its first
  * GEMV launch and stops events[1] with its last; apus_ghip_moe_prefill_dev
  * (n >= 8) times the permutation with events[0..1], the gate/up GEMM with
