@@ -70,7 +70,8 @@ def kernel_times(lib, rt, step, first, steps, n_ev, pairs):
         lib.apus_ghip_set_trace_events(arr, n_ev)
         step(first + i)
     lib.apus_ghip_set_trace_events(None, 0)
-    evs[-1][-1].synchronize()
+    # events a step leaves unrecorded (the fused decode's 2..3) do not wait
+    rt.synchronize()
     return {name: sum(evs[i][a].elapsed_ms(evs[i][b]) for i in range(steps)) / steps
             for name, (a, b) in pairs.items()}
 
@@ -386,7 +387,7 @@ def bench_prefill(lib, pkg, rt, steps, warmup, name):
             if rc:
                 pkg.check(rc, "moe_prefill_dev")
     lib.apus_ghip_set_trace_events(None, 0)
-    evs[-1][-1].synchronize()
+    rt.synchronize()
     n = len(evs)
     kt = {nm: sum(ev[a].elapsed_ms(ev[b]) for ev in evs) / n
           for nm, (a, b) in {"k_pf_permute": (0, 1), "k_pf_gemm_gateup": (2, 3),
@@ -413,12 +414,13 @@ def bench_prefill(lib, pkg, rt, steps, warmup, name):
     }
 
 
-def cpu_moe_prefill(lib, L, T):
+def cpu_moe_prefill(lib, L, T, decode_cpu=None):
     """The reference has no grouped GEMM: its prefill is the per-token loop
     (c/gmoe.h:278-320), 8 experts per token on BF16 payloads -- the same
-    per-token work as a decode step. Timed on a bounded token sample and
-    reported as TFLOP/s (50,331,648 FLOP per (token, expert))."""
-    r = cpu_moe_decode(lib)
+    per-token work as a decode step. Timed on a bounded token sample (or
+    taken from the decode leg's timing of that same loop) and reported as
+    TFLOP/s (50,331,648 FLOP per (token, expert))."""
+    r = decode_cpu if decode_cpu is not None else cpu_moe_decode(lib)
     tflops = 8 * 50_331_648 / (r["ms_per_token"] * 1e-3) / 1e12
     r = dict(r)
     r["value"], r["unit"] = tflops, "TFLOP/s"
@@ -459,6 +461,75 @@ def bench_copy(rt, steps, warmup, nbytes=256 << 20):
 
 # --------------------------------------------------------------------------
 
+def roofline_of(r):
+    traffic = traffic_from_profiles(r["kernel"])
+    mfma = r.get("unit") == "TFLOP/s"
+    if mfma:
+        achieved = r["kernel_flops"] / (r["kernel_ms"] * 1e-3) / 1e12
+    else:
+        achieved = r["kernel_bytes"] / (r["kernel_ms"] * 1e-3) / 1e9
+    peak = BF16_PEAK_TFLOPS if mfma else HBM_PEAK_GBS
+    return {
+        "bound": "mfma" if mfma else "hbm",
+        "kernel": r["kernel"],
+        "achieved": round(achieved, 2),
+        "peak": peak,
+        "unit": "TFLOP/s" if mfma else "GB/s",
+        "frac": round(achieved / peak, 4),
+        "traffic": traffic,
+        "algorithmic_bytes_per_launch": r["kernel_bytes"],
+        "algorithmic_flops_per_launch": r["kernel_flops"],
+        "avg_launch_ms": round(r["kernel_ms"], 6),
+        "launch_ms": r["launch_ms"],
+        "mfma_tflops": round(r["kernel_flops"] / (r["kernel_ms"] * 1e-3) / 1e12, 3),
+    }
+
+
+def run_workload(name, lib, pkg, rt, args, cpu_leg):
+    """(metric, result, cpu_baseline) of one workload."""
+    if name == "moe_decode":
+        r = bench_moe_decode(lib, pkg, rt, args.steps, args.warmup)
+        return ("FP8 MoE decode GEMV HBM GB/s", r,
+                cpu_moe_decode(lib) if cpu_leg else None)
+    if name == "dense_gemv":
+        r = bench_dense_gemv(lib, pkg, rt, args.steps, args.warmup, M=args.m)
+        return ("FP8 dense decode GEMV HBM GB/s", r,
+                cpu_dense_gemv(lib, M=args.m) if cpu_leg else None)
+    if name in PREFILL:
+        steps = args.prefill_steps if args.prefill_steps else args.steps
+        r = bench_prefill(lib, pkg, rt, steps, min(args.warmup, 2), name)
+        return ("prefill grouped-GEMM TFLOP/s", r,
+                cpu_moe_prefill(lib, PREFILL[name]["layers"], PREFILL[name]["T"])
+                if cpu_leg else None)
+    r = bench_copy(rt, args.steps, args.warmup)
+    return ("device copy HBM GB/s (read + write)", r, None)
+
+
+def line_of(metric, r, cpu, steps, warmup):
+    line = {
+        "metric": metric,
+        "value": round(r["value"], 2),
+        "unit": r.get("unit", "GB/s"),
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(r["ms_per_step"], 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (include/apus_synth.h generator, seeded)",
+        "config": r["config"],
+        "roofline": roofline_of(r),
+        "cpu_baseline": cpu,
+    }
+    if "hbm_gbs" in r:
+        line["hbm"] = {"achieved": round(r["hbm_gbs"], 2), "peak": HBM_PEAK_GBS,
+                       "unit": "GB/s", "frac": round(r["hbm_gbs"] / HBM_PEAK_GBS, 4),
+                       "algorithmic_bytes_per_step": r["bytes"]}
+    return line
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -468,8 +539,13 @@ def main():
                     choices=["moe_decode", "dense_gemv", "prefill_zipf",
                              "prefill_stack", "copy"])
     ap.add_argument("--m", type=int, default=1, help="dense_gemv rows (1, 2, 4)")
+    ap.add_argument("--prefill-steps", type=int, default=0,
+                    help="steps of the prefill workloads (default: --steps; "
+                         "5 when they run as the metric's second half)")
     ap.add_argument("--no-cpu", action="store_true",
                     help="skip the CPU baseline leg")
+    ap.add_argument("--no-prefill", action="store_true",
+                    help="moe_decode only: skip the prefill half of the metric")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -481,63 +557,24 @@ def main():
     err = ctypes.create_string_buffer(256)
     pkg.check(lib.apus_ghip_enable(err, 256), "apus_ghip_enable")
 
-    if args.workload == "moe_decode":
-        r = bench_moe_decode(lib, pkg, rt, args.steps, args.warmup)
-        metric = "FP8 MoE decode GEMV HBM GB/s"
-        cpu = None if args.no_cpu else cpu_moe_decode(lib)
-    elif args.workload == "dense_gemv":
-        r = bench_dense_gemv(lib, pkg, rt, args.steps, args.warmup, M=args.m)
-        metric = "FP8 dense decode GEMV HBM GB/s"
-        cpu = None if args.no_cpu else cpu_dense_gemv(lib, M=args.m)
-    elif args.workload in PREFILL:
-        r = bench_prefill(lib, pkg, rt, args.steps, args.warmup, args.workload)
-        metric = "prefill grouped-GEMM TFLOP/s"
-        cpu = None if args.no_cpu else cpu_moe_prefill(
-            lib, PREFILL[args.workload]["layers"], PREFILL[args.workload]["T"])
-    else:
-        r = bench_copy(rt, args.steps, args.warmup)
-        metric = "device copy HBM GB/s (read + write)"
-        cpu = None
-    traffic = traffic_from_profiles(r["kernel"])
-    mfma = r.get("unit") == "TFLOP/s"
-    if mfma:
-        achieved = r["kernel_flops"] / (r["kernel_ms"] * 1e-3) / 1e12
-    else:
-        achieved = r["kernel_bytes"] / (r["kernel_ms"] * 1e-3) / 1e9
-    line = {
-        "metric": metric,
-        "value": round(r["value"], 2),
-        "unit": r.get("unit", "GB/s"),
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(r["ms_per_step"], 6),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (include/apus_synth.h generator, seeded)",
-        "config": r["config"],
-        "roofline": {
-            "bound": "mfma" if mfma else "hbm",
-            "kernel": r["kernel"],
-            "achieved": round(achieved, 2),
-            "peak": BF16_PEAK_TFLOPS if mfma else HBM_PEAK_GBS,
-            "unit": "TFLOP/s" if mfma else "GB/s",
-            "frac": round(achieved / (BF16_PEAK_TFLOPS if mfma else HBM_PEAK_GBS), 4),
-            "traffic": traffic,
-            "algorithmic_bytes_per_launch": r["kernel_bytes"],
-            "algorithmic_flops_per_launch": r["kernel_flops"],
-            "avg_launch_ms": round(r["kernel_ms"], 6),
-            "launch_ms": r["launch_ms"],
-            "mfma_tflops": round(r["kernel_flops"] / (r["kernel_ms"] * 1e-3) / 1e12, 3),
-        },
-        "cpu_baseline": cpu,
-    }
-    if "hbm_gbs" in r:
-        line["hbm"] = {"achieved": round(r["hbm_gbs"], 2), "peak": HBM_PEAK_GBS,
-                       "unit": "GB/s", "frac": round(r["hbm_gbs"] / HBM_PEAK_GBS, 4),
-                       "algorithmic_bytes_per_step": r["bytes"]}
+    metric, r, cpu = run_workload(args.workload, lib, pkg, rt, args, not args.no_cpu)
+    print("bench: %s done (%.4f ms/step)" % (args.workload, r["ms_per_step"]),
+          file=sys.stderr, flush=True)
+    line = line_of(metric, r, cpu, args.steps, args.warmup)
+    if args.workload == "moe_decode" and not args.no_prefill:
+        # the metric's second half ("...; prefill grouped-GEMM
+        # TFLOP/s (%MFMA)"): configs 4 and 3, each a full step of its own
+        if not args.prefill_steps:
+            args.prefill_steps = 5
+        line["prefill"] = []
+        for name in ("prefill_stack", "prefill_zipf"):
+            m2, r2, _ = run_workload(name, lib, pkg, rt, args, False)
+            c2 = (cpu_moe_prefill(lib, PREFILL[name]["layers"], PREFILL[name]["T"], cpu)
+                  if cpu else None)
+            line["prefill"].append(line_of(m2, r2, c2, args.prefill_steps,
+                                           min(args.warmup, 2)))
+            print("bench: %s done (%.4f ms/step)" % (name, r2["ms_per_step"]),
+                  file=sys.stderr, flush=True)
     print(json.dumps(line))
 
 
