@@ -398,11 +398,17 @@ def bench_prefill(lib, pkg, rt, steps, warmup, name):
     flops = L * P * 2 * 3 * inter * dim
     nbytes = sum(touched) * slab + L * (2 * T * dim * 2 + P * 8)
     gu_flops = P * 2 * 2 * inter * dim
+    # gate/up launch bytes: the touched experts' gate and up members, the
+    # gathered x rows (one per pair) and the BF16 h rows it writes
+    nb = lambda n: (n + 127) // 128  # noqa: E731
+    gu_member = 2 * (inter * dim + nb(inter) * nb(dim) * 4)
+    gu_bytes = sum(touched) // L * gu_member + P * dim * 2 + P * inter * 2
     return {
         "ms_per_step": ms, "value": flops / (ms * 1e-3) / 1e12, "unit": "TFLOP/s",
         "bytes": nbytes, "flops": flops, "kernel": "k_pf_gemm_gateup",
         "kernel_ms": kt["k_pf_gemm_gateup"], "kernel_flops": gu_flops,
-        "kernel_bytes": None, "launch_ms": {n_: round(v, 5) for n_, v in kt.items()},
+        "kernel_bytes": gu_bytes, "traffic_key": "k_pf_gemm_gateup@" + name,
+        "launch_ms": {n_: round(v, 5) for n_, v in kt.items()},
         "hbm_gbs": nbytes / (ms * 1e-3) / 1e9,
         "config": {"workload": "%s (%s)" % (name, cfg["desc"]), "layers": L,
                    "experts": E, "topk": k, "dim": dim, "inter": inter,
@@ -462,7 +468,7 @@ def bench_copy(rt, steps, warmup, nbytes=256 << 20):
 # --------------------------------------------------------------------------
 
 def roofline_of(r):
-    traffic = traffic_from_profiles(r["kernel"])
+    traffic = traffic_from_profiles(r.get("traffic_key", r["kernel"]))
     mfma = r.get("unit") == "TFLOP/s"
     if mfma:
         achieved = r["kernel_flops"] / (r["kernel_ms"] * 1e-3) / 1e12
