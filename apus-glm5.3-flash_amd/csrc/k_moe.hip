@@ -1,25 +1,28 @@
 /*
- * k_moe.hip — K3: routed-MoE decode for one token (gfx950), two launches on
- * one stream, no inter-workgroup waits:
+ * k_moe.hip — K3: routed-MoE decode for one token (gfx950).
  *
- *   k_moe_gateup  routing first (one wave per workgroup: the harness
- *                 routing -- stable top-k of f32 logits, ties -> lower id,
- *                 softmax over the k selected -- or given idx/w,
- *                 deduplicated keeping the first slot of a repeated id,
- *                 c/gmoe.h:309-312, sorted by id; workgroup 0 publishes the
- *                 record), then per (slot q, 16 rows) the g and u GEMVs
- *                 over dim with the FP8 dequant fused (bit-exact weights)
- *                 and the SwiGLU epilogue of c/gmoe.h:217-225 -> h[q].
- *   k_moe_down    one workgroup per 16 output rows: wave q computes expert
- *                 q's down GEMV (h[q] . Wd^T, full inter in-wave), then the
- *                 ascending-expert combine y = bf16(y + bf16(bf16(o)*w))
- *                 (c/gmoe.h:307-320) runs in-workgroup -- no atomics, no
- *                 cross-workgroup reduction, deterministic.
+ * Three phases, shared by both launch forms:
+ *   route    one wave: the harness routing (stable top-k of f32 logits,
+ *            ties -> lower id, softmax over the k selected) or given idx/w,
+ *            a repeated id keeping its first slot (c/gmoe.h:309-312), kept
+ *            slots sorted by id; workgroup 0 publishes the record.
+ *   gate/up  per (slot q, 16 rows) the g and u GEMVs over dim with the FP8
+ *            dequant fused (bit-exact weights) and the SwiGLU epilogue of
+ *            c/gmoe.h:217-225 -> h[q].
+ *   down     per 16 output rows: wave q computes slot q's down GEMV
+ *            (h[q] . Wd^T, full inter in-wave), then the ascending-expert
+ *            combine y = bf16(y + bf16(bf16(o)*w)) (c/gmoe.h:307-320) runs
+ *            in-workgroup -- no float atomics, no cross-workgroup
+ *            reduction, deterministic.
  *
- * A single persistent launch with completion counters was tried first: its
- * agent-scope release/acquire fences (an L2 write-back / invalidate per wave
- * per tile) cost ~10x the weight streaming, so the phases are split at a
- * kernel boundary, which orders the h and routing handoff for free.
+ * k_moe_fused runs all three in one persistent launch (up to 8 kept slots):
+ * h crosses the device through agent-scope atomic stores and loads and one
+ * monotone arrival counter with a bounded wait. Release/acquire fences are
+ * avoided on purpose: on gfx950 each one is an L2 write-back or invalidate,
+ * which cost ~10x the weight streaming in a first fenced version.
+ * k_moe_gateup + k_moe_down are the two-launch form (more than 8 slots, or
+ * a store without the arrival counter): the kernel boundary orders the h
+ * handoff.
  *
  * Weight streaming: each wave pulls its 16-row chunks (128-wide k, one
  * scale block) through a wave-private LDS ring with direct global->LDS

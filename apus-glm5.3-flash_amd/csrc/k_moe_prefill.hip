@@ -19,19 +19,18 @@
  *                 bf16(O[s] * w) over the token's pairs (c/gmoe.h:307-320).
  *
  * GEMM tile (both modes). A workgroup of 4 waves owns one tile of up to 256
- * expert-sorted rows and one column block; K is walked in 128-wide steps,
- * one F32 scale block. Each wave owns two 32-column weight slots (gate and
- * up columns [c, c+32) in mode 0, so the SwiGLU epilogue is lane-local; two
- * 128-apart down column groups in mode 1) for all tile rows, accumulating
- * 2 x 8 v_mfma_f32_32x32x16_bf16 blocks (256 fp32 per lane) in AGPRs.
- * FP8 weights go straight from HBM into registers in the MFMA B layout
- * (lane (n, h) holds weight row n, codes [64h, 64h+64) of the step) and are
- * dequantized there, bit-exact (bf16_rne(e4m3 * scale), c/fp8blk.h:115-136).
- * The activation tile is gathered into LDS, double-buffered, one barrier
- * per step. MFMA k-step s takes codes [64h + 8s, +8) of lane half h and the
- * A operand is read with the same mapping: a permutation of k inside the
- * 128-block, identical for A and B. 32-row blocks past the tile's row count
- * skip their MFMAs, so ragged experts cost what their rows need.
+ * expert-sorted rows and one column block; K is walked in 64-wide stages
+ * (half an F32 scale block). Each wave owns two 32-column weight slots (gate
+ * and up columns [c, c+32) in mode 0, so the SwiGLU epilogue is lane-local;
+ * two 128-apart down column groups in mode 1) for all tile rows,
+ * accumulating 2 x NRB v_mfma_f32_32x32x16_bf16 blocks in AGPRs. Both
+ * operands stream HBM -> LDS by direct DMA (global_load_lds) through a ring
+ * of stages, the activation rows gathered by token in mode 0; the FP8 codes
+ * are dequantized in registers when read from LDS, bit-exact
+ * (bf16_rne(e4m3 * scale), c/fp8blk.h:115-136). MFMA step s of lane half h
+ * takes k = 32h + 8s + [0, 8) of the stage from both operands. 32-row blocks
+ * past the tile's row count are neither loaded nor computed, so ragged
+ * experts cost what their rows need.
  *
  * The GEMM grid is persistent and XCD-aware: one workgroup per CU;
  * hardware deals workgroups to the 8 XCDs round-robin, so workgroup b
