@@ -43,6 +43,8 @@
 #include "ghip_device.h"
 #include "ghip_internal.h"
 
+#include <type_traits>
+
 typedef float ghip_f32x16 __attribute__((ext_vector_type(16)));
 
 #define PF_CHUNK 1024            /* pairs per permutation workgroup */
@@ -52,7 +54,9 @@ typedef float ghip_f32x16 __attribute__((ext_vector_type(16)));
 #define PF_A_STAGE (PF_BM * PF_BK * 2)          /* 32 KB activation tile */
 #define PF_W_STAGE (256 * PF_BK)                /* 16 KB FP8 weight rows */
 #define PF_STAGE (PF_A_STAGE + PF_W_STAGE)
-#define PF_LDS (3 * PF_STAGE)                   /* 144 KB ring */
+#define PF_RING (3 * PF_STAGE)                  /* 144 KB ring */
+#define PF_SCT_MAX 128           /* k blocks in the per-tile scale table (K <= 16384) */
+#define PF_LDS (PF_RING + PF_SCT_MAX * 8)       /* ring + scale table */
 #define PF_MAXK 16               /* max top-k per token */
 #define PF_MAXE 1024             /* max experts in a bank */
 
@@ -223,36 +227,48 @@ struct PfTile {
  * are neither loaded nor computed; rows past `rows` inside the last block
  * repeat the last row: computed, never stored).
  *
- * K advances in stages of 64 through a 3-deep LDS ring filled by direct
- * global->LDS loads (no register staging): stage load j+2 is in flight
- * while stage j is computed. Stage layout, 16-byte pieces XOR-swizzled so
- * the MFMA operand reads hit distinct banks:
- *   A  [256 rows][8 pieces]  piece p of row r at (p ^ ((r >> 1) & 7))
- *   W  [256 rows][4 pieces]  weight row wr = 64*wave + 32*slot + n,
- *                            piece p at (p ^ ((wr >> 2) & 3))
+ * K advances in stages of 64 through an NS-deep LDS ring filled by direct
+ * global->LDS loads (no register staging). Stage layout, 16-byte pieces
+ * XOR-swizzled so the MFMA operand reads hit distinct banks:
+ *   A  [NRB*32 rows][8 pieces]  piece p of row r at (p ^ ((r >> 1) & 7))
+ *   W  [256 rows][4 pieces]     weight row wr = 64*wave + 32*slot + n,
+ *                               piece p at (p ^ ((wr >> 2) & 3))
  * Inside a stage, lane half h owns k in [32h, 32h+32); MFMA step s takes
- * k = 32h + 8s + [0, 8) from both operands. */
+ * k = 32h + 8s + [0, 8) from both operands.
+ *
+ * Software pipeline: the operands of step s+1 (A rows from LDS, B codes
+ * dequantized in registers) are prepared while step s's 16 MFMAs run. The
+ * stage barrier sits inside the last step of a stage: by then every wave
+ * holds that step's operands in registers, so the barrier (a) lets the
+ * freed buffer be refilled at once, keeping all NS stages in flight, and
+ * (b) is followed by MFMA work that hides the latency of the next stage's
+ * first LDS reads. Scales come from the per-tile table in LDS (sct: one
+ * {slot 0, slot 1} pair per 128-wide k block), not from memory. */
 template <int MODE, int NRB, bool EXACT>
-__device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds) {
+__device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
+                                        const ghip_f32x2 *sct) {
     constexpr uint32_t LPS = NRB + 4;            /* DMA loads per thread per stage */
-    /* ring depth: as many stages as the LDS holds, so tiles with few rows
+    /* ring depth: as many stages as the ring holds, so tiles with few rows
      * keep more weight bytes in flight (3, 4, 6, 7 stages for 8, 4, 2, 1
      * row blocks) */
     constexpr uint32_t ASTG = NRB * 32 * PF_BK * 2;
     constexpr uint32_t STG = ASTG + PF_W_STAGE;
-    constexpr uint32_t NS = PF_LDS / STG < 8 ? PF_LDS / STG : 8;
-    static_assert(NS >= 3 && LPS * (NS - 2) <= 63, "ring depth vs vmcnt range");
+    constexpr uint32_t NS = PF_RING / STG < 8 ? PF_RING / STG : 8;
+    static_assert(NS >= 2 && LPS * (NS - 1) <= 63, "ring depth vs vmcnt range");
     /* opaque thread id: keeps the lane-derived address math of this body
      * inside the persistent item loop instead of hoisted and held live
      * across items for every body */
     uint32_t tid = threadIdx.x;
     asm volatile("" : "+v"(tid));
-    const uint32_t wv = tid >> 6, lane = tid & 63;
+    const uint32_t lane = tid & 63;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t n = lane & 31, h = lane >> 5;
     const uint32_t K = t.K, nst = K / PF_BK;
 
-    /* --- DMA source addresses (stage 0); stage j adds j*64 elements ---- */
-    const uint8_t *asrc[NRB];
+    /* --- DMA sources: a wave-uniform base (SGPRs; stage j adds j*64
+     * elements) plus a 32-bit per-lane offset, so each load is one
+     * SGPR-based global_load_lds with no per-load 64-bit address math ---- */
+    uint32_t aofs[NRB];
 #pragma unroll
     for (int i = 0; i < NRB; i++) {
         const uint32_t r = 32 * i + 8 * wv + (lane >> 3);
@@ -260,25 +276,41 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds) {
         const uint32_t src = MODE == 0 ? (uint32_t)t.perm[t.row0 + rc] / t.topk
                                        : t.row0 + rc;
         const uint32_t p = (lane & 7) ^ ((r >> 1) & 7);
-        asrc[i] = (const uint8_t *)(t.act + (size_t)src * K) + 16 * p;
+        aofs[i] = src * K * 2u + 16u * p;
     }
-    const uint8_t *wsrc[4];
+    /* weight load i of wave wv, lane l: LDS weight row 64i + 16wv + l/4,
+     * i.e. slot (wv >> 1) & 1 (uniform), column 32i + 16(wv & 1) + l/4 of
+     * that slot's block, piece (l & 3) ^ ((l >> 4) & 3) */
+    const uint32_t wslot = (wv >> 1) & 1u;
+    const uint8_t *wbase = (wslot ? t.w1 : t.w0) + (size_t)(wslot ? t.cb1 : t.cb0) * K;
+    uint32_t wofs[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const uint32_t wr = 64 * i + 16 * wv + (lane >> 2);
-        const uint32_t w = wr >> 6, j = (wr >> 5) & 1, nn = wr & 31;
-        const uint32_t col = (j ? t.cb1 : t.cb0) + 32 * w + nn;
-        const uint32_t p = (lane & 3) ^ ((wr >> 2) & 3);
-        wsrc[i] = (j ? t.w1 : t.w0) + (size_t)col * K + 16 * p;
+        const uint32_t col = 32u * i + 16u * (wv & 1u) + (lane >> 2);
+        wofs[i] = col * K + 16u * ((lane & 3u) ^ ((lane >> 4) & 3u));
     }
-    auto issue = [&](uint32_t j) {
-        uint8_t *st = lds + (j % NS) * STG;
+    const uint8_t *abase = (const uint8_t *)t.act;
+    /* part P (of 4) of stage j's loads into ring buffer b % NS: load q of
+     * the stage (A rows q < NRB, weight rows NRB + i) when q % 4 == P, so a
+     * stage's LPS loads spread over the four MFMA steps of the stage before
+     * it instead of queueing behind each other at one point */
+    auto issue_part = [&](auto part_c, uint32_t j, uint32_t b) {
+        constexpr int P = decltype(part_c)::value;
+        uint8_t *st = lds + (b % NS) * STG;
+        const uint8_t *aj = abase + (size_t)j * PF_BK * 2;
+        const uint8_t *wj = wbase + (size_t)j * PF_BK;
 #pragma unroll
         for (int i = 0; i < NRB; i++)
-            ghip_dma16(asrc[i] + (size_t)j * PF_BK * 2, st + (4 * i + wv) * 1024);
+            if (i % 4 == P) ghip_dma16(aj + aofs[i], st + (4 * i + wv) * 1024);
 #pragma unroll
         for (int i = 0; i < 4; i++)
-            ghip_dma16(wsrc[i] + (size_t)j * PF_BK, st + ASTG + (4 * i + wv) * 1024);
+            if ((NRB + i) % 4 == P) ghip_dma16(wj + wofs[i], st + ASTG + (4 * i + wv) * 1024);
+    };
+    auto issue = [&](uint32_t j, uint32_t b) {
+        issue_part(std::integral_constant<int, 0>{}, j, b);
+        issue_part(std::integral_constant<int, 1>{}, j, b);
+        issue_part(std::integral_constant<int, 2>{}, j, b);
+        issue_part(std::integral_constant<int, 3>{}, j, b);
     };
 
     /* --- operand read offsets inside a stage --------------------------- */
@@ -299,62 +331,126 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds) {
 #pragma unroll
         for (int i = 0; i < 16; i++) { a0[rb][i] = 0.0f; a1[rb][i] = 0.0f; }
 
+    /* prologue: NS - 1 buffers in flight (a tile shorter than the ring
+     * fills the spare buffers with copies of its last stage, so every wait
+     * count below is one constant), then stage 0's step-0 operands; stage
+     * j's steps load stage j + NS - 1 into the buffer freed by stage j - 1 */
 #pragma unroll
     for (uint32_t i = 0; i + 1 < NS; i++)
-        if (i < nst) issue(i);
-    for (uint32_t j = 0; j < nst; j++) {
-        /* own DMA for stage j done (later stages may stay in flight), then a
-         * bare barrier: every wave's stage-j writes have landed and every
-         * wave is done reading buffer (j-1) % NS, refilled next. No fence:
-         * a fence would drain the whole DMA stream at each stage. */
-        const uint32_t later = nst - 1 - j;
-        ghip_wait_stages<LPS, NS - 2>(later);
-        __builtin_amdgcn_s_barrier();
-        if (j + NS - 1 < nst) issue(j + NS - 1);
-        const uint8_t *st = lds + (j % NS) * STG;
-        /* wave-uniform scale reads through the constant address space:
-         * scalar loads (lgkmcnt), so they never wait behind the DMA stream */
-        const float sc0 = ((const __attribute__((address_space(4))) float *)t.sr0)[j >> 1];
-        const float sc1 = ((const __attribute__((address_space(4))) float *)t.sr1)[j >> 1];
-        /* operands one MFMA step ahead: A rows of step s+1 and the dequant
-         * of B for step s+1 are in flight while step s's MFMAs run */
-        ghip_u32x4 q0[2], q1[2];
+        issue(i < nst ? i : nst - 1, i);      /* i >= nst: an unused buffer */
+    GHIP_VMCNT(LPS * (NS - 2));
+    __builtin_amdgcn_s_waitcnt(0xc07f);          /* lgkmcnt(0): scale table */
+    __builtin_amdgcn_s_barrier();
+    ghip_u32x4 q0[2], q1[2];
+    ghip_f32x2 sc;
+    ghip_bf16x8 av[NRB], an[NRB], b0, b1, nb0, nb1;
+    {
+        const uint8_t *st = lds;
+        sc = sct[0];
 #pragma unroll
         for (int u = 0; u < 2; u++) {
             q0[u] = *(const ghip_u32x4 *)(st + boff0[u]);
             q1[u] = *(const ghip_u32x4 *)(st + boff1[u]);
         }
-        ghip_bf16x8 av[NRB], an[NRB];
 #pragma unroll
         for (int rb = 0; rb < NRB; rb++)
             av[rb] = *(const ghip_bf16x8 *)(st + rb * 32 * 128 + aoff[0]);
-        ghip_bf16x8 b0 = pf_deq8<EXACT>(q0[0][0], q0[0][1], sc0);
-        ghip_bf16x8 b1 = pf_deq8<EXACT>(q1[0][0], q1[0][1], sc1);
+        b0 = pf_deq8<EXACT>(q0[0][0], q0[0][1], sc[0]);
+        b1 = pf_deq8<EXACT>(q1[0][0], q1[0][1], sc[1]);
+    }
+
+    /* one stage; NEXT: stage j+1 exists (its barrier, the refill of the
+     * freed buffer and its step-0 reads run in step 3). Branch-free inside,
+     * so each step is one scheduling region in which the next operands' LDS
+     * reads and dequant interleave with the MFMAs. Past the last stage the
+     * refill re-reads stage nst-1 (L2-hot) into the freed buffer, which no
+     * later stage of the tile reads: the wait counts stay uniform and the
+     * loop needs no second variant. */
+    auto stage = [&](uint32_t j, auto next_c) {
+        constexpr bool NEXT = decltype(next_c)::value;
+        const uint8_t *st = lds + (j % NS) * STG;
+        /* the stage loaded during this one (a copy of the last stage past
+         * the end: its buffer, freed by stage j - 1, is read by no later
+         * stage of the tile) */
+        const uint32_t ld = j + NS - 1 < nst ? j + NS - 1 : nst - 1;
+        const uint32_t lb = j + NS - 1;
 #pragma unroll
         for (int s = 0; s < 4; s++) {
-            ghip_bf16x8 nb0 = b0, nb1 = b1;
+            if (s == 0) issue_part(std::integral_constant<int, 0>{}, ld, lb);
+            if (s == 1) issue_part(std::integral_constant<int, 1>{}, ld, lb);
+            if (s == 2) issue_part(std::integral_constant<int, 2>{}, ld, lb);
+            if (s == 3) issue_part(std::integral_constant<int, 3>{}, ld, lb);
             if (s < 3) {
+                /* step s+1 of this stage: A rows from LDS, B codes already
+                 * in registers */
                 const int u = (s + 1) >> 1, v = 2 * ((s + 1) & 1);
 #pragma unroll
                 for (int rb = 0; rb < NRB; rb++)
                     an[rb] = *(const ghip_bf16x8 *)(st + rb * 32 * 128 + aoff[s + 1]);
-                nb0 = pf_deq8<EXACT>(q0[u][v], q0[u][v + 1], sc0);
-                nb1 = pf_deq8<EXACT>(q1[u][v], q1[u][v + 1], sc1);
+                nb0 = pf_deq8<EXACT>(q0[u][v], q0[u][v + 1], sc[0]);
+                nb1 = pf_deq8<EXACT>(q1[u][v], q1[u][v + 1], sc[1]);
+            } else if (NEXT) {
+                /* stage barrier: own DMA for stage j+1 done (later stages
+                 * may stay in flight), own reads of stage j done; then a
+                 * bare barrier (no fence: a fence would drain the DMA
+                 * ring) after which buffer j % NS is free for stage j+NS.
+                 * NS + j stages' worth of loads are issued by now, in
+                 * order; stage j+1 is the (j+2)-th */
+                GHIP_VMCNT(LPS * (NS - 2));
+                __builtin_amdgcn_s_waitcnt(0xc07f);
+                __builtin_amdgcn_s_barrier();
+                __builtin_amdgcn_sched_barrier(0);
+                const uint8_t *sn = lds + ((j + 1) % NS) * STG;
+                sc = sct[(j + 1) >> 1];
+#pragma unroll
+                for (int u = 0; u < 2; u++) {
+                    q0[u] = *(const ghip_u32x4 *)(sn + boff0[u]);
+                    q1[u] = *(const ghip_u32x4 *)(sn + boff1[u]);
+                }
+#pragma unroll
+                for (int rb = 0; rb < NRB; rb++)
+                    an[rb] = *(const ghip_bf16x8 *)(sn + rb * 32 * 128 + aoff[0]);
+                nb0 = pf_deq8<EXACT>(q0[0][0], q0[0][1], sc[0]);
+                nb1 = pf_deq8<EXACT>(q1[0][0], q1[0][1], sc[1]);
             }
 #pragma unroll
             for (int rb = 0; rb < NRB; rb++) {
                 a0[rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[rb], b0, a0[rb], 0, 0, 0);
                 a1[rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[rb], b1, a1[rb], 0, 0, 0);
             }
-            /* let the scheduler interleave the LDS reads of step s+1 with
-             * step s's MFMAs (small-GEMM interleave strategy) */
-            __builtin_amdgcn_iglp_opt(0);
+            /* interleave the next step's LDS reads and dequant (and, at a
+             * stage boundary, the DMA refill) between this step's MFMAs */
+            if (s == 3 && NEXT) {
+                /* 5 + NRB LDS reads (scales, B codes, A rows), then the
+                 * dequant of the next step's B */
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   /* MFMA */
+                    if (i < 2) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0); /* DS read */
+                    if (i == 2) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    if (i >= 3 && i < 3 + NRB) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    if (i >= 5) __builtin_amdgcn_sched_group_barrier(0x002, 4, 0); /* VALU */
+                }
+            } else if (s < 3) {
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    if (i < NRB) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+                }
+            }
+            /* step boundary: a scheduling region per step, so the next
+             * step's reads stay between this step's MFMAs instead of being
+             * pulled down next to their consumers */
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int rb = 0; rb < NRB; rb++) av[rb] = an[rb];
             b0 = nb0;
             b1 = nb1;
         }
-    }
+    };
+    for (uint32_t j = 0; j + 1 < nst; j++) stage(j, std::true_type{});
+    stage(nst - 1, std::false_type{});
 
     /* epilogue: lane (n, h), register i of row block rb holds output row
      * rb*32 + 8*(i/4) + 4*h + i%4, column n of each slot */
@@ -430,16 +526,29 @@ __global__ __launch_bounds__(256, 1) void k_pf_gemm(
             t.sr0 = (const float *)(slab + bank.off_ds) + (size_t)(2 * nb) * nkb;
             t.sr1 = (const float *)(slab + bank.off_ds) + (size_t)(2 * nb + 1) * nkb;
         }
+        /* the tile's scale table: {slot 0, slot 1} per k block, written
+         * here and made visible by the body's prologue barrier (the previous
+         * item's trailing barrier ordered all reads of the old table) */
+        ghip_f32x2 *sct = (ghip_f32x2 *)(pf_lds + PF_RING);
+        for (uint32_t b = threadIdx.x; b < nkb; b += 256) {
+            ghip_f32x2 v;
+            v[0] = t.sr0[b];
+            v[1] = t.sr1[b];
+            sct[b] = v;
+        }
         const uint32_t nrb = (t.rows + 31) >> 5;
-        if (bank.nan_flags && bank.nan_flags[e]) pf_tile<MODE, PF_RB, true>(t, pf_lds);
-        else if (nrb > 4) pf_tile<MODE, 8, false>(t, pf_lds);
-        else if (nrb > 2) pf_tile<MODE, 4, false>(t, pf_lds);
-        else if (nrb > 1) pf_tile<MODE, 2, false>(t, pf_lds);
-        else              pf_tile<MODE, 1, false>(t, pf_lds);
+        if (bank.nan_flags && bank.nan_flags[e]) pf_tile<MODE, PF_RB, true>(t, pf_lds, sct);
+        else if (nrb > 4) pf_tile<MODE, 8, false>(t, pf_lds, sct);
+        else if (nrb > 2) pf_tile<MODE, 4, false>(t, pf_lds, sct);
+        else if (nrb > 1) pf_tile<MODE, 2, false>(t, pf_lds, sct);
+        else              pf_tile<MODE, 1, false>(t, pf_lds, sct);
         /* every wave is done with the LDS ring before the next item's
          * prologue refills it */
         __builtin_amdgcn_s_barrier();
     }
+    /* the last tile's trailing refills land before the workgroup's LDS is
+     * released */
+    GHIP_VMCNT(0);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -519,6 +628,7 @@ extern "C" hipError_t ghip_launch_moe_prefill(const GhipBank *bank,
     if (topk <= 0 || topk > PF_MAXK || E == 0 || E > PF_MAXE)
         return hipErrorInvalidValue;
     if (dim == 0 || inter == 0 || dim % 256 || inter % 128) return hipErrorInvalidValue;
+    if (dim / 128 > PF_SCT_MAX || inter / 128 > PF_SCT_MAX) return hipErrorInvalidValue;
     const size_t P = T * (size_t)topk;
     if (P > ws->cap_pairs || P > 0x7fffffffu) return hipErrorInvalidValue;
     if (ws->n_cu == 0 || ws->n_cu % 8) return hipErrorInvalidValue;
