@@ -57,6 +57,7 @@ SIGNATURES = {
     "apus_ghip_store_put": (c_int, [c_vp, c_int, c_vp, c_size]),
     "apus_ghip_store_synth": (c_int, [c_vp, c_u64, c_int, c_float, c_float]),
     "apus_ghip_store_slab_dev": (c_vp, [c_vp, c_int]),
+    "apus_ghip_store_get": (c_int, [c_vp, c_int, c_vp, c_size]),
     "apus_ghip_store_expert_bf16": (c_int, [c_vp, c_int, c_vp]),
     "apus_ghip_moe_decode": (c_int, [c_vp, c_vp, c_vp, c_vp, c_int, c_vp]),
     "apus_ghip_moe_decode_dev": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_int,

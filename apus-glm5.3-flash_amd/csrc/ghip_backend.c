@@ -137,6 +137,9 @@ static int ghip_init(void) {
     G.n_cu = (uint32_t)((ncu + 7) / 8 * 8);
     HIPCHK(ghip_moe_decode_init());
     HIPCHK(ghip_linear_init(G.n_cu));
+    HIPCHK(ghip_moe_prefill_init());
+    G.pf.n_cu = G.n_cu;
+    G.pf_inited = 1;
     HIPCHK(hipMalloc((void **)&G.d_flag, 256));
     HIPCHK(hipMalloc((void **)&G.d_flags, GHIP_SCAN_SLOTS * sizeof(uint32_t)));
     HIPCHK(hipMemset(G.d_flags, 0, GHIP_SCAN_SLOTS * sizeof(uint32_t)));
@@ -642,6 +645,26 @@ int apus_ghip_store_put(ApusGhipStore *s, int expert, const void *slab,
     G.h2d += s->h_bytes;
     if (store_scan(s, expert, G.stream)) return 1;
     HIPCHK(hipStreamSynchronize(G.stream));
+    return 0;
+}
+
+int apus_ghip_store_get(ApusGhipStore *s, int expert, void *slab, size_t nbytes) {
+    if (!s || expert < 0 || expert >= s->n_experts || nbytes != s->h_bytes) {
+        ghip_seterr("store_get: bad expert %d or slab size %zu (want %zu)",
+                    expert, nbytes, s ? s->h_bytes : 0);
+        return 1;
+    }
+    /* each member from its 256-byte aligned device offset to its host
+     * (packed) offset: the inverse of apus_ghip_store_put */
+    const uint8_t *b = s->arena + (size_t)expert * s->d_stride;
+    uint8_t *h = (uint8_t *)slab;
+    const size_t hs[7] = { s->h_gw, s->h_gs, s->h_uw, s->h_us, s->h_dw, s->h_ds, s->h_bytes };
+    const size_t ds[6] = { s->d_gw, s->d_gs, s->d_uw, s->d_us, s->d_dw, s->d_ds };
+    for (int i = 0; i < 6; i++)
+        HIPCHK(hipMemcpyAsync(h + hs[i], b + ds[i], hs[i + 1] - hs[i],
+                              hipMemcpyDeviceToHost, G.stream));
+    HIPCHK(hipStreamSynchronize(G.stream));
+    G.d2h += s->h_bytes;
     return 0;
 }
 

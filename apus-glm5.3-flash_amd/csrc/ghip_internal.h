@@ -112,6 +112,18 @@ hipError_t ghip_launch_moe_prefill(const GhipBank *bank, const uint16_t *x,
                                    const GhipMoePrefillWs *ws,
                                    const hipEvent_t *ev, hipStream_t st);
 
+/* Dense FP8-block GEMM on MFMA (the prefill tile body): Y [M, N] =
+ * bf16(X [M, K] . dequant(W [N, K])^T). Shapes it takes: N % 256 == 0,
+ * K % 128 == 0, K <= 16384, 16-byte aligned codes and X
+ * (ghip_fp8_gemm_fits). Persistent grid of at most n_cu workgroups; the
+ * dynamic-LDS limit is raised by ghip_moe_prefill_init. ev: NULL or 2
+ * events. */
+int ghip_fp8_gemm_fits(size_t M, size_t N, size_t K, const void *codes, const void *x);
+hipError_t ghip_launch_fp8_gemm(const uint8_t *codes, const float *scales,
+                                const uint16_t *x, uint16_t *y, size_t M, size_t N,
+                                size_t K, const uint32_t *exact_dev, uint32_t n_cu,
+                                const hipEvent_t *ev, hipStream_t st);
+
 /* Fill n u32 words with value (a kernel, not a memset, so callers may
  * capture it in a graph). */
 hipError_t ghip_launch_fill_u32(uint32_t *p, size_t n, uint32_t value,

@@ -388,6 +388,10 @@ static hipError_t launch_gemv_m(const uint8_t *codes, const float *scales,
     return hipGetLastError();
 }
 
+/* Rows of X from which the FP8 linear runs as one GEMM (below: GEMV passes
+ * of <= 4 rows, each reading the weights once). */
+#define GHIP_GEMM_MIN_M 16
+
 /* Largest dynamic LDS the GEMV stages x into (per workgroup). */
 #define GEMV_LDS_MAX (48u * 1024u)
 
@@ -414,6 +418,11 @@ extern "C" hipError_t ghip_launch_fp8_linear(const uint8_t *codes,
                     (uint32_t)O, (uint32_t)K, nkb);
         return hipGetLastError();
     }
+    /* from GHIP_GEMM_MIN_M rows on, the weights are read once by the MFMA
+     * GEMM instead of once per group of <= 4 rows */
+    if (M >= GHIP_GEMM_MIN_M && g_gs_ncu && ghip_fp8_gemm_fits(M, O, K, codes, x))
+        return ghip_launch_fp8_gemm(codes, scales, x, y, M, O, K, exact_dev, g_gs_ncu, ev,
+                                    st);
     /* m-groups of up to 4 rows, each as large as the x staging allows */
     size_t m0 = 0;
     while (m0 < M) {

@@ -552,6 +552,69 @@ __global__ __launch_bounds__(256, 1) void k_pf_gemm(
 }
 
 /* ------------------------------------------------------------------------ */
+/* dense FP8-block GEMM (the fp8blk_linear hook at M > the GEMV range)      */
+/* ------------------------------------------------------------------------ */
+
+/* Y [M, N] = bf16(X [M, K] . dequant(W [N, K])^T), the composition of
+ * c/gdsa.h:525-534 (dequant_mt then gemm_mt) without the BF16 weight copy:
+ * the MODE-1 tile body above on tiles of 256 rows of X x 256 rows of W (two
+ * 128-row scale blocks). Items (row tile, column block) are dealt so that
+ * XCD x (workgroup b runs on XCD b % 8) owns column blocks x, x + 8, ...
+ * when there are at least 8, sharing each block's weights across its row
+ * tiles in one L2; otherwise it owns row tiles x, x + 8, ... exact_dev:
+ * NULL or a device flag, nonzero when W holds a NaN code (0x7F/0xFF) and
+ * the exact integer decode must be used. */
+__global__ __launch_bounds__(256, 1) void k_fp8_gemm(
+    const uint8_t *__restrict__ codes, const float *__restrict__ scales,
+    const uint16_t *__restrict__ x, uint16_t *__restrict__ y, uint32_t M, uint32_t N,
+    uint32_t K, const uint32_t *__restrict__ exact_dev) {
+    extern __shared__ __attribute__((aligned(1024))) uint8_t pf_lds[];
+    const uint32_t nkb = K >> 7, nblk = N >> 8, tiles = (M + PF_BM - 1) / PF_BM;
+    const bool exact = exact_dev && *exact_dev;
+    /* XCD xcd owns column blocks xcd, xcd + 8, ... (at least 8 of them) or
+     * else row tiles xcd, xcd + 8, ...; its workgroups split the owned
+     * units' items */
+    const uint32_t xcd = blockIdx.x & 7u, c = blockIdx.x >> 3, per = gridDim.x >> 3;
+    const bool colp = nblk >= 8;
+    const uint32_t nu = colp ? nblk : tiles, other = colp ? tiles : nblk;
+    const uint32_t nown = nu > xcd ? (nu - xcd + 7) / 8 : 0;
+    for (uint32_t q = c; q < nown * other; q += per) {
+        const uint32_t own = xcd + 8 * (q / other), o = q % other;
+        const uint32_t nb = colp ? own : o, tile = colp ? o : own;
+        PfTile t;
+        t.act = x;
+        t.perm = nullptr;
+        t.out = y;
+        t.row0 = tile * PF_BM;
+        t.rows = M - t.row0 < PF_BM ? M - t.row0 : PF_BM;
+        t.topk = 1;
+        t.limit = 0.0f;
+        t.K = K;
+        t.N = N;
+        t.cb0 = nb * 256;
+        t.cb1 = nb * 256 + 128;
+        t.w0 = t.w1 = codes;
+        t.sr0 = scales + (size_t)(2 * nb) * nkb;
+        t.sr1 = scales + (size_t)(2 * nb + 1) * nkb;
+        ghip_f32x2 *sct = (ghip_f32x2 *)(pf_lds + PF_RING);
+        for (uint32_t b = threadIdx.x; b < nkb; b += 256) {
+            ghip_f32x2 v;
+            v[0] = t.sr0[b];
+            v[1] = t.sr1[b];
+            sct[b] = v;
+        }
+        const uint32_t nrb = (t.rows + 31) >> 5;
+        if (exact) pf_tile<1, PF_RB, true>(t, pf_lds, sct);
+        else if (nrb > 4) pf_tile<1, 8, false>(t, pf_lds, sct);
+        else if (nrb > 2) pf_tile<1, 4, false>(t, pf_lds, sct);
+        else if (nrb > 1) pf_tile<1, 2, false>(t, pf_lds, sct);
+        else              pf_tile<1, 1, false>(t, pf_lds, sct);
+        __builtin_amdgcn_s_barrier();
+    }
+    GHIP_VMCNT(0);
+}
+
+/* ------------------------------------------------------------------------ */
 /* ordered combine                                                          */
 /* ------------------------------------------------------------------------ */
 
@@ -671,10 +734,35 @@ extern "C" hipError_t ghip_launch_moe_prefill(const GhipBank *bank,
     return hipGetLastError();
 }
 
+extern "C" int ghip_fp8_gemm_fits(size_t M, size_t N, size_t K, const void *codes,
+                                  const void *x) {
+    return M > 0 && M <= 0x7fffffffu && N % 256 == 0 && N <= 0x7fffffffu && K % 128 == 0
+        && K / 128 <= PF_SCT_MAX && K * 2 * (size_t)M <= 0xffffffffull
+        && ((uintptr_t)codes & 15) == 0 && ((uintptr_t)x & 15) == 0;
+}
+
+extern "C" hipError_t ghip_launch_fp8_gemm(const uint8_t *codes, const float *scales,
+                                           const uint16_t *x, uint16_t *y, size_t M,
+                                           size_t N, size_t K, const uint32_t *exact_dev,
+                                           uint32_t n_cu, const hipEvent_t *ev,
+                                           hipStream_t st) {
+    if (!ghip_fp8_gemm_fits(M, N, K, codes, x) || n_cu == 0 || n_cu % 8)
+        return hipErrorInvalidValue;
+    const size_t items = ((M + PF_BM - 1) / PF_BM) * (N / 256);
+    uint32_t g = items < n_cu ? (uint32_t)((items + 7) & ~(size_t)7) : n_cu;
+    hipEvent_t e0 = ev ? ev[0] : nullptr, e1 = ev ? ev[1] : nullptr;
+    GHIP_LAUNCH(e0, e1, k_fp8_gemm, dim3(g), dim3(256), PF_LDS, st, codes, scales, x, y,
+                (uint32_t)M, (uint32_t)N, (uint32_t)K, exact_dev);
+    return hipGetLastError();
+}
+
 extern "C" hipError_t ghip_moe_prefill_init(void) {
     const int lds = PF_LDS;
     hipError_t e = hipFuncSetAttribute((const void *)k_pf_gemm<0>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (e != hipSuccess) return e;
+    e = hipFuncSetAttribute((const void *)k_fp8_gemm,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (e != hipSuccess) return e;
     return hipFuncSetAttribute((const void *)k_pf_gemm<1>,
                                hipFuncAttributeMaxDynamicSharedMemorySize, lds);

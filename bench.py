@@ -9,7 +9,9 @@ bf16 combine). Inputs rotate over R tokens/routings so every step streams
 slabs + x + out + logits = 201,393,280 B) / measured time, in GB/s.
 
 --workload dense_gemv runs config 1 (W [16384,4096] FP8, M in {1,2,4}) over
-rotating weight copies (>= 3x the 256 MB MALL).
+rotating weight copies (>= 3x the 256 MB MALL). --workload dense_gemm runs
+the four DSA FP8 projections at M = 2048 prefill rows (the fp8blk_linear
+hook's MFMA GEMM path), in TFLOP/s.
 
 Prints ONE JSON line (rank 0). Extra objects: "roofline" (dominant kernel,
 HIP-event timed on its stream) and "cpu_baseline" (the reference CPU path,
@@ -313,6 +315,120 @@ def cpu_dense_gemv(lib, M=1, budget_s=10.0):
 
 
 # --------------------------------------------------------------------------
+# FP8-block linear at prefill M (the fp8blk_linear hook's MFMA GEMM path)
+# --------------------------------------------------------------------------
+
+# the DSA projections routed through the hook (c/gdsa.h:599-611,660-661)
+DSA_SHAPES = [("q_a", 1536, 4096), ("q_b", 16384, 1536), ("kv_a", 512, 4096),
+              ("o_proj", 4096, 16384)]
+
+
+def bench_dense_gemm(lib, pkg, rt, steps, warmup, M=2048):
+    """One step = the four DSA FP8 projections of one layer at M prefill
+    rows, each one apus_ghip_fp8blk_linear_dev call (weights resident in
+    HBM, one copy per shape). FLOPs = 2*M*N*K summed; the dominant kernel
+    (roofline) is o_proj's GEMM launch."""
+    seed = 0xD5
+    mats = []
+    for i, (nm, N, K) in enumerate(DSA_SHAPES):
+        nsb = (N // 128) * (K // 128)
+        codes = rt.DevBuf(N * K)
+        pkg.check(lib.apus_synth_fp8_codes_dev(codes.vp, N * K, seed + i, 10, 0, None),
+                  "synth codes")
+        sc = np.empty(nsb, np.float32)
+        lib.apus_synth_scales(sc.ctypes.data_as(ctypes.c_void_p), nsb, seed + i, 11,
+                              1e-4, 1e-2)
+        x = rt.DevBuf(M * K * 2)
+        pkg.check(lib.apus_synth_bf16_normal_dev(x.vp, M * K, seed + i, 12, 0, None),
+                  "synth x")
+        mats.append((nm, N, K, codes, rt.DevBuf.of(sc), x, rt.DevBuf(M * N * 2)))
+    st = rt.Stream()
+
+    def step(_i):
+        for (nm, N, K, codes, d_s, x, y) in mats:
+            rc = lib.apus_ghip_fp8blk_linear_dev(codes.vp, d_s.vp, x.vp, y.vp, M, N, K,
+                                                 0, st.vp)
+            if rc:
+                pkg.check(rc, "fp8blk_linear_dev " + nm)
+
+    for i in range(warmup):
+        step(i)
+    st.synchronize()
+    e0, e1 = rt.Event(), rt.Event()
+    e0.record(st)
+    for i in range(steps):
+        step(warmup + i)
+    e1.record(st)
+    e1.synchronize()
+    ms = e0.elapsed_ms(e1) / steps
+    # per-launch times of each projection (dispatch-packet events)
+    per = {}
+    for (nm, N, K, codes, d_s, x, y) in mats:
+        evs = [[rt.Event() for _ in range(2)] for _ in range(steps)]
+        arr_t = ctypes.c_void_p * 2
+        for i in range(steps):
+            lib.apus_ghip_set_trace_events(arr_t(*[e.handle for e in evs[i]]), 2)
+            pkg.check(lib.apus_ghip_fp8blk_linear_dev(codes.vp, d_s.vp, x.vp, y.vp, M, N,
+                                                      K, 0, st.vp), "linear")
+        lib.apus_ghip_set_trace_events(None, 0)
+        rt.synchronize()
+        per[nm] = sum(ev[0].elapsed_ms(ev[1]) for ev in evs) / steps
+    flops = sum(2 * M * N * K for (_, N, K) in DSA_SHAPES)
+    nbytes = sum(N * K + (N // 128) * (K // 128) * 4 + M * K * 2 + M * N * 2
+                 for (_, N, K) in DSA_SHAPES)
+    No, Ko = DSA_SHAPES[3][1], DSA_SHAPES[3][2]
+    return {
+        "ms_per_step": ms, "value": flops / (ms * 1e-3) / 1e12, "unit": "TFLOP/s",
+        "bytes": nbytes, "flops": flops, "kernel": "k_fp8_gemm",
+        "kernel_ms": per["o_proj"], "kernel_flops": 2 * M * No * Ko,
+        "kernel_bytes": No * Ko + (No // 128) * (Ko // 128) * 4 + M * Ko * 2 + M * No * 2,
+        "traffic_key": "k_fp8_gemm@o_proj",
+        "launch_ms": {n_: round(v, 5) for n_, v in per.items()},
+        "hbm_gbs": nbytes / (ms * 1e-3) / 1e9,
+        "config": {"workload": "dense_gemm (DSA FP8 projections at prefill M, "
+                               "c/gdsa.h:599-611,660-661)", "M": M,
+                   "shapes": {nm: [N, K] for (nm, N, K) in DSA_SHAPES},
+                   "weights": "fp8-e4m3 128x128 blocks"},
+    }
+
+
+def cpu_dense_gemm(lib, M=2048, budget_s=10.0):
+    """The reference's FP8 linear at M rows is dequant_mt + gemm_mt
+    (c/gdsa.h:532-533): timed on a bounded row sample of q_b and converted to
+    TFLOP/s (its cost is linear in M)."""
+    os.environ.setdefault("APUS_THREADS", str(CPU_THREADS))
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    P = O.ptr
+    N, K, Ms = 16384, 1536, 16
+    codes = np.empty((N, K), np.uint8)
+    lib.apus_synth_fp8_codes(P(codes), codes.size, 0xD5, 10, 0)
+    sc = np.empty((N // 128, K // 128), np.float32)
+    lib.apus_synth_scales(P(sc), sc.size, 0xD5, 11, 1e-4, 1e-2)
+    x = np.empty((Ms, K), np.uint16)
+    lib.apus_synth_bf16_normal(P(x), x.size, 0xD5, 12, 0)
+    y = np.empty((Ms, N), np.uint16)
+    use_ref = O.ref_available()
+    n, t = 0, 0.0
+    while t < budget_s and n < 200:
+        t0 = time.perf_counter()
+        if use_ref:
+            O.ref().ref_fp8blk_linear_mt(P(codes), P(sc), P(x), P(y), Ms, N, K)
+        else:
+            O.lib().apo_fp8blk_linear(P(codes), P(sc), P(x), P(y), Ms, N, K, CPU_THREADS)
+        t += time.perf_counter() - t0
+        n += 1
+    tflops = 2 * Ms * N * K / (t / n) / 1e12
+    return {"value": tflops, "unit": "TFLOP/s",
+            "cores": int(os.environ.get("APUS_THREADS", CPU_THREADS)),
+            "kind": "reference" if use_ref else "port",
+            "sample": "%d calls of dequant_mt + gemm_mt on q_b [16384, 1536], %d rows, "
+                      "%.1f ms/call; %d rows of all four projections would take %.1f s"
+                      % (n, Ms, t / n * 1e3, M,
+                         sum(2 * M * N_ * K_ for (_, N_, K_) in DSA_SHAPES) / (tflops * 1e12))}
+
+
+# --------------------------------------------------------------------------
 # configs 3 / 4: routed-MoE prefill (grouped GEMM, MFMA path)
 # --------------------------------------------------------------------------
 
@@ -501,6 +617,10 @@ def run_workload(name, lib, pkg, rt, args, cpu_leg):
         r = bench_dense_gemv(lib, pkg, rt, args.steps, args.warmup, M=args.m)
         return ("FP8 dense decode GEMV HBM GB/s", r,
                 cpu_dense_gemv(lib, M=args.m) if cpu_leg else None)
+    if name == "dense_gemm":
+        r = bench_dense_gemm(lib, pkg, rt, args.steps, args.warmup)
+        return ("FP8 dense linear GEMM TFLOP/s (DSA projections, prefill M)", r,
+                cpu_dense_gemm(lib) if cpu_leg else None)
     if name in PREFILL:
         steps = args.prefill_steps if args.prefill_steps else args.steps
         r = bench_prefill(lib, pkg, rt, steps, min(args.warmup, 2), name)
@@ -542,7 +662,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="moe_decode",
-                    choices=["moe_decode", "dense_gemv", "prefill_zipf",
+                    choices=["moe_decode", "dense_gemv", "dense_gemm", "prefill_zipf",
                              "prefill_stack", "copy"])
     ap.add_argument("--m", type=int, default=1, help="dense_gemv rows (1, 2, 4)")
     ap.add_argument("--prefill-steps", type=int, default=0,

@@ -165,8 +165,14 @@ int apus_ghip_store_put(ApusGhipStore *s, int expert, const void *slab,
  * scales log-uniform in [scale_lo, scale_hi] from the host. */
 int apus_ghip_store_synth(ApusGhipStore *s, uint64_t seed, int bank,
                           float scale_lo, float scale_hi);
-/* Device address of expert e's slab (NULL when out of range). */
+/* Device address of expert e's slab (NULL when out of range): members in
+ * the same order at 256-byte aligned offsets. */
 const void *apus_ghip_store_slab_dev(const ApusGhipStore *s, int expert);
+/* Read expert e's slab back in the host slab format (row-major members,
+ * c/gcache.h:852-861 order): the inverse of apus_ghip_store_put.
+ * Extension; no counterpart in the reference. */
+int apus_ghip_store_get(ApusGhipStore *s, int expert, void *slab,
+                        size_t nbytes);
 /* Dequant-on-fill: expert e's BF16 payload [gate | up | down] into a host
  * buffer (3*inter*dim u16), bitwise c/gcache.h:413-426. */
 int apus_ghip_store_expert_bf16(ApusGhipStore *s, int expert,

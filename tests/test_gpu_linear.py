@@ -96,6 +96,42 @@ def test_fp8_battery(ghip, M, N, K):
                  floor_linear(codes, scales, x), "M%d N%d K%d" % (M, N, K))
 
 
+# prefill-sized M: the MFMA GEMM path (M >= 16, N % 256 == 0, K % 128 == 0),
+# incl. ragged row tiles, K = 128 and K = 16384 (o_proj), the DSA shapes of
+# c/gdsa.h:599-611,660-661 at M = s; M = 15 stays on the GEMV passes
+GEMM = [(16, 512, 4096), (100, 1536, 4096), (300, 2048, 1536), (40, 16384, 1536),
+        (256, 4096, 16384), (513, 256, 128), (15, 512, 1024), (17, 300, 512)]
+
+
+@pytest.mark.parametrize("M,N,K", GEMM)
+def test_fp8_gemm_prefill_shapes(ghip, M, N, K):
+    rng = np.random.default_rng(M * 7919 + N * 13 + K)
+    codes = rng.integers(0, 254, (N, K), dtype=np.uint8)
+    codes[codes >= 0x7F] += 1
+    m = 0.25 + 3.75 * rng.random((O.nblocks(N), O.nblocks(K)))
+    e = rng.integers(-24, 17, m.shape)
+    scales = (np.ldexp(m, e) * rng.choice([-1, 1], m.shape)).astype(np.float32)
+    x = O.f32_to_bf16(rng.uniform(-4, 4, (M, K)).astype(np.float32))
+    want = O.fp8_linear(codes, scales, x, threads=16)
+    got = gpu_linear(ghip, codes, scales, x)
+    st = assert_close(got, want, floor_linear(codes, scales, x), "M%d N%d K%d" % (M, N, K))
+    print("gemm M%d N%d K%d" % (M, N, K), st)
+    assert np.array_equal(got, gpu_linear(ghip, codes, scales, x))   # deterministic
+
+
+def test_fp8_gemm_nan_codes_exact_decode(ghip):
+    """Every code incl. 0x7F/0xFF through the GEMM path (the NaN scan
+    selects the exact integer decode)."""
+    M, N, K = 48, 512, 1024
+    codes = (np.arange(N * K) & 0xFF).astype(np.uint8).reshape(N, K)
+    rng = np.random.default_rng(5)
+    scales = np.exp2(rng.uniform(-10, -4, (O.nblocks(N), O.nblocks(K)))).astype(np.float32)
+    x = O.f32_to_bf16(rng.standard_normal((M, K)).astype(np.float32))
+    want = O.fp8_linear(codes, scales, x, threads=8)
+    assert_close(gpu_linear(ghip, codes, scales, x), want,
+                 floor_linear(codes, scales, x), "gemm all codes")
+
+
 @pytest.mark.parametrize("M,N,K", [(1, 512, 512), (2, 300, 768), (1, 256, 1024)])
 def test_all_256_codes_incl_nan_codes(ghip, M, N, K):
     """Every code incl. 0x7F/0xFF (decoded as +-480 by the reference): the

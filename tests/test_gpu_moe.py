@@ -61,6 +61,55 @@ def small(ghip):
     ghip.apus_ghip_store_close(s)
 
 
+def test_store_roundtrip(small):
+    """get returns the put slab bitwise; the device slab holds the members
+    in the reference order at 256-byte aligned offsets."""
+    ghip, s, slabs, (E, dim, inter) = small
+    sb = slabs[0].nbytes
+    nbg = O.nblocks(inter) * O.nblocks(dim) * 4
+    up = lambda v: (v + 255) // 256 * 256  # noqa: E731
+    h_off, d_off, parts = 0, 0, []
+    for n in (inter * dim, nbg, inter * dim, nbg, dim * inter, nbg):
+        parts.append((h_off, d_off, n))
+        h_off += n
+        d_off += up(n)
+    for e in (0, 3, 15):
+        got = np.empty(sb, np.uint8)
+        assert ghip.apus_ghip_store_get(s, e, O.ptr(got), sb) == 0
+        assert np.array_equal(got, slabs[e]), e
+        dev = G.download_ptr(ghip.apus_ghip_store_slab_dev(s, e), np.uint8, (d_off,))
+        for h, d, n in parts:
+            assert np.array_equal(dev[d:d + n], slabs[e][h:h + n]), (e, h)
+
+
+def test_store_synth_matches_host_generator(ghip, pkg):
+    """The device synthetic fill writes the host generator's slab
+    (include/apus_synth.h streams), read back through store_get."""
+    lib = pkg.load()
+    E, dim, inter, seed, bank = 3, 256, 128, 0x5EED, 2
+    s = open_store(ghip, E, dim, inter)
+    try:
+        assert ghip.apus_ghip_store_synth(s, seed, bank, 1e-4, 1e-2) == 0
+        sb = ghip.apus_ghip_store_slab_bytes(s)
+        for e in range(E):
+            parts = []
+            for j, (o, k) in enumerate([(inter, dim), (inter, dim), (dim, inter)]):
+                c = np.empty(o * k, np.uint8)
+                lib.apus_synth_fp8_codes(O.ptr(c), c.size, seed,
+                                         lib.apus_synth_expert_stream(bank, e, 2 * j), 0)
+                sc = np.empty(O.nblocks(o) * O.nblocks(k), np.float32)
+                lib.apus_synth_scales(O.ptr(sc), sc.size, seed,
+                                      lib.apus_synth_expert_stream(bank, e, 2 * j + 1),
+                                      ctypes.c_float(1e-4), ctypes.c_float(1e-2))
+                parts += [c, sc.view(np.uint8)]
+            want = np.concatenate(parts)
+            got = np.empty(sb, np.uint8)
+            assert ghip.apus_ghip_store_get(s, e, O.ptr(got), sb) == 0
+            assert np.array_equal(got, want), e
+    finally:
+        ghip.apus_ghip_store_close(s)
+
+
 def test_store_dequant_on_fill_bitwise(small):
     ghip, s, slabs, (E, dim, inter) = small
     for e in (0, 3, 15):

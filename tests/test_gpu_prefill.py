@@ -150,7 +150,8 @@ def test_expert_output_real_shape(ghip):
     try:
         assert ghip.apus_ghip_store_synth(s, 0xC3, 0, 1e-4, 1e-2) == 0
         sb = ghip.apus_ghip_store_slab_bytes(s)
-        slab = G.download_ptr(ghip.apus_ghip_store_slab_dev(s, 0), np.uint8, (sb,))
+        slab = np.empty(sb, np.uint8)
+        assert ghip.apus_ghip_store_get(s, 0, O.ptr(slab), sb) == 0
         rng = np.random.default_rng(11)
         x = O.f32_to_bf16(rng.standard_normal((T, dim)).astype(np.float32))
         idx = np.zeros((T, 1), np.int32)
@@ -202,7 +203,8 @@ def test_config3_sampled_tokens(ghip, pkg):
         sb = ghip.apus_ghip_store_slab_bytes(s)
         slabs = [None] * E
         for e in used:
-            slabs[e] = G.download_ptr(ghip.apus_ghip_store_slab_dev(s, e), np.uint8, (sb,))
+            slabs[e] = np.empty(sb, np.uint8)
+            assert ghip.apus_ghip_store_get(s, e, O.ptr(slabs[e]), sb) == 0
         want, eo = O.moe_forward(slabs, dim, inter, x[toks], idx[toks], w[toks],
                                  want_expert_out=True, threads=16)
         fl = floor_of(eo, w[toks], idx[toks])
