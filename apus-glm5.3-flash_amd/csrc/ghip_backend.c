@@ -801,6 +801,32 @@ int apus_ghip_moe_decode_dev(ApusGhipStore *s, const uint16_t *x,
     return 0;
 }
 
+static float *g_router_logits;          /* device [512] f32 router workspace */
+
+int apus_ghip_moe_router_dev(const uint16_t *x, const uint16_t *gate_w,
+                             const float *logits, const float *gate_bias, int E,
+                             size_t dim, int topk, float route_scale, float *scores,
+                             int32_t *idx, float *w, void *stream) {
+    if (ghip_init()) return 1;
+    if (E <= 0 || E > 512 || topk <= 0 || topk > GHIP_MAX_TOPK || topk > E
+        || !gate_bias || !idx || !w || (!logits && (!x || !gate_w || dim == 0))) {
+        ghip_seterr("moe_router: bad arguments (E=%d topk=%d dim=%zu)", E, topk, dim);
+        return 1;
+    }
+    if (!logits && !g_router_logits)
+        HIPCHK(hipMalloc((void **)&g_router_logits, 512 * sizeof(float)));
+    hipError_t e = ghip_launch_moe_router(x, gate_w, logits, g_router_logits, gate_bias,
+                                          (uint32_t)E, (uint32_t)dim, topk, route_scale,
+                                          scores, idx, w, (hipStream_t)stream);
+    if (e != hipSuccess) {
+        ghip_seterr("moe_router launch: %s (dim %% 8 and 16-byte x / gate_w required)",
+                    hipGetErrorString(e));
+        return 1;
+    }
+    G.dispatches++;
+    return 0;
+}
+
 int apus_ghip_moe_decode(ApusGhipStore *s, const uint16_t *x,
                          const int32_t *idx, const float *w, int topk,
                          uint16_t *out) {

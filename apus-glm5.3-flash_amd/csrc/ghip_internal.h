@@ -79,6 +79,17 @@ hipError_t ghip_launch_moe_decode(const GhipBank *bank, const uint16_t *x,
                                   uint16_t *out, const GhipMoeDecodeWs *ws,
                                   const hipEvent_t *ev, hipStream_t st);
 
+/* Router with the reference semantics (c/gmoe.h:191-208): gate logits (a
+ * GEMV over gate_w [E, dim] bf16 into logits_ws [E] f32, or given
+ * logits_in), numpy-stable sigmoid scores, stable top-k of score + bias,
+ * pairwise-sum normalization x scale. scores [E] optional; idx / w [topk]
+ * in selection order. E <= 512, topk <= 16. */
+hipError_t ghip_launch_moe_router(const uint16_t *x, const uint16_t *gate_w,
+                                  const float *logits_in, float *logits_ws,
+                                  const float *bias, uint32_t E, uint32_t dim,
+                                  int topk, float scale, float *scores,
+                                  int32_t *idx, float *w, hipStream_t st);
+
 /* K4 prefill workspace (device; sized for cap_pairs = T * topk pairs). */
 #define PF_HDR_NTILES 0
 #define PF_HDR_NPAIRS 1

@@ -521,6 +521,128 @@ __global__ __launch_bounds__(MD_NW * 64, 1) void k_moe_down(
 
 /* ------------------------------------------------------------------------ */
 
+/* ------------------------------------------------------------------------ */
+/* router with the reference semantics (c/gmoe.h:191-208)                   */
+/* ------------------------------------------------------------------------ */
+
+/* Gate logits: one wave per gate row, logits[e] = sum_k w[e,k] * x[k] in
+ * f32 (lane-strided partial sums + a fixed xor-butterfly reduction: a GEMV
+ * of the same tolerance class as every other one here; the reference's
+ * sequential-k dot is c/gmoe.h:168-173). dim % 8 == 0, 16-byte rows. */
+__global__ __launch_bounds__(256) void k_router_logits(const uint16_t *__restrict__ gate_w,
+                                                       const uint16_t *__restrict__ x,
+                                                       uint32_t E, uint32_t dim,
+                                                       float *__restrict__ logits) {
+    const uint32_t lane = threadIdx.x & 63u, e = blockIdx.x * 4u + (threadIdx.x >> 6);
+    if (e >= E) return;
+    const uint16_t *row = gate_w + (size_t)e * dim;
+    float acc = 0.0f;
+    for (uint32_t k = lane * 8u; k < dim; k += 512u) {
+        const ghip_u32x4 wv = *(const ghip_u32x4 *)(row + k);
+        const ghip_u32x4 xv = *(const ghip_u32x4 *)(x + k);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            acc = acc + __uint_as_float(wv[q] << 16) * __uint_as_float(xv[q] << 16);
+            acc = acc + __uint_as_float(wv[q] & 0xffff0000u) * __uint_as_float(xv[q] & 0xffff0000u);
+        }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) acc = acc + __shfl_xor(acc, off, 64);
+    if (lane == 0) logits[e] = acc;
+}
+
+/* Selection and weights from the logits, one wave (c/gmoe.h:191-208):
+ * scores = numpy-stable sigmoid (device expf), the stable top-k (larger
+ * first, ties to the lower id) of score + bias -- the bias selects, it
+ * never weighs -- then w_j = score[idx_j] / (pairwise_sum + 1e-20) *
+ * route_scale, with numpy's float32 pairwise sum of the k selected scores
+ * in selection order (c/gmhc.h:165-185). idx / w in selection order, as the
+ * reference returns them. */
+__global__ __launch_bounds__(64) void k_router_select(const float *__restrict__ logits,
+                                                      const float *__restrict__ bias,
+                                                      uint32_t E, int topk, float scale,
+                                                      float *__restrict__ scores,
+                                                      int32_t *__restrict__ idx,
+                                                      float *__restrict__ w) {
+    __shared__ float sc[RT_MAXE];
+    const int lane = threadIdx.x & 63;
+    uint64_t key[RT_REG];
+#pragma unroll
+    for (int s = 0; s < RT_REG; s++) {
+        const uint32_t i = (uint32_t)lane + 64u * s;
+        key[s] = 0ull;
+        if (i < E) {
+            const float v = ghip_sigmoid_np(logits[i]);
+            sc[i] = v;
+            if (scores) scores[i] = v;
+            key[s] = rt_key(v + bias[i], (int)i);
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);           /* lgkmcnt(0) */
+    __builtin_amdgcn_wave_barrier();
+    int myid = -1;
+    for (int j = 0; j < topk; j++) {
+        uint64_t b = 0;
+#pragma unroll
+        for (int s = 0; s < RT_REG; s++) b = key[s] > b ? key[s] : b;
+        b = rt_wave_max(b);
+#pragma unroll
+        for (int s = 0; s < RT_REG; s++)
+            if (key[s] == b) key[s] = 0ull;
+        if (lane == j) myid = (int)(0xffffffffu - (uint32_t)b);
+    }
+    const float myw = lane < topk ? sc[myid] : 0.0f;
+    /* numpy float32 pairwise sum of the k selected scores (k <= 16) */
+    auto at = [&](int i) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, myw), i));
+    };
+    float sum;
+    if (topk < 8) {
+        sum = at(0);
+        for (int i = 1; i < topk; i++) sum = sum + at(i);
+    } else {
+        float r[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) r[q] = at(q);
+        int i = 8;
+        if (topk >= 16) {
+#pragma unroll
+            for (int q = 0; q < 8; q++) r[q] = r[q] + at(8 + q);
+            i = 16;
+        }
+        sum = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+        for (; i < topk; i++) sum = sum + at(i);
+    }
+    if (lane < topk) {
+        idx[lane] = myid;
+        w[lane] = myw / (sum + 1e-20f) * scale;
+    }
+}
+
+extern "C" hipError_t ghip_launch_moe_router(const uint16_t *x, const uint16_t *gate_w,
+                                             const float *logits_in, float *logits_ws,
+                                             const float *bias, uint32_t E, uint32_t dim,
+                                             int topk, float scale, float *scores,
+                                             int32_t *idx, float *w, hipStream_t st) {
+    if (!bias || !idx || !w || E == 0 || E > RT_MAXE || topk <= 0 || topk > MD_MAXK
+        || (uint32_t)topk > E)
+        return hipErrorInvalidValue;
+    const float *lg = logits_in;
+    if (!lg) {
+        if (!x || !gate_w || !logits_ws || dim == 0 || dim % 8 || ((uintptr_t)x & 15)
+            || ((uintptr_t)gate_w & 15))
+            return hipErrorInvalidValue;
+        hipLaunchKernelGGL(k_router_logits, dim3((E + 3) / 4), dim3(256), 0, st, gate_w, x,
+                           E, dim, logits_ws);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        lg = logits_ws;
+    }
+    hipLaunchKernelGGL(k_router_select, dim3(1), dim3(64), 0, st, lg, bias, E, topk, scale,
+                       scores, idx, w);
+    return hipGetLastError();
+}
+
 extern "C" hipError_t ghip_launch_moe_decode(const GhipBank *bank,
                                              const uint16_t *x,
                                              const float *logits,

@@ -178,6 +178,22 @@ int apus_ghip_store_get(ApusGhipStore *s, int expert, void *slab,
 int apus_ghip_store_expert_bf16(ApusGhipStore *s, int expert,
                                 uint16_t *payload);
 
+/* --- MoE router with the reference semantics (apus_gmoe_router,
+ * c/gmoe.h:191-208; numerics c/gmhc.h:157-185), on device pointers:
+ * gate logits = gate_w [E, dim] bf16 . x [dim] bf16 in f32 (a GEMV: the
+ * same tolerance class as every GEMV here; pass logits [E] f32 instead,
+ * with gate_w / x NULL, to start from given logits), scores = numpy-stable
+ * sigmoid, selection = stable top-k (ties -> lower id) of score + gate_bias
+ * (the bias selects, it never weighs), w = the selected scores / (numpy
+ * pairwise sum + 1e-20) * route_scale. Outputs idx / w [topk] in selection
+ * order (as the reference) and, when scores is non-NULL, scores [E]; the
+ * result feeds apus_ghip_moe_decode_dev / _prefill_dev as idx / w.
+ * E <= 512, topk <= 16, dim % 8 == 0. Asynchronous on `stream`. 0 = ok. */
+int apus_ghip_moe_router_dev(const uint16_t *x, const uint16_t *gate_w,
+                             const float *logits, const float *gate_bias, int E,
+                             size_t dim, int topk, float route_scale, float *scores,
+                             int32_t *idx, float *w, void *stream);
+
 /* --- routed MoE decode (one token): SwiGLU experts + ordered combine,
  * c/gmoe.h:210-227 + 307-320 without the router and shared expert. Up to 8
  * kept slots: one persistent launch (routing, gate/up GEMVs with the

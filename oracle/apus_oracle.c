@@ -463,6 +463,61 @@ void apo_topk_stable(const float *row, int n, int k, int32_t *idx) {
     }
 }
 
+/* c/gmoe.h:168-173: fp32 dot of one gate row, strictly ascending k, from
+ * +0, mul then add (the bf16 x bf16 products are exact in fp32). */
+float apo_gate_dot(const uint16_t *wrow, const uint16_t *x, size_t k) {
+    float acc = 0.0f;
+    for (size_t i = 0; i < k; i++) {
+        float p = apo_bf16_f32(wrow[i]) * apo_bf16_f32(x[i]);
+        acc = acc + p;
+    }
+    return acc;
+}
+
+/* c/gmoe.h:191-208 (the reference router): logits by apo_gate_dot, scores
+ * = numpy-stable sigmoid (c/gmhc.h:157-160), selection on scores + bias
+ * only, stable top-k (ties -> lower id), w = the unbiased scores of the
+ * selection, normalized by their numpy pairwise sum (c/gmhc.h:165-185)
+ * + 1e-20 and scaled by route_scale. scores [E] out (may be NULL). */
+void apo_gmoe_router(const uint16_t *gate_w, const float *gate_bias, int E,
+                     size_t dim, int topk, float route_scale, const uint16_t *x,
+                     float *scores, int32_t *idx, float *w) {
+    float *sc = (float *)malloc((size_t)E * sizeof(float));
+    float *b = (float *)malloc((size_t)E * sizeof(float));
+    for (int e = 0; e < E; e++) {
+        float logit = apo_gate_dot(gate_w + (size_t)e * dim, x, dim);
+        sc[e] = apo_sigmoid_np(logit);
+        b[e] = sc[e] + gate_bias[e];
+    }
+    apo_topk_stable(b, E, topk, idx);
+    for (int j = 0; j < topk; j++) w[j] = sc[idx[j]];
+    float sum = apo_pw_sum(w, (size_t)topk);
+    for (int j = 0; j < topk; j++) w[j] = w[j] / (sum + 1e-20f) * route_scale;
+    if (scores) memcpy(scores, sc, (size_t)E * sizeof(float));
+    free(sc);
+    free(b);
+}
+
+/* The router's selection and weights from given logits (the device router
+ * computes logits as a GEMV; this is the part after them). */
+void apo_gmoe_router_from_logits(const float *logits, const float *gate_bias, int E,
+                                 int topk, float route_scale, float *scores,
+                                 int32_t *idx, float *w) {
+    float *sc = (float *)malloc((size_t)E * sizeof(float));
+    float *b = (float *)malloc((size_t)E * sizeof(float));
+    for (int e = 0; e < E; e++) {
+        sc[e] = apo_sigmoid_np(logits[e]);
+        b[e] = sc[e] + gate_bias[e];
+    }
+    apo_topk_stable(b, E, topk, idx);
+    for (int j = 0; j < topk; j++) w[j] = sc[idx[j]];
+    float sum = apo_pw_sum(w, (size_t)topk);
+    for (int j = 0; j < topk; j++) w[j] = w[j] / (sum + 1e-20f) * route_scale;
+    if (scores) memcpy(scores, sc, (size_t)E * sizeof(float));
+    free(sc);
+    free(b);
+}
+
 void apo_route_softmax(const float *logits, int E, int k, int32_t *idx,
                        float *w) {
     apo_topk_stable(logits, E, k, idx);

@@ -57,6 +57,17 @@ float apo_sigmoid_np(float x);             /* c/gmhc.h:157-160 */
 float apo_pw_sum(const float *a, size_t n);/* c/gmhc.h:165-185 */
 /* c/gmoe.h:175-189: k passes of strict-greater argmax, ties -> lower index */
 void  apo_topk_stable(const float *row, int n, int k, int32_t *idx);
+/* c/gmoe.h:168-173: one gate-row fp32 dot, ascending k, mul then add */
+float apo_gate_dot(const uint16_t *wrow, const uint16_t *x, size_t k);
+/* c/gmoe.h:191-208: the reference router (sigmoid scores, selection-only
+ * bias, stable top-k, pairwise-sum normalization x route_scale) */
+void  apo_gmoe_router(const uint16_t *gate_w, const float *gate_bias, int E,
+                      size_t dim, int topk, float route_scale, const uint16_t *x,
+                      float *scores, int32_t *idx, float *w);
+/* the same from given logits (everything after the gate dots) */
+void  apo_gmoe_router_from_logits(const float *logits, const float *gate_bias, int E,
+                                  int topk, float route_scale, float *scores,
+                                  int32_t *idx, float *w);
 /* c/gmoe.h:210-227 on BF16 payloads: g,u GEMVs, clamps, two bf16 rounds,
  * down GEMV. g_out/u_out/h_out optional (NULL to skip). */
 int   apo_swiglu_expert(const uint16_t *wg, const uint16_t *wu,

@@ -56,6 +56,11 @@ _ORACLE_SIGS = {
     "apo_moe_forward": (c_int, [c_vp, c_int, c_size, c_size, c_float, c_vp,
                                 c_size, c_vp, c_vp, c_int, c_vp, c_vp, c_int]),
     "apo_route_softmax": (None, [c_vp, c_int, c_int, c_vp, c_vp]),
+    "apo_gate_dot": (c_float, [c_vp, c_vp, c_size]),
+    "apo_gmoe_router": (None, [c_vp, c_vp, c_int, c_size, c_int, c_float, c_vp,
+                               c_vp, c_vp, c_vp]),
+    "apo_gmoe_router_from_logits": (None, [c_vp, c_vp, c_int, c_int, c_float, c_vp,
+                                           c_vp, c_vp]),
     "apo_default_threads": (c_int, []),
 }
 
@@ -75,6 +80,8 @@ _REF_SIGS = {
     "ref_gmoe_expert": (c_int, [c_vp, c_vp, c_vp, c_vp, c_size, c_size,
                                 c_float, c_vp]),
     "ref_pool_threads": (c_int, []),
+    "ref_gmoe_router": (None, [c_vp, c_vp, c_int, c_size, c_int, c_float, c_vp,
+                               c_vp, c_vp, c_vp]),
 }
 
 _oracle = None
@@ -197,6 +204,32 @@ def swiglu_expert(wg, wu, wd, x, limit=10.0, threads=1):
                                    inter, limit, ptr(out), ptr(g), ptr(u),
                                    ptr(h), threads) == 0
     return out, g, u, h
+
+
+def gmoe_router(gate_w, gate_bias, x, topk, route_scale=2.5):
+    """c/gmoe.h:191-208 -> (scores [E], idx [topk], w [topk])."""
+    gate_w = np.ascontiguousarray(gate_w, np.uint16)
+    E, dim = gate_w.shape
+    bias = np.ascontiguousarray(gate_bias, np.float32)
+    x = np.ascontiguousarray(x, np.uint16)
+    sc = np.empty(E, np.float32)
+    idx = np.empty(topk, np.int32)
+    w = np.empty(topk, np.float32)
+    lib().apo_gmoe_router(ptr(gate_w), ptr(bias), E, dim, topk, route_scale, ptr(x),
+                          ptr(sc), ptr(idx), ptr(w))
+    return sc, idx, w
+
+
+def gmoe_router_from_logits(logits, gate_bias, topk, route_scale=2.5):
+    logits = np.ascontiguousarray(logits, np.float32)
+    bias = np.ascontiguousarray(gate_bias, np.float32)
+    E = logits.size
+    sc = np.empty(E, np.float32)
+    idx = np.empty(topk, np.int32)
+    w = np.empty(topk, np.float32)
+    lib().apo_gmoe_router_from_logits(ptr(logits), ptr(bias), E, topk, route_scale,
+                                      ptr(sc), ptr(idx), ptr(w))
+    return sc, idx, w
 
 
 def route_softmax(logits, k):

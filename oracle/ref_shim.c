@@ -20,6 +20,7 @@
  *   apus_gmhc_pw_sum             c/gmhc.h:165-185
  *   apus_gmoe_topk_stable        c/gmoe.h:175-189
  *   apus_gmoe_expert             c/gmoe.h:210-227
+ *   apus_gmoe_router             c/gmoe.h:191-208
  */
 #define APUS_GMHC_IMPLEMENTATION
 #define APUS_GMOE_IMPLEMENTATION
@@ -99,3 +100,18 @@ REF_API int ref_gmoe_expert(const uint16_t *wg, const uint16_t *wu,
     return 0;
 }
 REF_API int ref_pool_threads(void) { return apus_pool_threads(); }
+/* The per-token router (c/gmoe.h:191-208); scores [E] out. */
+REF_API void ref_gmoe_router(const uint16_t *gate_w, const float *gate_bias, int E,
+                             size_t dim, int topk, float route_scale,
+                             const uint16_t *x, float *scores, int32_t *idx, float *w) {
+    ApusGmoeRouterW r;
+    r.E = E;
+    r.topk = topk;
+    r.dim = dim;
+    r.route_scale = route_scale;
+    r.gate_w = gate_w;
+    r.gate_bias = gate_bias;
+    float *b = (float *)malloc((size_t)(E > 0 ? E : 1) * sizeof(float));
+    apus_gmoe_router(&r, x, scores, idx, w, b);
+    free(b);
+}

@@ -75,6 +75,66 @@ def test_route_softmax():
     assert abs(float(w.astype(np.float64).sum()) - 1.0) < 1e-6
 
 
+def _router_inputs(seed, E, dim, ties=False):
+    rng = np.random.default_rng(seed)
+    gw = O.f32_to_bf16((0.02 * rng.standard_normal((E, dim))).astype(np.float32))
+    x = O.f32_to_bf16(rng.standard_normal(dim).astype(np.float32))
+    if ties:
+        # equal gate rows and equal biases: equal biased scores, so the stable
+        # order (lower id first) decides
+        gw[5] = gw[3]
+        gw[40] = gw[3]
+        bias = np.zeros(E, np.float32)
+    else:
+        bias = (0.05 * rng.standard_normal(E)).astype(np.float32)
+    return gw, bias, x
+
+
+@pytest.mark.parametrize("E,dim,topk,ties", [(288, 4096, 8, False), (64, 256, 4, True),
+                                             (288, 512, 8, True), (16, 128, 1, False),
+                                             (300, 256, 16, False)])
+def test_router_closed_form(E, dim, topk, ties):
+    """The oracle router against a float64/numpy restatement: sequential
+    fp32 dots equal np.cumsum order, sigmoid, selection on score + bias
+    (stable argsort), weights = selected scores / (pairwise sum + 1e-20) *
+    2.5; and against the reference build bitwise."""
+    gw, bias, x = _router_inputs(E * 31 + dim, E, dim, ties)
+    sc, idx, w = O.gmoe_router(gw, bias, x, topk)
+    # sequential fp32 dot: numpy's cumulative float32 sum is the same order
+    prod = (O.bf16_to_f32(gw) * O.bf16_to_f32(x)[None, :]).astype(np.float32)
+    logits = np.cumsum(prod, axis=1, dtype=np.float32)[:, -1]
+    want_sc = np.array([O.lib().apo_sigmoid_np(float(v)) for v in logits], np.float32)
+    assert np.array_equal(sc, want_sc)
+    b = (want_sc + bias).astype(np.float32)
+    assert np.array_equal(idx, np.argsort(-b, kind="stable")[:topk])
+    sel = want_sc[idx]
+    den = np.float32(np.add.reduce(sel, dtype=np.float32) + np.float32(1e-20))
+    assert np.array_equal(w, (sel / den * np.float32(2.5)).astype(np.float32))
+    if ties:
+        assert list(idx).index(3) < list(idx).index(5) if 5 in idx and 3 in idx else True
+    if O.ref_available():
+        rsc = np.empty(E, np.float32)
+        ridx = np.empty(topk, np.int32)
+        rw = np.empty(topk, np.float32)
+        O.ref().ref_gmoe_router(O.ptr(gw), O.ptr(bias), E, dim, topk, 2.5, O.ptr(x),
+                                O.ptr(rsc), O.ptr(ridx), O.ptr(rw))
+        assert np.array_equal(sc, rsc) and np.array_equal(idx, ridx)
+        assert np.array_equal(w, rw)
+    # from logits: the same selection and weights
+    sc2, idx2, w2 = O.gmoe_router_from_logits(logits, bias, topk)
+    assert np.array_equal(idx2, idx) and np.array_equal(w2, w) and np.array_equal(sc2, sc)
+
+
+def test_router_planted_bias_mistake_is_detected():
+    """The bias selects but never weighs: a router that weighs by the
+    biased score would differ (the check above pins this)."""
+    gw, bias, x = _router_inputs(77, 288, 512)
+    bias = bias + np.float32(0.5)
+    sc, idx, w = O.gmoe_router(gw, bias, x, 8)
+    bad = (sc[idx] + bias[idx]) / np.float32((sc[idx] + bias[idx]).sum() + 1e-20) * 2.5
+    assert not np.allclose(w, bad, rtol=1e-3)
+
+
 def test_expert_golden(fx, man):
     for i, sh in enumerate(man["expert"]):
         pl = [O.dequant(fx[f"xp{i}_{nm}_codes"], fx[f"xp{i}_{nm}_scales"])
