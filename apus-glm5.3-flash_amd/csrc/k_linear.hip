@@ -277,13 +277,17 @@ extern "C" hipError_t ghip_launch_nan_scan(const uint8_t *codes, size_t n,
 /* Y[m, rows] for M <= 4 token rows. A row group (16 weight rows) is split
  * over KS waves along K (KS in {2, 8}); a workgroup pass covers 8 / KS row
  * groups, passes run over the groups persistently (grid <= CUs). Each wave
- * streams its chunks (16 rows x 128 codes, one scale block) through a
- * wave-private GS_R-stage LDS ring filled by direct DMA, dequantizes in
- * registers and reduces on MFMA with the token rows of x (staged once per
- * workgroup) as the A operand: A row i = lane % 16 is token min(i, M-1),
- * rows past M feed output rows that are discarded. The KS partial sums of a
- * group are added in LDS in a fixed order (deterministic). */
-template <int M, int KS>
+ * streams its chunks (16 rows x 128 bytes: 128 FP8 codes with one scale
+ * block, or 64 BF16 weights when BF) through a wave-private GS_R-stage LDS
+ * ring filled by direct DMA, dequantizes in registers (FP8) and reduces on
+ * MFMA with the token rows of x (staged once per workgroup) as the A
+ * operand: A row i = lane % 16 is token min(i, M-1), rows past M feed
+ * output rows that are discarded. The KS partial sums of a group are added
+ * in LDS in a fixed order (deterministic). BF: the BF16 GEMV of the
+ * bf16_gemm hook (c/bf16.h:712-767), no scales; lane 16g + n holds row n,
+ * weights [16g, 16g + 16) of the chunk, two v_mfma_f32_16x16x32_bf16 with
+ * x at the same k. */
+template <int M, int KS, bool BF = false>
 __global__ __launch_bounds__(GS_NW * 64, 1) void k_fp8_gemv_stream(
     const uint8_t *__restrict__ W, const float *__restrict__ S,
     const uint16_t *__restrict__ X, uint16_t *__restrict__ Y, uint32_t O,
@@ -298,24 +302,26 @@ __global__ __launch_bounds__(GS_NW * 64, 1) void k_fp8_gemv_stream(
     for (uint32_t i = tid; i < (uint32_t)M * (K >> 3); i += GS_NW * 64)
         ((ghip_u32x4 *)xs)[i] = ((const ghip_u32x4 *)X)[i];
     __syncthreads();
-    const bool exact = exact_flag != nullptr && *exact_flag != 0u;
+    const bool exact = !BF && exact_flag != nullptr && *exact_flag != 0u;
     uint8_t *ring = gsl + (((size_t)M * K * 2u + 1023u) & ~(size_t)1023u) +
                     wv * (GS_R * 2048u);
-    const uint32_t nch = K >> 7, nkb = nch;
+    /* chunk = 128 bytes of each of 16 rows; row stride in bytes */
+    const uint32_t KB = BF ? 2u * K : K;
+    const uint32_t nch = KB >> 7, nkb = K >> 7;
     const uint32_t part = wv % KS, slot = wv / KS;
     const uint32_t c0 = part * nch / KS, c1 = (part + 1) * nch / KS, nc = c1 - c0;
     const uint32_t groups = (O + 15) / 16, passes = (groups + GPP - 1) / GPP;
-    const uint16_t *xa = xs + (size_t)min(n, (uint32_t)M - 1u) * K + 32u * g;
+    const uint16_t *xa = xs + (size_t)min(n, (uint32_t)M - 1u) * K + (BF ? 16u : 32u) * g;
     for (uint32_t ps = blockIdx.x; ps < passes; ps += gridDim.x) {
         const uint32_t grp = ps * GPP + slot;
         const bool live = grp < groups;
         if (live) {
             /* a wave with no chunks (K < KS * 128) contributes zeros */
             const uint32_t row0 = grp * 16;
-            const uint8_t *rows = W + (size_t)row0 * K;
+            const uint8_t *rows = W + (size_t)row0 * KB;
             /* a partial last group re-reads row O-1 (outputs discarded) */
-            const ghip_cdma d = ghip_cdma_offsets(lane, K, min(15u, O - 1u - row0));
-            const float *srow = S + (size_t)(row0 >> 7) * nkb;
+            const ghip_cdma d = ghip_cdma_offsets(lane, KB, min(15u, O - 1u - row0));
+            const float *srow = BF ? nullptr : S + (size_t)(row0 >> 7) * nkb;
 #pragma unroll
             for (uint32_t i = 0; i + 1 < GS_R; i++)
                 if (i < nc) ghip_cdma_issue(rows, c0 + i, d, ring + i * 2048u);
@@ -327,9 +333,17 @@ __global__ __launch_bounds__(GS_NW * 64, 1) void k_fp8_gemv_stream(
                                     ring + ((t + GS_R - 1) % GS_R) * 2048u);
                 const ghip_chunk cw = ghip_cdma_read(ring + (t % GS_R) * 2048u, n, g);
                 const uint32_t c = c0 + t;
-                const float sc = ghip_sload(srow, c);
-                if (exact) ghip_chunk_mfma<true>(cw, sc, xa + c * 128u, acc);
-                else ghip_chunk_mfma<false>(cw, sc, xa + c * 128u, acc);
+                if (BF) {
+                    const ghip_bf16x8 *a = (const ghip_bf16x8 *)(xa + c * 64u);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        a[0], __builtin_bit_cast(ghip_bf16x8, cw.lo), acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        a[1], __builtin_bit_cast(ghip_bf16x8, cw.hi), acc, 0, 0, 0);
+                } else {
+                    const float sc = ghip_sload(srow, c);
+                    if (exact) ghip_chunk_mfma<true>(cw, sc, xa + c * 128u, acc);
+                    else ghip_chunk_mfma<false>(cw, sc, xa + c * 128u, acc);
+                }
             }
             if (g == 0) {
 #pragma unroll
@@ -445,6 +459,26 @@ extern "C" hipError_t ghip_launch_fp8_linear(const uint8_t *codes,
     return hipSuccess;
 }
 
+template <int M>
+static hipError_t launch_bf16_gemv_m(const uint16_t *w, const uint16_t *x, uint16_t *y,
+                                     size_t O, size_t K, hipStream_t st) {
+    const size_t groups = (O + 15) / 16;
+    const size_t lds = gs_lds(M, K);
+    const uint8_t *wb = (const uint8_t *)w;
+    if ((groups + 3) / 4 >= g_gs_ncu) {              /* KS = 2: 4 groups a pass */
+        uint32_t g = (uint32_t)((groups + 3) / 4);
+        if (g > g_gs_ncu) g = g_gs_ncu;
+        hipLaunchKernelGGL((k_fp8_gemv_stream<M, 2, true>), dim3(g), dim3(GS_NW * 64), lds,
+                           st, wb, nullptr, x, y, (uint32_t)O, (uint32_t)K, nullptr);
+    } else {                                           /* KS = 8: 1 group a pass */
+        uint32_t g = (uint32_t)groups;
+        if (g > g_gs_ncu) g = g_gs_ncu;
+        hipLaunchKernelGGL((k_fp8_gemv_stream<M, 8, true>), dim3(g), dim3(GS_NW * 64), lds,
+                           st, wb, nullptr, x, y, (uint32_t)O, (uint32_t)K, nullptr);
+    }
+    return hipGetLastError();
+}
+
 extern "C" hipError_t ghip_launch_bf16_linear(const uint16_t *w,
                                               const uint16_t *x, uint16_t *y,
                                               size_t M, size_t O, size_t K,
@@ -452,6 +486,29 @@ extern "C" hipError_t ghip_launch_bf16_linear(const uint16_t *w,
     if (M == 0 || O == 0) return hipSuccess;
     if (K == 0 || O > 0x7fffffffu || K > 0x7fffffffu || M > 0x7fffffffu)
         return hipErrorInvalidValue;
+    /* the streaming MFMA GEMV, in groups of <= 4 token rows (each reading
+     * the weights once), when the shape and alignment allow */
+    if (g_gs_ncu && K % 64 == 0 && ((uintptr_t)w & 15) == 0 && ((uintptr_t)x & 15) == 0
+        && gs_lds(1, K) <= GS_LDS) {
+        size_t m0 = 0;
+        while (m0 < M) {
+            size_t mc = M - m0;
+            if (mc > 4) mc = 4;
+            while (mc > 1 && gs_lds(mc, K) > GS_LDS) mc--;
+            const uint16_t *xm = x + m0 * K;
+            uint16_t *ym = y + m0 * O;
+            hipError_t e;
+            switch (mc) {
+            case 4: e = launch_bf16_gemv_m<4>(w, xm, ym, O, K, st); break;
+            case 3: e = launch_bf16_gemv_m<3>(w, xm, ym, O, K, st); break;
+            case 2: e = launch_bf16_gemv_m<2>(w, xm, ym, O, K, st); break;
+            default: e = launch_bf16_gemv_m<1>(w, xm, ym, O, K, st); break;
+            }
+            if (e != hipSuccess) return e;
+            m0 += mc;
+        }
+        return hipSuccess;
+    }
     size_t items = M * O;
     if (items > 0xffffffffull * 4) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_bf16_linear_any, dim3((uint32_t)((items + 3) / 4)),
@@ -462,11 +519,16 @@ extern "C" hipError_t ghip_launch_bf16_linear(const uint16_t *w,
 
 template <int M>
 static hipError_t gs_attr(void) {
-    hipError_t e = hipFuncSetAttribute((const void *)k_fp8_gemv_stream<M, 2>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, GS_LDS);
-    if (e != hipSuccess) return e;
-    return hipFuncSetAttribute((const void *)k_fp8_gemv_stream<M, 8>,
-                               hipFuncAttributeMaxDynamicSharedMemorySize, GS_LDS);
+    const void *ks[4] = {(const void *)k_fp8_gemv_stream<M, 2>,
+                         (const void *)k_fp8_gemv_stream<M, 8>,
+                         (const void *)k_fp8_gemv_stream<M, 2, true>,
+                         (const void *)k_fp8_gemv_stream<M, 8, true>};
+    for (int i = 0; i < 4; i++) {
+        hipError_t e = hipFuncSetAttribute(ks[i], hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           GS_LDS);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 extern "C" hipError_t ghip_linear_init(uint32_t n_cu) {

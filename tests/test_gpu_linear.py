@@ -174,9 +174,11 @@ def test_bf16_gemm_golden(ghip, fx, man):
 
 
 def test_bf16_gemm_real_shapes(ghip):
+    """Real shapes (streaming MFMA GEMV, M in groups of <= 4) and ragged
+    ones: O % 16 != 0, K = 64, K % 64 != 0 (the generic kernel)."""
     rng = np.random.default_rng(3)
-    for (Oo, K) in [(2048, 4096), (4096, 2048), (288, 4096)]:
-        for M in (1, 5):
+    for (Oo, K) in [(2048, 4096), (4096, 2048), (288, 4096), (300, 64), (129, 200)]:
+        for M in (1, 3, 5):
             w = O.f32_to_bf16(rng.uniform(-4, 4, (Oo, K)).astype(np.float32))
             x = O.f32_to_bf16(rng.uniform(-4, 4, (M, K)).astype(np.float32))
             y = np.empty((M, Oo), np.uint16)
