@@ -58,6 +58,13 @@ SIGNATURES = {
     "apus_ghip_store_synth": (c_int, [c_vp, c_u64, c_int, c_float, c_float]),
     "apus_ghip_store_slab_dev": (c_vp, [c_vp, c_int]),
     "apus_ghip_store_get": (c_int, [c_vp, c_int, c_vp, c_size]),
+    "apus_ghip_store_load_container": (c_int, [c_vp, ctypes.c_char_p, c_int,
+                                               ctypes.POINTER(c_int), ctypes.c_char_p,
+                                               c_size]),
+    "apus_ghip_container_slab": (c_int, [ctypes.c_char_p, c_int, c_int, c_size,
+                                         ctypes.c_char_p, c_size,
+                                         ctypes.POINTER(c_u64), ctypes.c_char_p,
+                                         c_size]),
     "apus_ghip_store_expert_bf16": (c_int, [c_vp, c_int, c_vp]),
     "apus_ghip_moe_decode": (c_int, [c_vp, c_vp, c_vp, c_vp, c_int, c_vp]),
     "apus_ghip_moe_decode_dev": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_int,

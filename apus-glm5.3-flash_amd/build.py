@@ -17,7 +17,7 @@ LIB = os.path.join(HERE, "libapus_ghip.so")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 
-C_SRCS = ["ghip_backend.c", "ghip_synth.c"]
+C_SRCS = ["ghip_backend.c", "ghip_synth.c", "ghip_container.c"]
 HIP_SRCS = ["k_linear.hip", "k_moe.hip", "k_moe_prefill.hip", "k_synth.hip"]
 
 INC = ["-I" + os.path.join(ROOT, "include"), "-I" + CSRC]

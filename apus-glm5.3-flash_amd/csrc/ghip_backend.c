@@ -19,7 +19,9 @@
 #include "ghip_internal.h"
 
 #include <hip/hip_runtime_api.h>
+#include <fcntl.h>
 #include <stdarg.h>
+#include <unistd.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -666,6 +668,108 @@ int apus_ghip_store_get(ApusGhipStore *s, int expert, void *slab, size_t nbytes)
     HIPCHK(hipStreamSynchronize(G.stream));
     G.d2h += s->h_bytes;
     return 0;
+}
+
+int apus_ghip_store_load_container(ApusGhipStore *s, const char *dir, int layer,
+                                   int *n_loaded, char *err, size_t errcap) {
+    if (n_loaded) *n_loaded = 0;
+    if (err && errcap) err[0] = 0;
+    if (!s) {
+        ghip_seterr("store_load_container: no store");
+        if (err && errcap) snprintf(err, errcap, "%s", g_err);
+        return 1;
+    }
+    GhipSlabRec *recs = NULL;
+    int n = 0;
+    char lerr[512] = {0};
+    if (ghip_container_layer(dir, layer, s->h_bytes, &recs, &n, lerr, sizeof lerr)) {
+        ghip_seterr("%s", lerr);
+        if (err && errcap) snprintf(err, errcap, "%s", g_err);
+        return 1;
+    }
+    for (int i = 0; i < n; i++)
+        if (recs[i].expert >= s->n_experts) {
+            ghip_seterr("store_load_container: record (layers.%d, %d) past the store's %d "
+                        "experts", layer, recs[i].expert, s->n_experts);
+            if (err && errcap) snprintf(err, errcap, "%s", g_err);
+            free(recs);
+            return 1;
+        }
+    /* two pinned slab buffers: the pread of slab i+1 overlaps the H2D of
+     * slab i (one pread per slab, as c/gcache.h:394-451) */
+    uint8_t *pin[2] = {NULL, NULL};
+    hipEvent_t done[2] = {NULL, NULL};
+    int fds_n = 0, rc = 0;
+    struct { char name[256]; int fd; } fds[64];
+    for (int b = 0; b < 2 && !rc; b++)
+        rc = hipHostMalloc((void **)&pin[b], s->h_bytes, 0) != hipSuccess
+             || hipEventCreateWithFlags(&done[b], hipEventDisableTiming) != hipSuccess;
+    if (rc) ghip_seterr("store_load_container: pinned staging (%zu B) failed", s->h_bytes);
+    int loaded = 0;
+    for (int i = 0; i < n && !rc; i++) {
+        int fd = -1;
+        for (int k = 0; k < fds_n; k++)
+            if (!strcmp(fds[k].name, recs[i].shard)) fd = fds[k].fd;
+        if (fd < 0) {
+            char path[4400];
+            snprintf(path, sizeof path, "%s/%s", dir, recs[i].shard);
+            fd = open(path, O_RDONLY | O_CLOEXEC);
+            if (fd < 0 || fds_n == 64) {
+                ghip_seterr("store_load_container: cannot open shard %s", path);
+                if (fd >= 0) close(fd);
+                rc = 1;
+                break;
+            }
+            snprintf(fds[fds_n].name, sizeof fds[fds_n].name, "%s", recs[i].shard);
+            fds[fds_n++].fd = fd;
+        }
+        uint8_t *h = pin[i & 1];
+        if (i >= 2 && hipEventSynchronize(done[i & 1]) != hipSuccess) {
+            ghip_seterr("store_load_container: copy failed");
+            rc = 1;
+            break;
+        }
+        size_t got = 0;
+        while (got < s->h_bytes) {
+            ssize_t r = pread(fd, h + got, s->h_bytes - got, (off_t)(recs[i].offset + got));
+            if (r <= 0) break;
+            got += (size_t)r;
+        }
+        if (got != s->h_bytes) {
+            ghip_seterr("store_load_container: short read of (layers.%d, %d) in %s",
+                        layer, recs[i].expert, recs[i].shard);
+            rc = 1;
+            break;
+        }
+        uint8_t *b = s->arena + (size_t)recs[i].expert * s->d_stride;
+        const size_t hs[7] = { s->h_gw, s->h_gs, s->h_uw, s->h_us, s->h_dw, s->h_ds,
+                               s->h_bytes };
+        const size_t ds[6] = { s->d_gw, s->d_gs, s->d_uw, s->d_us, s->d_dw, s->d_ds };
+        for (int m = 0; m < 6 && !rc; m++)
+            rc = hipMemcpyAsync(b + ds[m], h + hs[m], hs[m + 1] - hs[m],
+                                hipMemcpyHostToDevice, G.stream) != hipSuccess;
+        if (!rc) rc = store_scan(s, recs[i].expert, G.stream);
+        if (!rc) rc = hipEventRecord(done[i & 1], G.stream) != hipSuccess;
+        if (rc) {
+            ghip_seterr("store_load_container: upload of expert %d failed", recs[i].expert);
+            break;
+        }
+        G.h2d += s->h_bytes;
+        loaded++;
+    }
+    if (hipStreamSynchronize(G.stream) != hipSuccess && !rc) {
+        ghip_seterr("store_load_container: sync failed");
+        rc = 1;
+    }
+    for (int k = 0; k < fds_n; k++) close(fds[k].fd);
+    for (int b = 0; b < 2; b++) {
+        if (pin[b]) hipHostFree(pin[b]);
+        if (done[b]) hipEventDestroy(done[b]);
+    }
+    free(recs);
+    if (n_loaded) *n_loaded = loaded;
+    if (rc && err && errcap) snprintf(err, errcap, "%s", g_err);
+    return rc;
 }
 
 int apus_ghip_store_synth(ApusGhipStore *s, uint64_t seed, int bank,

@@ -135,6 +135,20 @@ hipError_t ghip_launch_fp8_gemm(const uint8_t *codes, const float *scales,
                                 size_t K, const uint32_t *exact_dev, uint32_t n_cu,
                                 const hipEvent_t *ev, hipStream_t st);
 
+/* One expert slab record of a converted v2 container's apus.index.json
+ * (c/gcache.h:896-930): the shard file name and the slab's file offset. */
+typedef struct {
+    int expert;
+    char shard[256];
+    uint64_t offset, nbytes;
+} GhipSlabRec;
+
+/* Parse <dir>/apus.index.json (format_version 2, model_type glm5_next) and
+ * return the slab records of block "layers.<layer>" (malloc'd, *n_out of
+ * them), each checked to hold exactly slab_bytes. 0 on success, else err. */
+int ghip_container_layer(const char *dir, int layer, size_t slab_bytes,
+                         GhipSlabRec **out, int *n_out, char *err, size_t errcap);
+
 /* Fill n u32 words with value (a kernel, not a memset, so callers may
  * capture it in a graph). */
 hipError_t ghip_launch_fill_u32(uint32_t *p, size_t n, uint32_t value,

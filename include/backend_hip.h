@@ -173,6 +173,23 @@ const void *apus_ghip_store_slab_dev(const ApusGhipStore *s, int expert);
  * Extension; no counterpart in the reference. */
 int apus_ghip_store_get(ApusGhipStore *s, int expert, void *slab,
                         size_t nbytes);
+/* Fill the store from a converted v2 container directory (the format the
+ * reference's expert cache opens, c/gcache.h:832-930; schema
+ * tests/m1/README.md:21-55): parses <dir>/apus.index.json (format_version
+ * 2, model_type glm5_next), takes the expert_slabs records of block
+ * "layers.<layer>" (each must hold exactly one slab), and loads every
+ * listed expert with one pread of its slab from <dir>/<shard> at the
+ * record's offset (c/gcache.h:394-451) into pinned staging and one H2D
+ * copy, overlapping the next read. Unlisted experts are left as they are.
+ * n_loaded: experts loaded (may be NULL). 0 = ok, else err filled. */
+int apus_ghip_store_load_container(ApusGhipStore *s, const char *dir, int layer,
+                                   int *n_loaded, char *err, size_t errcap);
+/* The index lookup alone (host only, no device): shard file name and file
+ * offset of the slab (layers.<layer>, expert), checked to hold slab_bytes.
+ * Extension for loaders and tests; no counterpart in the reference. */
+int apus_ghip_container_slab(const char *dir, int layer, int expert, size_t slab_bytes,
+                             char *shard, size_t shard_cap, uint64_t *offset,
+                             char *err, size_t errcap);
 /* Dequant-on-fill: expert e's BF16 payload [gate | up | down] into a host
  * buffer (3*inter*dim u16), bitwise c/gcache.h:413-426. */
 int apus_ghip_store_expert_bf16(ApusGhipStore *s, int expert,

@@ -82,6 +82,58 @@ def test_store_roundtrip(small):
             assert np.array_equal(dev[d:d + n], slabs[e][h:h + n]), (e, h)
 
 
+def test_store_load_container(ghip, tmp_path):
+    """A converted v2 container (two layers in two shards): the layer's
+    listed experts load bitwise (one pread per slab), unlisted ones keep
+    their bytes, another layer loads its own slabs, and the decode over the
+    loaded bank matches the oracle on the same slabs."""
+    from container_util import write_container
+    E, dim, inter = 16, 256, 128
+    rng = np.random.default_rng(77)
+    l3 = random_slabs(E, dim, inter, rng)
+    l4 = random_slabs(E, dim, inter, rng)
+    listed = [e for e in range(E) if e != 6]
+    write_container(str(tmp_path), {3: {e: l3[e] for e in listed},
+                                    4: {e: l4[e] for e in range(E)}}, l3[0].nbytes)
+    s = open_store(ghip, E, dim, inter)
+    try:
+        sb = ghip.apus_ghip_store_slab_bytes(s)
+        assert ghip.apus_ghip_store_put(s, 6, O.ptr(l4[6]), sb) == 0
+        n = ctypes.c_int()
+        err = ctypes.create_string_buffer(512)
+        assert ghip.apus_ghip_store_load_container(s, str(tmp_path).encode(), 3,
+                                                   ctypes.byref(n), err, 512) == 0, err.value
+        assert n.value == E - 1
+        got = np.empty(sb, np.uint8)
+        for e in range(E):
+            assert ghip.apus_ghip_store_get(s, e, O.ptr(got), sb) == 0
+            assert np.array_equal(got, l4[6] if e == 6 else l3[e]), e
+        bank = [l4[6] if e == 6 else l3[e] for e in range(E)]
+        x = O.f32_to_bf16(rng.standard_normal(dim).astype(np.float32))
+        idx = np.array([6, 2, 11], np.int32)
+        w = np.array([0.5, 0.3, 0.2], np.float32)
+        out = np.empty(dim, np.uint16)
+        assert ghip.apus_ghip_moe_decode(s, O.ptr(x), O.ptr(idx), O.ptr(w), 3, O.ptr(out)) == 0
+        want, eo = O.moe_forward(bank, dim, inter, x, idx[None], w[None], want_expert_out=True)
+        assert_close_combined(out, want[0], moe_floor(eo, w[None], idx[None])[0],
+                              "decode over a container-loaded bank")
+        assert ghip.apus_ghip_store_load_container(s, str(tmp_path).encode(), 4,
+                                                   ctypes.byref(n), err, 512) == 0
+        assert n.value == E
+        assert ghip.apus_ghip_store_get(s, 0, O.ptr(got), sb) == 0
+        assert np.array_equal(got, l4[0])
+        # a container for another slab size is refused, nothing loaded
+        s2 = open_store(ghip, E, dim, 2 * inter)
+        try:
+            assert ghip.apus_ghip_store_load_container(s2, str(tmp_path).encode(), 3,
+                                                       ctypes.byref(n), err, 512) == 1
+            assert b"holds" in err.value and n.value == 0
+        finally:
+            ghip.apus_ghip_store_close(s2)
+    finally:
+        ghip.apus_ghip_store_close(s)
+
+
 def test_store_synth_matches_host_generator(ghip, pkg):
     """The device synthetic fill writes the host generator's slab
     (include/apus_synth.h streams), read back through store_get."""
