@@ -20,6 +20,8 @@
 
 #include <hip/hip_runtime_api.h>
 #include <fcntl.h>
+#include <pthread.h>
+#include <semaphore.h>
 #include <stdarg.h>
 #include <unistd.h>
 #include <stdio.h>
@@ -357,7 +359,7 @@ int apus_ghip_bf16_gemm(const uint16_t *w, const uint16_t *x, uint16_t *y,
         || h2d(G.d_x, x, M * K * 2))
         return 1;
     HIPCHK(ghip_launch_bf16_linear((const uint16_t *)dw, (const uint16_t *)G.d_x,
-                                   (uint16_t *)G.d_y, M, O, K, G.stream));
+                                   (uint16_t *)G.d_y, M, O, K, NULL, G.stream));
     G.dispatches++;
     if (sync_out(y, G.d_y, M * O * 2)) return 1;
     G.off_bf16++;
@@ -489,7 +491,8 @@ int apus_ghip_bf16_gemm_dev(const uint16_t *w, const uint16_t *x,
                             uint16_t *y, size_t M, size_t O, size_t K,
                             void *stream) {
     if (ghip_init() || check_sizes(M, O, K)) return 1;
-    HIPCHK(ghip_launch_bf16_linear(w, x, y, M, O, K, (hipStream_t)stream));
+    HIPCHK(ghip_launch_bf16_linear(w, x, y, M, O, K, G.trace_n >= 2 ? G.trace_ev : NULL,
+                                   (hipStream_t)stream));
     G.dispatches++;
     return 0;
 }
@@ -670,6 +673,68 @@ int apus_ghip_store_get(ApusGhipStore *s, int expert, void *slab, size_t nbytes)
     return 0;
 }
 
+/* Parallel pread of one slab for the container loader. A shard in the host
+ * page cache is read at one thread's memcpy rate (~25 GB/s), below the host
+ * link, so each slab is split into one part per reader of a pool that
+ * lives for one load call; the main thread hands out a slab by posting
+ * each reader's semaphore and waits for as many completions. */
+#define GHIP_LOAD_THREADS 4
+
+typedef struct {
+    sem_t go[GHIP_LOAD_THREADS], done;
+    int fd, quit, nthr;
+    uint8_t *dst;
+    uint64_t off;
+    size_t bytes;
+    int ok[GHIP_LOAD_THREADS];
+} SlabReader;
+
+typedef struct {
+    SlabReader *r;
+    int t;
+} SlabReaderArg;
+
+static int pread_full(int fd, uint8_t *dst, size_t n, uint64_t off) {
+    size_t got = 0;
+    while (got < n) {
+        ssize_t k = pread(fd, dst + got, n - got, (off_t)(off + got));
+        if (k <= 0) return 0;
+        got += (size_t)k;
+    }
+    return 1;
+}
+
+static void *slab_reader_main(void *arg) {
+    SlabReaderArg *a = (SlabReaderArg *)arg;
+    SlabReader *r = a->r;
+    for (;;) {
+        while (sem_wait(&r->go[a->t]) != 0) {}
+        if (r->quit) break;
+        const size_t part = (r->bytes + (size_t)r->nthr - 1) / (size_t)r->nthr;
+        const size_t lo = (size_t)a->t * part < r->bytes ? (size_t)a->t * part : r->bytes;
+        const size_t hi = lo + part < r->bytes ? lo + part : r->bytes;
+        r->ok[a->t] = pread_full(r->fd, r->dst + lo, hi - lo, r->off + lo);
+        sem_post(&r->done);
+    }
+    return NULL;
+}
+
+/* one slab through the pool (nthr > 0) or on this thread */
+static int slab_read(SlabReader *r, int fd, uint8_t *dst, size_t n, uint64_t off) {
+    if (!r->nthr) return pread_full(fd, dst, n, off);
+    r->fd = fd;
+    r->dst = dst;
+    r->off = off;
+    r->bytes = n;
+    for (int t = 0; t < r->nthr; t++) sem_post(&r->go[t]);
+    int ok = 1;
+    for (int t = 0; t < r->nthr; t++) {
+        while (sem_wait(&r->done) != 0) {}
+    }
+    for (int t = 0; t < r->nthr; t++) ok &= r->ok[t];
+    return ok;
+}
+
 int apus_ghip_store_load_container(ApusGhipStore *s, const char *dir, int layer,
                                    int *n_loaded, char *err, size_t errcap) {
     if (n_loaded) *n_loaded = 0;
@@ -695,8 +760,9 @@ int apus_ghip_store_load_container(ApusGhipStore *s, const char *dir, int layer,
             free(recs);
             return 1;
         }
-    /* two pinned slab buffers: the pread of slab i+1 overlaps the H2D of
-     * slab i (one pread per slab, as c/gcache.h:394-451) */
+    /* two pinned slab buffers: the read of slab i+1 overlaps the H2D of
+     * slab i (one slab per read, as the reference's one pread per slab,
+     * c/gcache.h:394-451, here split over the reader pool) */
     uint8_t *pin[2] = {NULL, NULL};
     hipEvent_t done[2] = {NULL, NULL};
     int fds_n = 0, rc = 0;
@@ -705,6 +771,24 @@ int apus_ghip_store_load_container(ApusGhipStore *s, const char *dir, int layer,
         rc = hipHostMalloc((void **)&pin[b], s->h_bytes, 0) != hipSuccess
              || hipEventCreateWithFlags(&done[b], hipEventDisableTiming) != hipSuccess;
     if (rc) ghip_seterr("store_load_container: pinned staging (%zu B) failed", s->h_bytes);
+    /* reader pool (as many readers as could be started; none: this thread
+     * reads) */
+    SlabReader rd;
+    SlabReaderArg rarg[GHIP_LOAD_THREADS];
+    pthread_t rthr[GHIP_LOAD_THREADS];
+    memset(&rd, 0, sizeof rd);
+    int sems = 0;
+    if (sem_init(&rd.done, 0, 0) == 0) {
+        sems = 1;
+        for (; sems <= GHIP_LOAD_THREADS && sem_init(&rd.go[sems - 1], 0, 0) == 0; sems++) {}
+    }
+    /* sems - 1 go-semaphores exist */
+    for (int t = 0; !rc && t < sems - 1; t++) {
+        rarg[t].r = &rd;
+        rarg[t].t = t;
+        if (pthread_create(&rthr[t], NULL, slab_reader_main, &rarg[t])) break;
+        rd.nthr = t + 1;
+    }
     int loaded = 0;
     for (int i = 0; i < n && !rc; i++) {
         int fd = -1;
@@ -729,13 +813,7 @@ int apus_ghip_store_load_container(ApusGhipStore *s, const char *dir, int layer,
             rc = 1;
             break;
         }
-        size_t got = 0;
-        while (got < s->h_bytes) {
-            ssize_t r = pread(fd, h + got, s->h_bytes - got, (off_t)(recs[i].offset + got));
-            if (r <= 0) break;
-            got += (size_t)r;
-        }
-        if (got != s->h_bytes) {
+        if (!slab_read(&rd, fd, h, s->h_bytes, recs[i].offset)) {
             ghip_seterr("store_load_container: short read of (layers.%d, %d) in %s",
                         layer, recs[i].expert, recs[i].shard);
             rc = 1;
@@ -761,6 +839,11 @@ int apus_ghip_store_load_container(ApusGhipStore *s, const char *dir, int layer,
         ghip_seterr("store_load_container: sync failed");
         rc = 1;
     }
+    rd.quit = 1;
+    for (int t = 0; t < rd.nthr; t++) sem_post(&rd.go[t]);
+    for (int t = 0; t < rd.nthr; t++) pthread_join(rthr[t], NULL);
+    for (int t = 0; t < sems - 1; t++) sem_destroy(&rd.go[t]);
+    if (sems) sem_destroy(&rd.done);
     for (int k = 0; k < fds_n; k++) close(fds[k].fd);
     for (int b = 0; b < 2; b++) {
         if (pin[b]) hipHostFree(pin[b]);
@@ -905,7 +988,10 @@ int apus_ghip_moe_decode_dev(ApusGhipStore *s, const uint16_t *x,
     return 0;
 }
 
-static float *g_router_logits;          /* device [512] f32 router workspace */
+/* device router workspace: logits [512] f32, then the one-launch router's
+ * arrival counter (one u32, 0 between launches) */
+static float *g_router_logits;
+#define GHIP_ROUTER_WS_WORDS (512 + 64)
 
 int apus_ghip_moe_router_dev(const uint16_t *x, const uint16_t *gate_w,
                              const float *logits, const float *gate_bias, int E,
@@ -917,11 +1003,17 @@ int apus_ghip_moe_router_dev(const uint16_t *x, const uint16_t *gate_w,
         ghip_seterr("moe_router: bad arguments (E=%d topk=%d dim=%zu)", E, topk, dim);
         return 1;
     }
-    if (!logits && !g_router_logits)
-        HIPCHK(hipMalloc((void **)&g_router_logits, 512 * sizeof(float)));
-    hipError_t e = ghip_launch_moe_router(x, gate_w, logits, g_router_logits, gate_bias,
-                                          (uint32_t)E, (uint32_t)dim, topk, route_scale,
-                                          scores, idx, w, (hipStream_t)stream);
+    if (!logits && !g_router_logits) {
+        HIPCHK(hipMalloc((void **)&g_router_logits, GHIP_ROUTER_WS_WORDS * sizeof(float)));
+        HIPCHK(hipMemset(g_router_logits, 0, GHIP_ROUTER_WS_WORDS * sizeof(float)));
+        HIPCHK(hipDeviceSynchronize());
+    }
+    hipError_t e = ghip_launch_moe_router(x, gate_w, logits, g_router_logits,
+                                          logits ? NULL : (uint32_t *)(g_router_logits + 512),
+                                          gate_bias, (uint32_t)E, (uint32_t)dim, topk,
+                                          route_scale, scores, idx, w,
+                                          G.trace_n >= 2 ? G.trace_ev : NULL,
+                                          (hipStream_t)stream);
     if (e != hipSuccess) {
         ghip_seterr("moe_router launch: %s (dim %% 8 and 16-byte x / gate_w required)",
                     hipGetErrorString(e));

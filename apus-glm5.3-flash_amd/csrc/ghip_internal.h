@@ -35,10 +35,11 @@ hipError_t ghip_launch_fp8_linear(const uint8_t *codes, const float *scales,
                                   size_t O, size_t K, const uint32_t *exact_dev,
                                   const hipEvent_t *ev, hipStream_t st);
 
-/* BF16-weight GEMV/GEMM: y[M,O] = x[M,K] . W[O,K]^T. Any shape. */
+/* BF16-weight GEMV/GEMM: y[M,O] = x[M,K] . W[O,K]^T. Any shape. ev: NULL or
+ * two timing events (start on the first launch, stop on the last). */
 hipError_t ghip_launch_bf16_linear(const uint16_t *w, const uint16_t *x,
                                    uint16_t *y, size_t M, size_t O, size_t K,
-                                   hipStream_t st);
+                                   const hipEvent_t *ev, hipStream_t st);
 
 /* K3 MoE decode workspace (device): the routing handoff between the
  * launches, the SwiGLU activations, and an error word. */
@@ -83,12 +84,16 @@ hipError_t ghip_launch_moe_decode(const GhipBank *bank, const uint16_t *x,
  * GEMV over gate_w [E, dim] bf16 into logits_ws [E] f32, or given
  * logits_in), numpy-stable sigmoid scores, stable top-k of score + bias,
  * pairwise-sum normalization x scale. scores [E] optional; idx / w [topk]
- * in selection order. E <= 512, topk <= 16. */
+ * in selection order. E <= 512, topk <= 16. One launch either way; with
+ * gate_w, `count` is a device word that is 0 before the launch and 0 after
+ * it (launches that overlap on one device race on it and on logits_ws).
+ * ev: NULL or two timing events around the launch. */
 hipError_t ghip_launch_moe_router(const uint16_t *x, const uint16_t *gate_w,
                                   const float *logits_in, float *logits_ws,
-                                  const float *bias, uint32_t E, uint32_t dim,
-                                  int topk, float scale, float *scores,
-                                  int32_t *idx, float *w, hipStream_t st);
+                                  uint32_t *count, const float *bias, uint32_t E,
+                                  uint32_t dim, int topk, float scale, float *scores,
+                                  int32_t *idx, float *w, const hipEvent_t *ev,
+                                  hipStream_t st);
 
 /* K4 prefill workspace (device; sized for cap_pairs = T * topk pairs). */
 #define PF_HDR_NTILES 0

@@ -461,20 +461,21 @@ extern "C" hipError_t ghip_launch_fp8_linear(const uint8_t *codes,
 
 template <int M>
 static hipError_t launch_bf16_gemv_m(const uint16_t *w, const uint16_t *x, uint16_t *y,
-                                     size_t O, size_t K, hipStream_t st) {
+                                     size_t O, size_t K, hipEvent_t ev0, hipEvent_t ev1,
+                                     hipStream_t st) {
     const size_t groups = (O + 15) / 16;
     const size_t lds = gs_lds(M, K);
     const uint8_t *wb = (const uint8_t *)w;
     if ((groups + 3) / 4 >= g_gs_ncu) {              /* KS = 2: 4 groups a pass */
         uint32_t g = (uint32_t)((groups + 3) / 4);
         if (g > g_gs_ncu) g = g_gs_ncu;
-        hipLaunchKernelGGL((k_fp8_gemv_stream<M, 2, true>), dim3(g), dim3(GS_NW * 64), lds,
-                           st, wb, nullptr, x, y, (uint32_t)O, (uint32_t)K, nullptr);
+        GHIP_LAUNCH(ev0, ev1, (k_fp8_gemv_stream<M, 2, true>), dim3(g), dim3(GS_NW * 64),
+                    lds, st, wb, nullptr, x, y, (uint32_t)O, (uint32_t)K, nullptr);
     } else {                                           /* KS = 8: 1 group a pass */
         uint32_t g = (uint32_t)groups;
         if (g > g_gs_ncu) g = g_gs_ncu;
-        hipLaunchKernelGGL((k_fp8_gemv_stream<M, 8, true>), dim3(g), dim3(GS_NW * 64), lds,
-                           st, wb, nullptr, x, y, (uint32_t)O, (uint32_t)K, nullptr);
+        GHIP_LAUNCH(ev0, ev1, (k_fp8_gemv_stream<M, 8, true>), dim3(g), dim3(GS_NW * 64),
+                    lds, st, wb, nullptr, x, y, (uint32_t)O, (uint32_t)K, nullptr);
     }
     return hipGetLastError();
 }
@@ -482,10 +483,12 @@ static hipError_t launch_bf16_gemv_m(const uint16_t *w, const uint16_t *x, uint1
 extern "C" hipError_t ghip_launch_bf16_linear(const uint16_t *w,
                                               const uint16_t *x, uint16_t *y,
                                               size_t M, size_t O, size_t K,
-                                              hipStream_t st) {
+                                              const hipEvent_t *ev, hipStream_t st) {
     if (M == 0 || O == 0) return hipSuccess;
     if (K == 0 || O > 0x7fffffffu || K > 0x7fffffffu || M > 0x7fffffffu)
         return hipErrorInvalidValue;
+    /* timing events: start on the first launch, stop on the last */
+    hipEvent_t ev0 = ev ? ev[0] : nullptr, ev1 = ev ? ev[1] : nullptr;
     /* the streaming MFMA GEMV, in groups of <= 4 token rows (each reading
      * the weights once), when the shape and alignment allow */
     if (g_gs_ncu && K % 64 == 0 && ((uintptr_t)w & 15) == 0 && ((uintptr_t)x & 15) == 0
@@ -497,12 +500,13 @@ extern "C" hipError_t ghip_launch_bf16_linear(const uint16_t *w,
             while (mc > 1 && gs_lds(mc, K) > GS_LDS) mc--;
             const uint16_t *xm = x + m0 * K;
             uint16_t *ym = y + m0 * O;
+            hipEvent_t a = m0 == 0 ? ev0 : nullptr, b = m0 + mc == M ? ev1 : nullptr;
             hipError_t e;
             switch (mc) {
-            case 4: e = launch_bf16_gemv_m<4>(w, xm, ym, O, K, st); break;
-            case 3: e = launch_bf16_gemv_m<3>(w, xm, ym, O, K, st); break;
-            case 2: e = launch_bf16_gemv_m<2>(w, xm, ym, O, K, st); break;
-            default: e = launch_bf16_gemv_m<1>(w, xm, ym, O, K, st); break;
+            case 4: e = launch_bf16_gemv_m<4>(w, xm, ym, O, K, a, b, st); break;
+            case 3: e = launch_bf16_gemv_m<3>(w, xm, ym, O, K, a, b, st); break;
+            case 2: e = launch_bf16_gemv_m<2>(w, xm, ym, O, K, a, b, st); break;
+            default: e = launch_bf16_gemv_m<1>(w, xm, ym, O, K, a, b, st); break;
             }
             if (e != hipSuccess) return e;
             m0 += mc;
@@ -511,9 +515,8 @@ extern "C" hipError_t ghip_launch_bf16_linear(const uint16_t *w,
     }
     size_t items = M * O;
     if (items > 0xffffffffull * 4) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_bf16_linear_any, dim3((uint32_t)((items + 3) / 4)),
-                       dim3(256), 0, st, w, x, y, (uint32_t)M, (uint32_t)O,
-                       (uint32_t)K);
+    GHIP_LAUNCH(ev0, ev1, k_bf16_linear_any, dim3((uint32_t)((items + 3) / 4)),
+                dim3(256), 0, st, w, x, y, (uint32_t)M, (uint32_t)O, (uint32_t)K);
     return hipGetLastError();
 }
 

@@ -47,50 +47,129 @@
 /* routing                                                                  */
 /* ------------------------------------------------------------------------ */
 
-#define RT_REG 8                 /* logits per lane held in registers */
-#define RT_MAXE (64 * RT_REG)    /* 512 experts */
+#define RT_MAXE 512              /* experts a routing wave can hold (8 per lane) */
 
-/* Monotone key of (value, index): larger value first, then LOWER index —
- * the stable top-k order of c/gmoe.h:175-189 — as one unsigned 64-bit max. */
-__device__ __forceinline__ uint64_t rt_key(float v, int i) {
-    /* -0 and +0 compare equal in the reference, so they must share a key */
+/* Monotone u32 key of a float: a larger value gives a larger key, and -0
+ * and +0 share one (they compare equal in the reference). Keys are >= 1, so
+ * 0 marks an empty or already-taken slot. */
+__device__ __forceinline__ uint32_t rt_key(float v) {
     uint32_t u = __float_as_uint(v == 0.0f ? 0.0f : v);
     u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    return ((uint64_t)u << 32) | (uint32_t)(0xffffffffu - (uint32_t)i);
+    return u ? u : 1u;
 }
 
-/* k = max(k, k moved by a DPP pattern); lanes without a source keep k */
-template <int CTRL, int ROWMASK>
-__device__ __forceinline__ uint64_t rt_dpp_max(uint64_t k) {
-    const int lo = (int)(uint32_t)k, hi = (int)(uint32_t)(k >> 32);
-    const uint32_t olo = (uint32_t)__builtin_amdgcn_update_dpp(lo, lo, CTRL, ROWMASK, 0xf, false);
-    const uint32_t ohi = (uint32_t)__builtin_amdgcn_update_dpp(hi, hi, CTRL, ROWMASK, 0xf, false);
-    const uint64_t o = ((uint64_t)ohi << 32) | olo;
-    return o > k ? o : k;
+/* the value of a key (the inverse of rt_key for every non-NaN value) */
+__device__ __forceinline__ float rt_val(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
-/* 64-bit wave max on DPP (VALU lane moves, no LDS round trips): row shifts
- * give each row's max in its lane 15, two row broadcasts carry it to lane
- * 63, read back as a wave-uniform value. */
-__device__ __forceinline__ uint64_t rt_wave_max(uint64_t k) {
-    k = rt_dpp_max<0x111, 0xf>(k);       /* row_shr:1 */
-    k = rt_dpp_max<0x112, 0xf>(k);       /* row_shr:2 */
-    k = rt_dpp_max<0x114, 0xf>(k);       /* row_shr:4 */
-    k = rt_dpp_max<0x118, 0xf>(k);       /* row_shr:8 */
-    k = rt_dpp_max<0x142, 0xa>(k);       /* row_bcast:15 */
-    k = rt_dpp_max<0x143, 0xc>(k);       /* row_bcast:31 */
-    const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)k, 63);
-    const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(k >> 32), 63);
-    return ((uint64_t)hi << 32) | lo;
+/* k = max (or min) of k and k moved by a DPP pattern; lanes without a
+ * source keep k */
+template <int CTRL, int ROWMASK, bool MAX>
+__device__ __forceinline__ uint32_t rt_dpp(uint32_t k) {
+    const uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp((int)k, (int)k, CTRL, ROWMASK,
+                                                             0xf, false);
+    return MAX ? (o > k ? o : k) : (o < k ? o : k);
+}
+
+/* Wave max (or min) on DPP (VALU lane moves, no LDS round trips): row
+ * shifts leave each row's result in its lane 15, two row broadcasts carry
+ * it to lane 63, read back as a wave-uniform value. */
+template <bool MAX>
+__device__ __forceinline__ uint32_t rt_wave_red(uint32_t k) {
+    k = rt_dpp<0x111, 0xf, MAX>(k);      /* row_shr:1 */
+    k = rt_dpp<0x112, 0xf, MAX>(k);      /* row_shr:2 */
+    k = rt_dpp<0x114, 0xf, MAX>(k);      /* row_shr:4 */
+    k = rt_dpp<0x118, 0xf, MAX>(k);      /* row_shr:8 */
+    k = rt_dpp<0x142, 0xa, MAX>(k);      /* row_bcast:15 */
+    k = rt_dpp<0x143, 0xc, MAX>(k);      /* row_bcast:31 */
+    return (uint32_t)__builtin_amdgcn_readlane((int)k, 63);
+}
+
+/* Stable top-k by one wave (c/gmoe.h:175-189: larger first, ties to the
+ * lower index): slot s of lane l holds the key of index l + 64 s (0 =
+ * empty). Each of the k rounds takes the largest key (a lane-local max and
+ * one DPP wave max); the lanes holding it name their lowest index, and a
+ * second wave reduction (min index) runs only when more than one lane
+ * does. Lane j < k returns pick j's index and its key in mykey. */
+template <int R>
+__device__ __forceinline__ int rt_select(uint32_t (&key)[R], int topk, uint32_t &mykey) {
+    const uint32_t lane = threadIdx.x & 63u;
+    int myid = -1;
+    mykey = 0u;
+    for (int j = 0; j < topk; j++) {
+        uint32_t lm = key[0];
+#pragma unroll
+        for (int s = 1; s < R; s++) lm = key[s] > lm ? key[s] : lm;
+        const uint32_t wm = rt_wave_red<true>(lm);
+        uint32_t cand = 0xffffffffu;
+#pragma unroll
+        for (int s = R - 1; s >= 0; s--)
+            if (key[s] == wm) cand = lane + 64u * s;
+        const uint64_t bal = __ballot(cand != 0xffffffffu);
+        uint32_t widx;
+        if (__popcll(bal) == 1)
+            widx = (uint32_t)__builtin_amdgcn_readlane((int)cand, (int)__builtin_ctzll(bal));
+        else
+            widx = rt_wave_red<false>(cand);
+#pragma unroll
+        for (int s = 0; s < R; s++)
+            if (lane + 64u * s == widx) key[s] = 0u;
+        if ((int)lane == j) {
+            myid = (int)widx;
+            mykey = wm;
+        }
+    }
+    return myid;
+}
+
+/* the harness routing from logits: stable top-k, softmax over the k
+ * selected in slot order (m = slot 0's logit, e_j = expf(l_j - m),
+ * s = e_0 + e_1 + ... ascending j, w = e / s); kept slots placed by
+ * ascending id. R logits per lane. */
+template <int R>
+__device__ __forceinline__ void md_route_softmax(const float *__restrict__ logits, int topk,
+                                                 int E, uint32_t *rt) {
+    const int lane = threadIdx.x & 63;
+    uint32_t key[R];
+#pragma unroll
+    for (int s = 0; s < R; s++) {
+        const int i = lane + 64 * s;
+        key[s] = i < E ? rt_key(logits[i]) : 0u;
+    }
+    uint32_t mk;
+    const int myid = rt_select<R>(key, topk, mk);
+    const float mylog = rt_val(mk);
+    const float m = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                                  __builtin_bit_cast(int, mylog), 0));
+    const float ej = expf(mylog - m);
+    float ssum = 0.0f;
+    for (int j = 0; j < topk; j++)
+        ssum = ssum + __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                                     __builtin_bit_cast(int, ej), j));
+    const float wj = ej / ssum;
+    /* distinct ids: place slot j by its rank among the k ids */
+    int pos = 0;
+    for (int j = 0; j < topk; j++)
+        pos += __builtin_amdgcn_readlane(myid, j) < myid;
+    if (lane < MD_MAXK) {
+        rt[RT_IDS + lane] = 0u;
+        rt[RT_W + lane] = 0u;
+    }
+    __builtin_amdgcn_wave_barrier();
+    if (lane < topk) {
+        rt[RT_IDS + pos] = (uint32_t)myid;
+        rt[RT_W + pos] = __float_as_uint(wj);
+    }
+    if (lane == 0) rt[RT_NSEL] = (uint32_t)topk;
+    __builtin_amdgcn_s_waitcnt(0xc07f);           /* lgkmcnt(0) */
+    __builtin_amdgcn_wave_barrier();
 }
 
 /* Routing by one wave into rt[] (an LDS route record: RT_NSEL, RT_IDS,
- * RT_W words). Either the harness routing (stable top-k of f32 logits,
- * ties -> lower id, softmax over the k selected, in slot order) or given
- * idx/w; a repeated id keeps its first slot (c/gmoe.h:309-312), kept slots
- * are placed by ascending expert id (the combine order). Logits live in
- * registers (RT_REG per lane); each of the k rounds takes the lane-local
- * best key and one 64-bit wave max. */
+ * RT_W words). Either the harness routing from logits (md_route_softmax)
+ * or given idx/w; a repeated id keeps its first slot (c/gmoe.h:309-312),
+ * kept slots are placed by ascending expert id (the combine order). */
 __device__ __forceinline__ void md_route(const float *__restrict__ logits,
                                          const int32_t *__restrict__ idx,
                                          const float *__restrict__ w, int topk, int E,
@@ -98,55 +177,8 @@ __device__ __forceinline__ void md_route(const float *__restrict__ logits,
                                          uint32_t *__restrict__ err) {
     const int lane = threadIdx.x & 63;
     if (logits) {
-        uint64_t key[RT_REG];
-#pragma unroll
-        for (int s = 0; s < RT_REG; s++) {
-            int i = lane + 64 * s;
-            key[s] = i < E ? rt_key(logits[i], i) : 0ull;
-        }
-        /* slot j's (id, logit) ends in lane j */
-        int myid = -1;
-        float mylog = 0.0f;
-        for (int j = 0; j < topk; j++) {
-            uint64_t b = 0;
-#pragma unroll
-            for (int s = 0; s < RT_REG; s++) b = key[s] > b ? key[s] : b;
-            b = rt_wave_max(b);
-#pragma unroll
-            for (int s = 0; s < RT_REG; s++)
-                if (key[s] == b) key[s] = 0ull;
-            if (lane == j) {
-                /* the value is in the key: undo the monotone transform */
-                const uint32_t hi = (uint32_t)(b >> 32);
-                myid = (int)(0xffffffffu - (uint32_t)b);
-                mylog = __uint_as_float((hi & 0x80000000u) ? (hi & 0x7fffffffu) : ~hi);
-            }
-        }
-        /* softmax over the k slots in slot order: m = slot 0's logit,
-         * e_j = expf(l_j - m), s = e_0 + e_1 + ... (ascending j), w = e / s */
-        const float m = __shfl(mylog, 0, 64);
-        const float ej = expf(mylog - m);
-        float ssum = 0.0f;
-        for (int j = 0; j < topk; j++)
-            ssum = ssum + __builtin_bit_cast(float, __builtin_amdgcn_readlane(
-                                                         __builtin_bit_cast(int, ej), j));
-        const float wj = ej / ssum;
-        /* distinct ids: place slot j by its rank among the k ids */
-        int pos = 0;
-        for (int j = 0; j < topk; j++)
-            pos += __builtin_amdgcn_readlane(myid, j) < myid;
-        if (lane < MD_MAXK) {
-            rt[RT_IDS + lane] = 0u;
-            rt[RT_W + lane] = 0u;
-        }
-        __builtin_amdgcn_wave_barrier();
-        if (lane < topk) {
-            rt[RT_IDS + pos] = (uint32_t)myid;
-            rt[RT_W + pos] = __float_as_uint(wj);
-        }
-        if (lane == 0) rt[RT_NSEL] = (uint32_t)topk;
-        __builtin_amdgcn_s_waitcnt(0xc07f);       /* lgkmcnt(0) */
-        __builtin_amdgcn_wave_barrier();
+        if (E <= 5 * 64) md_route_softmax<5>(logits, topk, E, rt);
+        else md_route_softmax<8>(logits, topk, E, rt);
         return;
     }
     if (lane < topk) {
@@ -162,17 +194,13 @@ __device__ __forceinline__ void md_route(const float *__restrict__ logits,
         keep = false;
         if (err) atomicOr(err, 2u);
     }
-    for (int q = 0; q < MD_MAXK; q++) {
-        const int eq = __shfl(e, q, 64);
-        if (q < lane && q < topk && eq == e) keep = false;
-    }
-    int pos = 0;
-    for (int q = 0; q < MD_MAXK; q++) {
-        const int eq = __shfl(e, q, 64);
-        const int kq = __shfl((int)keep, q, 64);
-        pos += (kq && eq < e);
-    }
+    /* slot q is uniform: read it with readlane, not a lane permute */
+    for (int q = 0; q < topk; q++)
+        if (q < lane && __builtin_amdgcn_readlane(e, q) == e) keep = false;
     const uint64_t kept = __ballot(keep);
+    int pos = 0;
+    for (int q = 0; q < topk; q++)
+        pos += ((kept >> q) & 1u) && __builtin_amdgcn_readlane(e, q) < e;
     const uint32_t nsel = (uint32_t)__popcll(kept);
     if (lane < MD_MAXK) {                 /* clear, then place kept slots */
         rt[RT_IDS + lane] = 0u;
@@ -228,6 +256,9 @@ __device__ __forceinline__ void md_phase_route(const GhipBank &bank,
                  blockIdx.x == 0 ? err : nullptr);
     for (uint32_t i = tid; i < (bank.dim >> 3); i += GU_NW * 64)
         ((ghip_u32x4 *)xs)[i] = ((const ghip_u32x4 *)x)[i];
+    /* nothing of the routing (its error-flag atomic included) stays in
+     * flight into the streaming loops, whose vmcnt waits count only DMA */
+    GHIP_VMCNT(0);
     __syncthreads();
 }
 
@@ -525,30 +556,41 @@ __global__ __launch_bounds__(MD_NW * 64, 1) void k_moe_down(
 /* router with the reference semantics (c/gmoe.h:191-208)                   */
 /* ------------------------------------------------------------------------ */
 
-/* Gate logits: one wave per gate row, logits[e] = sum_k w[e,k] * x[k] in
- * f32 (lane-strided partial sums + a fixed xor-butterfly reduction: a GEMV
- * of the same tolerance class as every other one here; the reference's
- * sequential-k dot is c/gmoe.h:168-173). dim % 8 == 0, 16-byte rows. */
-__global__ __launch_bounds__(256) void k_router_logits(const uint16_t *__restrict__ gate_w,
-                                                       const uint16_t *__restrict__ x,
-                                                       uint32_t E, uint32_t dim,
-                                                       float *__restrict__ logits) {
-    const uint32_t lane = threadIdx.x & 63u, e = blockIdx.x * 4u + (threadIdx.x >> 6);
-    if (e >= E) return;
-    const uint16_t *row = gate_w + (size_t)e * dim;
+/* Gate logit of one row by one wave: sum_k w[k] * x[k] in f32, lane-strided
+ * partial sums (lane l takes k = 8l + 512i, ascending i) and a fixed
+ * xor-butterfly reduction: a GEMV of the same tolerance class as every
+ * other one here (the reference's sequential-k dot is c/gmoe.h:168-173).
+ * Eight row segments per lane are loaded before any is used, so a row
+ * costs one memory round trip, not one per segment. dim % 8 == 0, 16-byte
+ * aligned rows. */
+__device__ __forceinline__ float rt_gate_dot(const uint16_t *__restrict__ row,
+                                             const uint16_t *__restrict__ x, uint32_t dim,
+                                             uint32_t lane) {
     float acc = 0.0f;
-    for (uint32_t k = lane * 8u; k < dim; k += 512u) {
-        const ghip_u32x4 wv = *(const ghip_u32x4 *)(row + k);
-        const ghip_u32x4 xv = *(const ghip_u32x4 *)(x + k);
+    auto fma8 = [&](const ghip_u32x4 &wv, const ghip_u32x4 &xv) {
 #pragma unroll
         for (int q = 0; q < 4; q++) {
             acc = acc + __uint_as_float(wv[q] << 16) * __uint_as_float(xv[q] << 16);
-            acc = acc + __uint_as_float(wv[q] & 0xffff0000u) * __uint_as_float(xv[q] & 0xffff0000u);
+            acc = acc + __uint_as_float(wv[q] & 0xffff0000u) *
+                            __uint_as_float(xv[q] & 0xffff0000u);
         }
+    };
+    uint32_t k = lane * 8u;
+    for (; k + 7u * 512u < dim; k += 8u * 512u) {
+        ghip_u32x4 wv[8], xv[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            wv[u] = *(const ghip_u32x4 *)(row + k + 512u * u);
+            xv[u] = *(const ghip_u32x4 *)(x + k + 512u * u);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) fma8(wv[u], xv[u]);
     }
+    for (; k < dim; k += 512u)
+        fma8(*(const ghip_u32x4 *)(row + k), *(const ghip_u32x4 *)(x + k));
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) acc = acc + __shfl_xor(acc, off, 64);
-    if (lane == 0) logits[e] = acc;
+    return acc;
 }
 
 /* Selection and weights from the logits, one wave (c/gmoe.h:191-208):
@@ -557,40 +599,30 @@ __global__ __launch_bounds__(256) void k_router_logits(const uint16_t *__restric
  * never weighs -- then w_j = score[idx_j] / (pairwise_sum + 1e-20) *
  * route_scale, with numpy's float32 pairwise sum of the k selected scores
  * in selection order (c/gmhc.h:165-185). idx / w in selection order, as the
- * reference returns them. */
-__global__ __launch_bounds__(64) void k_router_select(const float *__restrict__ logits,
-                                                      const float *__restrict__ bias,
-                                                      uint32_t E, int topk, float scale,
-                                                      float *__restrict__ scores,
-                                                      int32_t *__restrict__ idx,
-                                                      float *__restrict__ w) {
-    __shared__ float sc[RT_MAXE];
+ * reference returns them. lg(i) loads logit i; sc is LDS [E]. */
+template <int R, typename Logit>
+__device__ __forceinline__ void rt_sigmoid_select(Logit lg, const float *__restrict__ bias,
+                                                  uint32_t E, int topk, float scale,
+                                                  float *sc, float *__restrict__ scores,
+                                                  int32_t *__restrict__ idx,
+                                                  float *__restrict__ w) {
     const int lane = threadIdx.x & 63;
-    uint64_t key[RT_REG];
+    uint32_t key[R];
 #pragma unroll
-    for (int s = 0; s < RT_REG; s++) {
+    for (int s = 0; s < R; s++) {
         const uint32_t i = (uint32_t)lane + 64u * s;
-        key[s] = 0ull;
+        key[s] = 0u;
         if (i < E) {
-            const float v = ghip_sigmoid_np(logits[i]);
+            const float v = ghip_sigmoid_np(lg(i));
             sc[i] = v;
             if (scores) scores[i] = v;
-            key[s] = rt_key(v + bias[i], (int)i);
+            key[s] = rt_key(v + bias[i]);
         }
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);           /* lgkmcnt(0) */
     __builtin_amdgcn_wave_barrier();
-    int myid = -1;
-    for (int j = 0; j < topk; j++) {
-        uint64_t b = 0;
-#pragma unroll
-        for (int s = 0; s < RT_REG; s++) b = key[s] > b ? key[s] : b;
-        b = rt_wave_max(b);
-#pragma unroll
-        for (int s = 0; s < RT_REG; s++)
-            if (key[s] == b) key[s] = 0ull;
-        if (lane == j) myid = (int)(0xffffffffu - (uint32_t)b);
-    }
+    uint32_t mk;
+    const int myid = rt_select<R>(key, topk, mk);
     const float myw = lane < topk ? sc[myid] : 0.0f;
     /* numpy float32 pairwise sum of the k selected scores (k <= 16) */
     auto at = [&](int i) {
@@ -619,27 +651,78 @@ __global__ __launch_bounds__(64) void k_router_select(const float *__restrict__ 
     }
 }
 
+/* The whole router in one launch: workgroup b's waves compute gate logits
+ * 4b..4b+3 and store them with agent-scope (device-coherent) stores; each
+ * workgroup waits for its stores, then bumps a counter; the workgroup that
+ * arrives last resets the counter and selects from the logits (read with
+ * agent-scope loads, so logits written on other XCDs are seen), with no
+ * second launch and no fences. The counter starts at 0 and every launch
+ * leaves it at 0; launches that overlap on one device race. */
+__global__ __launch_bounds__(256) void k_router(const uint16_t *__restrict__ gate_w,
+                                                const uint16_t *__restrict__ x, uint32_t E,
+                                                uint32_t dim, const float *__restrict__ bias,
+                                                int topk, float scale, float *logits_ws,
+                                                uint32_t *count, float *__restrict__ scores,
+                                                int32_t *__restrict__ idx,
+                                                float *__restrict__ w) {
+    __shared__ float sc[RT_MAXE];
+    __shared__ uint32_t last;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, e = blockIdx.x * 4u + (tid >> 6);
+    if (e < E) {
+        const float acc = rt_gate_dot(gate_w + (size_t)e * dim, x, dim, lane);
+        if (lane == 0)
+            __hip_atomic_store((uint32_t *)logits_ws + e, __float_as_uint(acc),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    GHIP_VMCNT(0);                                /* own logit stores complete */
+    __syncthreads();
+    if (tid == 0)
+        last = __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+               == gridDim.x - 1;
+    __syncthreads();
+    if (!last || tid >= 64) return;
+    if (tid == 0) __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    auto lg = [&](uint32_t i) {
+        return __uint_as_float(__hip_atomic_load((const uint32_t *)logits_ws + i,
+                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    };
+    if (E <= 5 * 64) rt_sigmoid_select<5>(lg, bias, E, topk, scale, sc, scores, idx, w);
+    else rt_sigmoid_select<8>(lg, bias, E, topk, scale, sc, scores, idx, w);
+}
+
+/* Selection from given logits (one wave). */
+__global__ __launch_bounds__(64) void k_router_select(const float *__restrict__ logits,
+                                                      const float *__restrict__ bias,
+                                                      uint32_t E, int topk, float scale,
+                                                      float *__restrict__ scores,
+                                                      int32_t *__restrict__ idx,
+                                                      float *__restrict__ w) {
+    __shared__ float sc[RT_MAXE];
+    auto lg = [&](uint32_t i) { return logits[i]; };
+    if (E <= 5 * 64) rt_sigmoid_select<5>(lg, bias, E, topk, scale, sc, scores, idx, w);
+    else rt_sigmoid_select<8>(lg, bias, E, topk, scale, sc, scores, idx, w);
+}
+
 extern "C" hipError_t ghip_launch_moe_router(const uint16_t *x, const uint16_t *gate_w,
                                              const float *logits_in, float *logits_ws,
-                                             const float *bias, uint32_t E, uint32_t dim,
-                                             int topk, float scale, float *scores,
-                                             int32_t *idx, float *w, hipStream_t st) {
+                                             uint32_t *count, const float *bias, uint32_t E,
+                                             uint32_t dim, int topk, float scale,
+                                             float *scores, int32_t *idx, float *w,
+                                             const hipEvent_t *ev, hipStream_t st) {
     if (!bias || !idx || !w || E == 0 || E > RT_MAXE || topk <= 0 || topk > MD_MAXK
         || (uint32_t)topk > E)
         return hipErrorInvalidValue;
-    const float *lg = logits_in;
-    if (!lg) {
-        if (!x || !gate_w || !logits_ws || dim == 0 || dim % 8 || ((uintptr_t)x & 15)
-            || ((uintptr_t)gate_w & 15))
+    hipEvent_t ev0 = ev ? ev[0] : nullptr, ev1 = ev ? ev[1] : nullptr;
+    if (!logits_in) {
+        if (!x || !gate_w || !logits_ws || !count || dim == 0 || dim % 8
+            || ((uintptr_t)x & 15) || ((uintptr_t)gate_w & 15))
             return hipErrorInvalidValue;
-        hipLaunchKernelGGL(k_router_logits, dim3((E + 3) / 4), dim3(256), 0, st, gate_w, x,
-                           E, dim, logits_ws);
-        hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
-        lg = logits_ws;
+        GHIP_LAUNCH(ev0, ev1, k_router, dim3((E + 3) / 4), dim3(256), 0, st, gate_w, x, E, dim,
+                    bias, topk, scale, logits_ws, count, scores, idx, w);
+        return hipGetLastError();
     }
-    hipLaunchKernelGGL(k_router_select, dim3(1), dim3(64), 0, st, lg, bias, E, topk, scale,
-                       scores, idx, w);
+    GHIP_LAUNCH(ev0, ev1, k_router_select, dim3(1), dim3(64), 0, st, logits_in, bias, E,
+                topk, scale, scores, idx, w);
     return hipGetLastError();
 }
 

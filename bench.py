@@ -11,7 +11,10 @@ slabs + x + out + logits = 201,393,280 B) / measured time, in GB/s.
 --workload dense_gemv runs config 1 (W [16384,4096] FP8, M in {1,2,4}) over
 rotating weight copies (>= 3x the 256 MB MALL). --workload dense_gemm runs
 the four DSA FP8 projections at M = 2048 prefill rows (the fp8blk_linear
-hook's MFMA GEMM path), in TFLOP/s.
+hook's MFMA GEMM path), in TFLOP/s. --workload bf16_gemv runs the LM head
+through the bf16_gemm hook; --workload moe_decode_router runs config 2 routed
+by the reference's sigmoid/bias router on the GPU; --workload store_load
+fills the HBM expert store from a converted v2 container.
 
 Prints ONE JSON line (rank 0). Extra objects: "roofline" (dominant kernel,
 HIP-event timed on its stream) and "cpu_baseline" (the reference CPU path,
@@ -32,6 +35,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.join(ROOT, "apus-glm5.3-flash_amd")
 HBM_PEAK_GBS = 8000.0            # MI355X HBM3E, AMD published
 BF16_PEAK_TFLOPS = 2500.0        # MI355X dense BF16 MFMA, AMD published
+HOST_LINK_PEAK_GBS = 64.0        # PCIe 5.0 x16, one direction (host -> MI355X)
 CPU_THREADS = 16                 # the GPU box's CPU share per GPU
 
 
@@ -429,6 +433,356 @@ def cpu_dense_gemm(lib, M=2048, budget_s=10.0):
 
 
 # --------------------------------------------------------------------------
+# BF16 GEMV hook at decode: the LM head (c/bf16.h:712-767)
+# --------------------------------------------------------------------------
+
+# vocab_size x hidden_size of the reference's model config
+LM_HEAD = (154880, 4096)
+
+
+def bench_bf16_gemv(lib, pkg, rt, steps, warmup, M=1, copies=2):
+    """One step = one apus_ghip_bf16_gemm_dev call of the LM head
+    ([154880, 4096] BF16, 1.27 GB, larger than the 256 MB MALL; two copies
+    alternate). Bytes = weights + x + y."""
+    N, K = LM_HEAD
+    W = rt.DevBuf(copies * N * K * 2)
+    pkg.check(lib.apus_synth_bf16_normal_dev(W.vp, copies * N * K, 0xB1, 1, 0, None),
+              "synth w")
+    x = rt.DevBuf(M * K * 2)
+    pkg.check(lib.apus_synth_bf16_normal_dev(x.vp, M * K, 0xB1, 2, 0, None), "synth x")
+    y = rt.DevBuf(M * N * 2)
+    st = rt.Stream()
+
+    def step(i):
+        rc = lib.apus_ghip_bf16_gemm_dev(ctypes.c_void_p(W.ptr + (i % copies) * N * K * 2),
+                                         x.vp, y.vp, M, N, K, st.vp)
+        if rc:
+            pkg.check(rc, "bf16_gemm_dev")
+
+    for i in range(warmup):
+        step(i)
+    st.synchronize()
+    e0, e1 = rt.Event(), rt.Event()
+    e0.record(st)
+    for i in range(steps):
+        step(warmup + i)
+    e1.record(st)
+    e1.synchronize()
+    ms = e0.elapsed_ms(e1) / steps
+    kname = "k_fp8_gemv_stream<%d, 2, true>" % min(M, 4)
+    kt = kernel_times(lib, rt, step, warmup + steps, steps, 2, {kname: (0, 1)})
+    nbytes = N * K * 2 + M * K * 2 + M * N * 2
+    return {"ms_per_step": ms, "value": nbytes / (ms * 1e-3) / 1e9,
+            "bytes": nbytes, "flops": 2 * M * N * K, "kernel": kname,
+            "kernel_ms": kt[kname], "kernel_bytes": nbytes,
+            "kernel_flops": 2 * M * N * K,
+            "launch_ms": {n: round(v, 5) for n, v in kt.items()},
+            "config": {"workload": "bf16_gemv (LM head through the bf16_gemm hook, "
+                                   "c/bf16.h:712-767)", "N": N, "K": K, "M": M,
+                       "weight_copies": copies, "weights": "bf16"}}
+
+
+def cpu_bf16_gemv(lib, M=1, budget_s=10.0):
+    """The reference's BF16 GEMV (apus_bf16_gemm_mt, c/bf16.h:444-649) on the
+    LM head, timed over a bounded number of calls."""
+    os.environ.setdefault("APUS_THREADS", str(CPU_THREADS))
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    P = O.ptr
+    N, K = LM_HEAD
+    w = np.empty((N, K), np.uint16)
+    lib.apus_synth_bf16_normal(P(w), w.size, 0xB1, 1, 0)
+    x = np.empty((M, K), np.uint16)
+    lib.apus_synth_bf16_normal(P(x), x.size, 0xB1, 2, 0)
+    y = np.empty((M, N), np.uint16)
+    use_ref = O.ref_available()
+    n, t = 0, 0.0
+    while t < budget_s and n < 200:
+        t0 = time.perf_counter()
+        if use_ref:
+            O.ref().ref_bf16_gemm_mt(P(w), P(x), P(y), M, N, K)
+        else:
+            O.lib().apo_bf16_gemm_mt(P(w), P(x), P(y), M, N, K, CPU_THREADS)
+        t += time.perf_counter() - t0
+        n += 1
+    nbytes = N * K * 2 + M * K * 2 + M * N * 2
+    return {"value": nbytes / (t / n) / 1e9, "unit": "GB/s",
+            "cores": int(os.environ.get("APUS_THREADS", CPU_THREADS)),
+            "kind": "reference" if use_ref else "port",
+            "sample": "%d calls of bf16_gemm_mt on the LM head [%d, %d], M=%d, "
+                      "%.1f ms/call" % (n, N, K, M, t / n * 1e3)}
+
+
+# --------------------------------------------------------------------------
+# config 2 with the reference router (sigmoid, selection-only bias)
+# --------------------------------------------------------------------------
+
+ROUTE_SCALE = 2.5      # routed_scaling_factor of the reference's model config
+
+
+def bench_moe_decode_router(lib, pkg, rt, steps, warmup, rotate=64):
+    """One step = apus_ghip_moe_router_dev (gate GEMV over gate_w [288, 4096]
+    BF16, sigmoid, stable top-8 of score + bias, pairwise normalization x 2.5,
+    c/gmoe.h:191-208) feeding apus_ghip_moe_decode_dev with the selected
+    ids/weights, both on one stream with no host round trip. Bytes = 8 expert
+    slabs + x + out + gate_w + bias."""
+    E, k, dim, inter, seed = (MOE[x] for x in ("E", "k", "dim", "inter", "seed"))
+    store = ctypes.c_void_p()
+    err = ctypes.create_string_buffer(256)
+    pkg.check(lib.apus_ghip_store_open(ctypes.byref(store), E, dim, inter,
+                                       MOE["limit"], err, 256), "store_open")
+    pkg.check(lib.apus_ghip_store_synth(store, seed, 0, 1e-4, 1e-2), "store_synth")
+    gw = rt.DevBuf(E * dim * 2)
+    pkg.check(lib.apus_synth_bf16_normal_dev(gw.vp, E * dim, seed, 40, 0, None), "gate_w")
+    bias = np.empty(E, np.float32)
+    lib.apus_synth_f32_normal(bias.ctypes.data_as(ctypes.c_void_p), E, seed, 41, 0)
+    d_bias = rt.DevBuf.of((bias * np.float32(0.05)).astype(np.float32))
+    xs = np.empty((rotate, dim), np.uint16)
+    lib.apus_synth_bf16_normal(xs.ctypes.data_as(ctypes.c_void_p), xs.size, seed, 31, 0)
+    d_x = rt.DevBuf.of(xs)
+    d_out = rt.DevBuf(rotate * dim * 2)
+    d_idx = rt.DevBuf(64 * 4)
+    d_w = rt.DevBuf(64 * 4)
+    st = rt.Stream()
+
+    def router(i):
+        j = i % rotate
+        rc = lib.apus_ghip_moe_router_dev(ctypes.c_void_p(d_x.ptr + j * dim * 2), gw.vp,
+                                          None, d_bias.vp, E, dim, k,
+                                          ctypes.c_float(ROUTE_SCALE), None, d_idx.vp,
+                                          d_w.vp, st.vp)
+        if rc:
+            pkg.check(rc, "moe_router_dev")
+
+    def decode(i):
+        j = i % rotate
+        rc = lib.apus_ghip_moe_decode_dev(store, ctypes.c_void_p(d_x.ptr + j * dim * 2),
+                                          None, d_idx.vp, d_w.vp, k,
+                                          ctypes.c_void_p(d_out.ptr + j * dim * 2), st.vp)
+        if rc:
+            pkg.check(rc, "moe_decode_dev")
+
+    for i in range(warmup):
+        router(i)
+        decode(i)
+    st.synchronize()
+    e0, e1 = rt.Event(), rt.Event()
+    e0.record(st)
+    for i in range(steps):
+        router(warmup + i)
+        decode(warmup + i)
+    e1.record(st)
+    e1.synchronize()
+    ms = e0.elapsed_ms(e1) / steps
+    # per-launch times: the router pair and the fused decode launch, each
+    # with its own dispatch-packet events
+    n = steps
+    evs = [[rt.Event() for _ in range(6)] for _ in range(n)]
+    arr2, arr4 = ctypes.c_void_p * 2, ctypes.c_void_p * 4
+    for i in range(n):
+        lib.apus_ghip_set_trace_events(arr2(*[e.handle for e in evs[i][:2]]), 2)
+        router(warmup + steps + i)
+        # the decode entry point takes four (the fused launch uses the first two)
+        lib.apus_ghip_set_trace_events(arr4(*[e.handle for e in evs[i][2:]]), 4)
+        decode(warmup + steps + i)
+    lib.apus_ghip_set_trace_events(None, 0)
+    rt.synchronize()
+    t_router = sum(e[0].elapsed_ms(e[1]) for e in evs) / n
+    t_fused = sum(e[2].elapsed_ms(e[3]) for e in evs) / n
+    lib.apus_ghip_store_close(store)
+    slabs = moe_algorithmic_bytes(E, k, dim, inter)[0] - E * 4     # no logits
+    nbytes = slabs + E * dim * 2 + E * 4
+    return {
+        "ms_per_step": ms, "value": nbytes / (ms * 1e-3) / 1e9,
+        "bytes": nbytes, "flops": 2 * k * 3 * inter * dim + 2 * E * dim,
+        "kernel": "k_moe_fused", "kernel_ms": t_fused, "kernel_bytes": slabs,
+        "kernel_flops": 2 * k * 3 * inter * dim,
+        "launch_ms": {"router (k_router_logits + k_router_select)": round(t_router, 5),
+                      "k_moe_fused": round(t_fused, 5)},
+        "config": {"workload": "moe_decode_router (BASELINE config 2 shapes, routed by "
+                               "the reference router c/gmoe.h:191-208)",
+                   "experts": E, "topk": k, "dim": dim, "inter": inter,
+                   "route_scale": ROUTE_SCALE, "rotated_tokens": rotate,
+                   "weights": "fp8-e4m3 128x128 blocks; gate_w bf16"},
+    }
+
+
+def cpu_moe_decode_router(lib, budget_s=3.0):
+    """The reference router (apus_gmoe_router, c/gmoe.h:191-208) on this host,
+    added to the config-2 expert sample of cpu_moe_decode."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    P = O.ptr
+    E, k, dim, inter, seed = (MOE[x] for x in ("E", "k", "dim", "inter", "seed"))
+    gw = np.empty((E, dim), np.uint16)
+    lib.apus_synth_bf16_normal(P(gw), gw.size, seed, 40, 0)
+    bias = np.empty(E, np.float32)
+    lib.apus_synth_f32_normal(P(bias), E, seed, 41, 0)
+    bias = (bias * np.float32(0.05)).astype(np.float32)
+    x = np.empty(dim, np.uint16)
+    lib.apus_synth_bf16_normal(P(x), dim, seed, 31, 0)
+    sc, idx, w = (np.empty(E, np.float32), np.empty(k, np.int32), np.empty(k, np.float32))
+    use_ref = O.ref_available()
+    n, t = 0, 0.0
+    while t < budget_s and n < 5000:
+        t0 = time.perf_counter()
+        if use_ref:
+            O.ref().ref_gmoe_router(P(gw), P(bias), E, dim, k, ROUTE_SCALE, P(x), P(sc),
+                                    P(idx), P(w))
+        else:
+            O.gmoe_router(gw, bias, x, k, ROUTE_SCALE)
+        t += time.perf_counter() - t0
+        n += 1
+    experts = cpu_moe_decode(lib)
+    per_tok = experts["ms_per_token"] * 1e-3 + t / n
+    nbytes = moe_algorithmic_bytes(E, k, dim, inter)[0] - E * 4 + E * dim * 2 + E * 4
+    experts.update({
+        "value": nbytes / per_tok / 1e9,
+        "sample": experts["sample"] + "; router %d calls, %.3f ms/call, added"
+                  % (n, t / n * 1e3),
+        "router_ms": t / n * 1e3})
+    return experts
+
+
+# --------------------------------------------------------------------------
+# HBM expert store filled from a converted v2 container
+# --------------------------------------------------------------------------
+
+def write_bench_container(root, layer, n_experts, slab):
+    """A converted-v2 container (apus.index.json expert_slabs records
+    {block, expert, shard, offset, nbytes}, tests/m1/README.md:21-55) with
+    one shard holding n_experts copies of `slab`, each at its own offset."""
+    os.makedirs(root, exist_ok=True)
+    hdr = json.dumps({"__metadata__": {"format": "pt"}}).encode()
+    hdr += b" " * ((8 - len(hdr) % 8) % 8)
+    recs = []
+    name = "apus-00001.safetensors"
+    with open(os.path.join(root, name), "wb") as f:
+        f.write(len(hdr).to_bytes(8, "little"))
+        f.write(hdr)
+        off = 8 + len(hdr)
+        for e in range(n_experts):
+            f.write(slab)
+            recs.append({"block": "layers.%d" % layer, "expert": e, "shard": name,
+                         "offset": off, "nbytes": len(slab)})
+            off += len(slab)
+    with open(os.path.join(root, "apus.index.json"), "w") as f:
+        json.dump({"format_version": 2, "model_type": "glm5_next",
+                   "expert_slabs": recs}, f)
+    return os.path.getsize(os.path.join(root, name))
+
+
+def bench_store_load(lib, pkg, rt, steps, warmup, n_experts=64):
+    """One step = apus_ghip_store_load_container of one layer's n_experts
+    slabs (25,171,968 B each at 4096/2048) from a container written just
+    before, so the shard is in the host page cache: the rate is pread into
+    pinned staging overlapped with the H2D copies, not disk. One slab is
+    read back and compared with the file."""
+    import tempfile
+    E, dim, inter = MOE["E"], MOE["dim"], MOE["inter"]
+    store = ctypes.c_void_p()
+    err = ctypes.create_string_buffer(512)
+    pkg.check(lib.apus_ghip_store_open(ctypes.byref(store), E, dim, inter,
+                                       MOE["limit"], err, 512), "store_open")
+    sb = lib.apus_ghip_store_slab_bytes(store)
+    rng = np.random.default_rng(0x5B)
+    slab = rng.integers(0, 256, size=sb, dtype=np.uint8).tobytes()
+    layer = 3
+    with tempfile.TemporaryDirectory(prefix="apus_bench_") as d:
+        fsz = write_bench_container(d, layer, n_experts, slab)
+        nl = ctypes.c_int(0)
+        times = []
+        for i in range(warmup + steps):
+            t0 = time.perf_counter()
+            rc = lib.apus_ghip_store_load_container(store, d.encode(), layer,
+                                                    ctypes.byref(nl), err, 512)
+            if rc:
+                raise RuntimeError("store_load_container: " + err.value.decode())
+            if i >= warmup:
+                times.append(time.perf_counter() - t0)
+        if nl.value != n_experts:
+            raise RuntimeError("loaded %d slabs, expected %d" % (nl.value, n_experts))
+        back = np.empty(sb, np.uint8)
+        pkg.check(lib.apus_ghip_store_get(store, n_experts - 1,
+                                          back.ctypes.data_as(ctypes.c_void_p), sb),
+                  "store_get")
+        if back.tobytes() != slab:
+            raise RuntimeError("slab read back differs from the container bytes")
+    lib.apus_ghip_store_close(store)
+    ms = sum(times) / len(times) * 1e3
+    nbytes = n_experts * sb
+    return {"ms_per_step": ms, "value": nbytes / (ms * 1e-3) / 1e9,
+            "bytes": nbytes, "flops": 0, "kernel": "store_load_container",
+            "kernel_ms": ms, "kernel_bytes": nbytes, "kernel_flops": 0,
+            "launch_ms": {"store_load_container": round(ms, 4)},
+            "host_link": True,
+            "config": {"workload": "store_load (one layer of a converted v2 container "
+                                   "-> HBM store, page-cache resident)",
+                       "slabs": n_experts, "slab_bytes": sb, "shard_bytes": fsz}}
+
+
+def cpu_store_load(lib, n_experts=8, budget_s=8.0):
+    """The reference's fill of one expert (c/gcache.h:394-451 pread, then the
+    dequant-on-fill c/gcache.h:413-426: three fp8blk dequants to BF16) on this
+    host, from page-cache-resident slabs, in slab GB/s."""
+    import tempfile
+    os.environ.setdefault("APUS_THREADS", str(CPU_THREADS))
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    P = O.ptr
+    dim, inter = MOE["dim"], MOE["inter"]
+    nb = O.nblocks
+    members = [(inter, dim), (inter, dim), (dim, inter)]
+    sizes = []
+    for (o, kk) in members:
+        sizes += [o * kk, nb(o) * nb(kk) * 4]
+    sb = sum(sizes)
+    rng = np.random.default_rng(0x5C)
+    slab = rng.integers(0, 256, size=sb, dtype=np.uint8)
+    # scales: positive finite floats
+    off = 0
+    for m, sz in enumerate(sizes):
+        if m % 2:
+            slab[off:off + sz] = np.full(sz // 4, 1e-3, np.float32).view(np.uint8)
+        off += sz
+    use_ref = O.ref_available()
+    with tempfile.TemporaryDirectory(prefix="apus_cpu_") as d:
+        path = os.path.join(d, "slabs.bin")
+        with open(path, "wb") as f:
+            for _ in range(n_experts):
+                f.write(slab.tobytes())
+        fd = os.open(path, os.O_RDONLY)
+        buf = np.empty(sb, np.uint8)
+        outs = [np.empty(o * kk, np.uint16) for (o, kk) in members]
+        n, t = 0, 0.0
+        try:
+            while t < budget_s and n < 400:
+                t0 = time.perf_counter()
+                got = os.preadv(fd, [memoryview(buf)], (n % n_experts) * sb)
+                if got != sb:
+                    raise RuntimeError("short read")
+                off = 0
+                for j, (o, kk) in enumerate(members):
+                    c = buf[off:off + o * kk]
+                    s = buf[off + o * kk:off + o * kk + nb(o) * nb(kk) * 4]
+                    if use_ref:
+                        O.ref().ref_fp8blk_dequant_mt(P(c), P(s), P(outs[j]), o, kk)
+                    else:
+                        O.lib().apo_fp8blk_dequant_mt(P(c), P(s), P(outs[j]), o, kk,
+                                                      CPU_THREADS)
+                    off += o * kk + nb(o) * nb(kk) * 4
+                t += time.perf_counter() - t0
+                n += 1
+        finally:
+            os.close(fd)
+    return {"value": sb / (t / n) / 1e9, "unit": "GB/s",
+            "cores": int(os.environ.get("APUS_THREADS", CPU_THREADS)),
+            "kind": "reference" if use_ref else "port",
+            "sample": "%d slab fills (pread + dequant-on-fill of the 3 members to BF16), "
+                      "%.2f ms/slab" % (n, t / n * 1e3)}
+
+
+# --------------------------------------------------------------------------
 # configs 3 / 4: routed-MoE prefill (grouped GEMM, MFMA path)
 # --------------------------------------------------------------------------
 
@@ -591,8 +945,11 @@ def roofline_of(r):
     else:
         achieved = r["kernel_bytes"] / (r["kernel_ms"] * 1e-3) / 1e9
     peak = BF16_PEAK_TFLOPS if mfma else HBM_PEAK_GBS
+    bound = "mfma" if mfma else "hbm"
+    if r.get("host_link"):
+        peak, bound = HOST_LINK_PEAK_GBS, "pcie"
     return {
-        "bound": "mfma" if mfma else "hbm",
+        "bound": bound,
         "kernel": r["kernel"],
         "achieved": round(achieved, 2),
         "peak": peak,
@@ -621,6 +978,18 @@ def run_workload(name, lib, pkg, rt, args, cpu_leg):
         r = bench_dense_gemm(lib, pkg, rt, args.steps, args.warmup)
         return ("FP8 dense linear GEMM TFLOP/s (DSA projections, prefill M)", r,
                 cpu_dense_gemm(lib) if cpu_leg else None)
+    if name == "bf16_gemv":
+        r = bench_bf16_gemv(lib, pkg, rt, args.steps, args.warmup, M=args.m)
+        return ("BF16 decode GEMV HBM GB/s (LM head)", r,
+                cpu_bf16_gemv(lib, M=args.m) if cpu_leg else None)
+    if name == "moe_decode_router":
+        r = bench_moe_decode_router(lib, pkg, rt, args.steps, args.warmup)
+        return ("FP8 MoE decode GEMV HBM GB/s (reference router on the GPU)", r,
+                cpu_moe_decode_router(lib) if cpu_leg else None)
+    if name == "store_load":
+        r = bench_store_load(lib, pkg, rt, min(args.steps, 5), min(args.warmup, 1))
+        return ("expert store fill GB/s (container -> HBM)", r,
+                cpu_store_load(lib) if cpu_leg else None)
     if name in PREFILL:
         steps = args.prefill_steps if args.prefill_steps else args.steps
         r = bench_prefill(lib, pkg, rt, steps, min(args.warmup, 2), name)
@@ -662,9 +1031,11 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="moe_decode",
-                    choices=["moe_decode", "dense_gemv", "dense_gemm", "prefill_zipf",
+                    choices=["moe_decode", "dense_gemv", "dense_gemm", "bf16_gemv",
+                             "moe_decode_router", "store_load", "prefill_zipf",
                              "prefill_stack", "copy"])
-    ap.add_argument("--m", type=int, default=1, help="dense_gemv rows (1, 2, 4)")
+    ap.add_argument("--m", type=int, default=1,
+                    help="dense_gemv / bf16_gemv rows (1, 2, 4)")
     ap.add_argument("--prefill-steps", type=int, default=0,
                     help="steps of the prefill workloads (default: --steps; "
                          "5 when they run as the metric's second half)")

@@ -205,7 +205,9 @@ int apus_ghip_store_expert_bf16(ApusGhipStore *s, int expert,
  * pairwise sum + 1e-20) * route_scale. Outputs idx / w [topk] in selection
  * order (as the reference) and, when scores is non-NULL, scores [E]; the
  * result feeds apus_ghip_moe_decode_dev / _prefill_dev as idx / w.
- * E <= 512, topk <= 16, dim % 8 == 0. Asynchronous on `stream`. 0 = ok. */
+ * E <= 512, topk <= 16, dim % 8 == 0. One kernel launch, asynchronous on
+ * `stream`; the gate-logit form uses a process-wide device workspace, so
+ * calls that overlap on the device race (order them on one stream). 0 = ok. */
 int apus_ghip_moe_router_dev(const uint16_t *x, const uint16_t *gate_w,
                              const float *logits, const float *gate_bias, int E,
                              size_t dim, int topk, float route_scale, float *scores,
@@ -260,8 +262,9 @@ int apus_ghip_moe_prefill_dev(ApusGhipStore *s, const uint16_t *x, size_t T,
  * with events[0..1] and the down launch with events[2..3] (when it runs as
  * one fused launch, top-k <= 8, events[0..1] time that launch and
  * events[2..3] are not recorded);
- * apus_ghip_fp8blk_linear_dev (n >= 2) starts events[0] with its first
- * GEMV launch and stops events[1] with its last; apus_ghip_moe_prefill_dev
+ * apus_ghip_fp8blk_linear_dev, apus_ghip_bf16_gemm_dev and
+ * apus_ghip_moe_router_dev (n >= 2) start events[0] with their first launch
+ * and stop events[1] with their last; apus_ghip_moe_prefill_dev
  * (n >= 8) times the permutation with events[0..1], the gate/up GEMM with
  * events[2..3], the down GEMM with events[4..5] and the combine with
  * events[6..7]. Process-wide, not
