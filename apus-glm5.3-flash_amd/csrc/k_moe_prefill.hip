@@ -219,8 +219,9 @@ struct PfTile {
     const uint8_t *w0, *w1;       /* weight matrices of the two slots */
     const float *sr0, *sr1;       /* scale rows of the two slots */
     uint16_t *out;
-    uint32_t K, N, row0, rows, cb0, cb1, topk;  /* cbX: slot X column base */
-    float limit;
+    float *outf;                  /* MODE 2: fp32 partial outputs */
+    uint32_t K, KS, N, row0, rows, cb0, cb1, topk;  /* cbX: slot X column base */
+    float limit;                  /* K: row stride; KS: k span of this tile */
 };
 
 /* The tile body for tiles of at most NRB 32-row blocks (rows past NRB*32
@@ -263,7 +264,7 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
     const uint32_t lane = tid & 63;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t n = lane & 31, h = lane >> 5;
-    const uint32_t K = t.K, nst = K / PF_BK;
+    const uint32_t K = t.K, nst = t.KS / PF_BK;
 
     /* --- DMA sources: a wave-uniform base (SGPRs; stage j adds j*64
      * elements) plus a 32-bit per-lane offset, so each load is one
@@ -466,6 +467,10 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
                     const float g = ghip_bf16_round(a0[rb][i]);
                     const float u = ghip_bf16_round(a1[rb][i]);
                     o[c0] = (uint16_t)pf_swiglu(g, u, t.limit);
+                } else if (MODE == 2) {
+                    float *of = t.outf + (size_t)(t.row0 + r) * t.N;
+                    of[c0] = a0[rb][i];
+                    of[c1] = a1[rb][i];
                 } else {
                     o[c0] = (uint16_t)ghip_bf16_bits(a0[rb][i]);
                     o[c1] = (uint16_t)ghip_bf16_bits(a1[rb][i]);
@@ -511,6 +516,8 @@ __global__ __launch_bounds__(256, 1) void k_pf_gemm(
         t.topk = topk;
         t.limit = limit;
         t.K = K;
+        t.KS = K;
+        t.outf = nullptr;
         t.N = MODE == 0 ? bank.inter : bank.dim;
         const uint8_t *slab = bank.base + (size_t)e * bank.stride;
         if (MODE == 0) {
@@ -557,61 +564,98 @@ __global__ __launch_bounds__(256, 1) void k_pf_gemm(
 
 /* Y [M, N] = bf16(X [M, K] . dequant(W [N, K])^T), the composition of
  * c/gdsa.h:525-534 (dequant_mt then gemm_mt) without the BF16 weight copy:
- * the MODE-1 tile body above on tiles of 256 rows of X x 256 rows of W (two
- * 128-row scale blocks). Items (row tile, column block) are dealt so that
- * XCD x (workgroup b runs on XCD b % 8) owns column blocks x, x + 8, ...
- * when there are at least 8, sharing each block's weights across its row
- * tiles in one L2; otherwise it owns row tiles x, x + 8, ... exact_dev:
- * NULL or a device flag, nonzero when W holds a NaN code (0x7F/0xFF) and
- * the exact integer decode must be used. */
+ * the tile body above on tiles of bm rows of X (256, 128, 64 or 32, chosen
+ * by the launcher) x 256 rows of W (two 128-row scale blocks).
+ *
+ * With S > 1 the K range is split too (split-K for launches with fewer
+ * tiles than CUs): split s covers k blocks [s*nkb/S, (s+1)*nkb/S) and
+ * writes its fp32 partial sums to part[s] [M, N] (MODE 2); k_splitk_sum
+ * then adds the S partials in ascending s and rounds once. With S == 1 the
+ * tile writes bf16 Y directly (MODE 1).
+ *
+ * Items (row tile x split, column block) are dealt so that XCD x
+ * (workgroup b runs on XCD b % 8) owns column blocks x, x + 8, ... when
+ * there are at least 8, sharing each block's weights across its row tiles
+ * in one L2; otherwise it owns (row tile, split) units x, x + 8, ...
+ * exact_dev: NULL or a device flag, nonzero when W holds a NaN code
+ * (0x7F/0xFF) and the exact integer decode must be used. */
 __global__ __launch_bounds__(256, 1) void k_fp8_gemm(
     const uint8_t *__restrict__ codes, const float *__restrict__ scales,
-    const uint16_t *__restrict__ x, uint16_t *__restrict__ y, uint32_t M, uint32_t N,
-    uint32_t K, const uint32_t *__restrict__ exact_dev) {
+    const uint16_t *__restrict__ x, uint16_t *__restrict__ y, float *__restrict__ part,
+    uint32_t M, uint32_t N, uint32_t K, uint32_t bm, uint32_t S,
+    const uint32_t *__restrict__ exact_dev) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t pf_lds[];
-    const uint32_t nkb = K >> 7, nblk = N >> 8, tiles = (M + PF_BM - 1) / PF_BM;
+    const uint32_t nkb = K >> 7, nblk = N >> 8, tiles = (M + bm - 1) / bm;
+    const uint32_t rows_u = tiles * S;             /* (row tile, split) units */
     const bool exact = exact_dev && *exact_dev;
-    /* XCD xcd owns column blocks xcd, xcd + 8, ... (at least 8 of them) or
-     * else row tiles xcd, xcd + 8, ...; its workgroups split the owned
-     * units' items */
     const uint32_t xcd = blockIdx.x & 7u, c = blockIdx.x >> 3, per = gridDim.x >> 3;
     const bool colp = nblk >= 8;
-    const uint32_t nu = colp ? nblk : tiles, other = colp ? tiles : nblk;
+    const uint32_t nu = colp ? nblk : rows_u, other = colp ? rows_u : nblk;
     const uint32_t nown = nu > xcd ? (nu - xcd + 7) / 8 : 0;
     for (uint32_t q = c; q < nown * other; q += per) {
         const uint32_t own = xcd + 8 * (q / other), o = q % other;
-        const uint32_t nb = colp ? own : o, tile = colp ? o : own;
+        const uint32_t nb = colp ? own : o, ru = colp ? o : own;
+        const uint32_t tile = ru / S, sp = ru - tile * S;
+        const uint32_t kb0 = sp * nkb / S, kb1 = (sp + 1) * nkb / S;
         PfTile t;
-        t.act = x;
+        t.act = x + (size_t)kb0 * 128;
         t.perm = nullptr;
         t.out = y;
-        t.row0 = tile * PF_BM;
-        t.rows = M - t.row0 < PF_BM ? M - t.row0 : PF_BM;
+        t.outf = part + (size_t)sp * M * N;
+        t.row0 = tile * bm;
+        t.rows = M - t.row0 < bm ? M - t.row0 : bm;
         t.topk = 1;
         t.limit = 0.0f;
         t.K = K;
+        t.KS = (kb1 - kb0) * 128;
         t.N = N;
         t.cb0 = nb * 256;
         t.cb1 = nb * 256 + 128;
-        t.w0 = t.w1 = codes;
-        t.sr0 = scales + (size_t)(2 * nb) * nkb;
-        t.sr1 = scales + (size_t)(2 * nb + 1) * nkb;
+        t.w0 = t.w1 = codes + (size_t)kb0 * 128;
+        t.sr0 = scales + (size_t)(2 * nb) * nkb + kb0;
+        t.sr1 = scales + (size_t)(2 * nb + 1) * nkb + kb0;
         ghip_f32x2 *sct = (ghip_f32x2 *)(pf_lds + PF_RING);
-        for (uint32_t b = threadIdx.x; b < nkb; b += 256) {
+        for (uint32_t b = threadIdx.x; b < kb1 - kb0; b += 256) {
             ghip_f32x2 v;
             v[0] = t.sr0[b];
             v[1] = t.sr1[b];
             sct[b] = v;
         }
         const uint32_t nrb = (t.rows + 31) >> 5;
-        if (exact) pf_tile<1, PF_RB, true>(t, pf_lds, sct);
-        else if (nrb > 4) pf_tile<1, 8, false>(t, pf_lds, sct);
-        else if (nrb > 2) pf_tile<1, 4, false>(t, pf_lds, sct);
-        else if (nrb > 1) pf_tile<1, 2, false>(t, pf_lds, sct);
-        else              pf_tile<1, 1, false>(t, pf_lds, sct);
+        if (S > 1) {
+            if (exact) pf_tile<2, PF_RB, true>(t, pf_lds, sct);
+            else if (nrb > 4) pf_tile<2, 8, false>(t, pf_lds, sct);
+            else if (nrb > 2) pf_tile<2, 4, false>(t, pf_lds, sct);
+            else if (nrb > 1) pf_tile<2, 2, false>(t, pf_lds, sct);
+            else              pf_tile<2, 1, false>(t, pf_lds, sct);
+        } else {
+            if (exact) pf_tile<1, PF_RB, true>(t, pf_lds, sct);
+            else if (nrb > 4) pf_tile<1, 8, false>(t, pf_lds, sct);
+            else if (nrb > 2) pf_tile<1, 4, false>(t, pf_lds, sct);
+            else if (nrb > 1) pf_tile<1, 2, false>(t, pf_lds, sct);
+            else              pf_tile<1, 1, false>(t, pf_lds, sct);
+        }
         __builtin_amdgcn_s_barrier();
     }
     GHIP_VMCNT(0);
+}
+
+/* y = bf16(part[0] + part[1] + ... + part[S-1]) elementwise, ascending s
+ * (a fixed order: deterministic); 4 outputs per thread. */
+__global__ __launch_bounds__(256) void k_splitk_sum(const float *__restrict__ part,
+                                                    uint32_t S, size_t n,
+                                                    uint16_t *__restrict__ y) {
+    const size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i >= n) return;
+    ghip_f32x4 a = *(const ghip_f32x4 *)(part + i);
+    for (uint32_t sp = 1; sp < S; sp++) {
+        const ghip_f32x4 b = *(const ghip_f32x4 *)(part + (size_t)sp * n + i);
+#pragma unroll
+        for (int j = 0; j < 4; j++) a[j] = a[j] + b[j];
+    }
+    /* 16-bit stores: y needs only its element alignment */
+#pragma unroll
+    for (int j = 0; j < 4; j++) y[i + j] = (uint16_t)ghip_bf16_bits(a[j]);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -741,6 +785,12 @@ extern "C" int ghip_fp8_gemm_fits(size_t M, size_t N, size_t K, const void *code
         && ((uintptr_t)codes & 15) == 0 && ((uintptr_t)x & 15) == 0;
 }
 
+/* split-K partials: one device buffer, grown on demand, kept for the
+ * process (launches on one device are stream-ordered users of it) */
+static float *g_part;
+static size_t g_part_cap;
+#define GHIP_SPLITK_MAX_BYTES ((size_t)256 << 20)
+
 extern "C" hipError_t ghip_launch_fp8_gemm(const uint8_t *codes, const float *scales,
                                            const uint16_t *x, uint16_t *y, size_t M,
                                            size_t N, size_t K, const uint32_t *exact_dev,
@@ -748,11 +798,64 @@ extern "C" hipError_t ghip_launch_fp8_gemm(const uint8_t *codes, const float *sc
                                            hipStream_t st) {
     if (!ghip_fp8_gemm_fits(M, N, K, codes, x) || n_cu == 0 || n_cu % 8)
         return hipErrorInvalidValue;
-    const size_t items = ((M + PF_BM - 1) / PF_BM) * (N / 256);
+    const size_t nblk = N / 256, nkb = K / 128;
+    /* Tile height bm and K splits S: among bm in {256, 128, 64, 32} (no
+     * taller than M needs) with the fewest splits that give 3/4 of the CUs
+     * an item, the choice that moves the fewest bytes -- activation rows
+     * (read once per column block), weights (once per row tile) and the
+     * fp32 partials (written and read once per split). Splits keep >= 2 k
+     * blocks each. When no choice reaches 3/4 of the CUs, the one with the
+     * most items. */
+    const size_t want = (size_t)n_cu * 3 / 4;
+    uint32_t bm = 32, S = 1;
+    size_t items = 0;
+    {
+        double best = -1.0;
+        size_t best_items = 0;
+        bool best_ok = false;
+        for (uint32_t b = PF_BM; b >= 32; b >>= 1) {
+            if (b > 32 && b / 2 >= M) continue;
+            const size_t tiles = (M + b - 1) / b, base = tiles * nblk;
+            size_t sp = 1;
+            while (base * sp < want && sp + 1 <= nkb / 2
+                   && (sp + 1) * M * N * sizeof(float) <= GHIP_SPLITK_MAX_BYTES)
+                sp++;
+            const size_t it = base * sp;
+            const bool ok = it >= want;
+            const double bytes = (double)nblk * tiles * b * K * 2 + (double)tiles * N * K
+                               + (sp > 1 ? (double)sp * M * N * 8 : 0.0);
+            const bool better = best < 0.0 || (ok && !best_ok)
+                              || (ok == best_ok && (ok ? bytes < best : it > best_items));
+            if (better) {
+                best = bytes;
+                best_items = it;
+                best_ok = ok;
+                bm = b;
+                S = (uint32_t)sp;
+            }
+        }
+        items = best_items;
+    }
+    if (S > 1) {
+        const size_t need = (size_t)S * M * N * sizeof(float);
+        if (need > g_part_cap) {
+            if (g_part) (void)hipFree(g_part);
+            g_part = nullptr;
+            g_part_cap = 0;
+            hipError_t e = hipMalloc((void **)&g_part, need);
+            if (e != hipSuccess) return e;
+            g_part_cap = need;
+        }
+    }
     uint32_t g = items < n_cu ? (uint32_t)((items + 7) & ~(size_t)7) : n_cu;
     hipEvent_t e0 = ev ? ev[0] : nullptr, e1 = ev ? ev[1] : nullptr;
-    GHIP_LAUNCH(e0, e1, k_fp8_gemm, dim3(g), dim3(256), PF_LDS, st, codes, scales, x, y,
-                (uint32_t)M, (uint32_t)N, (uint32_t)K, exact_dev);
+    GHIP_LAUNCH(e0, S > 1 ? nullptr : e1, k_fp8_gemm, dim3(g), dim3(256), PF_LDS, st, codes,
+                scales, x, y, g_part, (uint32_t)M, (uint32_t)N, (uint32_t)K, bm, S, exact_dev);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || S == 1) return e;
+    const size_t n = M * N;                          /* N % 256 == 0: n % 4 == 0 */
+    GHIP_LAUNCH(nullptr, e1, k_splitk_sum, dim3((uint32_t)((n / 4 + 255) / 256)), dim3(256),
+                0, st, g_part, S, n, y);
     return hipGetLastError();
 }
 

@@ -98,9 +98,13 @@ def test_fp8_battery(ghip, M, N, K):
 
 # prefill-sized M: the MFMA GEMM path (M >= 16, N % 256 == 0, K % 128 == 0),
 # incl. ragged row tiles, K = 128 and K = 16384 (o_proj), the DSA shapes of
-# c/gdsa.h:599-611,660-661 at M = s; M = 15 stays on the GEMV passes
+# c/gdsa.h:599-611,660-661 at M = s; M = 15 stays on the GEMV passes. Most
+# small-M shapes run split-K (fp32 partials summed in a fixed order):
+# (16, 256, 16384) with 64 splits of 2 k blocks, (64, 4096, 16384) with 12,
+# (2048, 512, 4096) with 6 on 128-row tiles; (513, 256, 128) cannot split
 GEMM = [(16, 512, 4096), (100, 1536, 4096), (300, 2048, 1536), (40, 16384, 1536),
-        (256, 4096, 16384), (513, 256, 128), (15, 512, 1024), (17, 300, 512)]
+        (256, 4096, 16384), (513, 256, 128), (15, 512, 1024), (17, 300, 512),
+        (16, 256, 16384), (64, 4096, 16384), (2048, 512, 4096)]
 
 
 @pytest.mark.parametrize("M,N,K", GEMM)
