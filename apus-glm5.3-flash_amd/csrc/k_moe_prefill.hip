@@ -573,28 +573,29 @@ __global__ __launch_bounds__(256, 1) void k_pf_gemm(
  * then adds the S partials in ascending s and rounds once. With S == 1 the
  * tile writes bf16 Y directly (MODE 1).
  *
- * Items (row tile x split, column block) are dealt so that XCD x
- * (workgroup b runs on XCD b % 8) owns column blocks x, x + 8, ... when
- * there are at least 8, sharing each block's weights across its row tiles
- * in one L2; otherwise it owns (row tile, split) units x, x + 8, ...
- * exact_dev: NULL or a device flag, nonzero when W holds a NaN code
- * (0x7F/0xFF) and the exact integer decode must be used. */
+ * Items ((row tile, split) unit, column block) are dealt to the 8 XCDs
+ * (workgroup b runs on XCD b % 8) as an R x (8/R) grid: XCD x owns the
+ * units u == x / (8/R) (mod R) and the column blocks nb == x % (8/R)
+ * (mod 8/R), so each XCD's L2 holds 1/R of X's rows and (R/8) of the
+ * weights; the launcher picks R to minimize the bytes fetched into the
+ * L2s, (8/R) |X| + R |W|. exact_dev: NULL or a device flag, nonzero when W
+ * holds a NaN code (0x7F/0xFF) and the exact integer decode must be
+ * used. */
 __global__ __launch_bounds__(256, 1) void k_fp8_gemm(
     const uint8_t *__restrict__ codes, const float *__restrict__ scales,
     const uint16_t *__restrict__ x, uint16_t *__restrict__ y, float *__restrict__ part,
-    uint32_t M, uint32_t N, uint32_t K, uint32_t bm, uint32_t S,
+    uint32_t M, uint32_t N, uint32_t K, uint32_t bm, uint32_t S, uint32_t R,
     const uint32_t *__restrict__ exact_dev) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t pf_lds[];
     const uint32_t nkb = K >> 7, nblk = N >> 8, tiles = (M + bm - 1) / bm;
     const uint32_t rows_u = tiles * S;             /* (row tile, split) units */
     const bool exact = exact_dev && *exact_dev;
     const uint32_t xcd = blockIdx.x & 7u, c = blockIdx.x >> 3, per = gridDim.x >> 3;
-    const bool colp = nblk >= 8;
-    const uint32_t nu = colp ? nblk : rows_u, other = colp ? rows_u : nblk;
-    const uint32_t nown = nu > xcd ? (nu - xcd + 7) / 8 : 0;
-    for (uint32_t q = c; q < nown * other; q += per) {
-        const uint32_t own = xcd + 8 * (q / other), o = q % other;
-        const uint32_t nb = colp ? own : o, ru = colp ? o : own;
+    const uint32_t C = 8u / R, xr = xcd / C, xc = xcd - xr * C;
+    const uint32_t nru = rows_u > xr ? (rows_u - xr + R - 1) / R : 0;
+    const uint32_t nnb = nblk > xc ? (nblk - xc + C - 1) / C : 0;
+    for (uint32_t q = c; q < nru * nnb; q += per) {
+        const uint32_t ru = xr + R * (q / nnb), nb = xc + C * (q % nnb);
         const uint32_t tile = ru / S, sp = ru - tile * S;
         const uint32_t kb0 = sp * nkb / S, kb1 = (sp + 1) * nkb / S;
         PfTile t;
@@ -847,10 +848,30 @@ extern "C" hipError_t ghip_launch_fp8_gemm(const uint8_t *codes, const float *sc
             g_part_cap = need;
         }
     }
+    /* XCD grid R x (8/R): fewest bytes into the 8 L2s, (8/R) |X| + R |W|,
+     * among the grids that give every XCD the same number of units and of
+     * column blocks (an uneven split would leave XCDs idle at the end) */
+    uint32_t R = 0;
+    {
+        const size_t rows_u = ((M + bm - 1) / bm) * S;
+        const double xb = (double)((M + bm - 1) / bm) * bm * K * 2, wb = (double)N * K;
+        double best = -1.0;
+        for (uint32_t r = 1; r <= 8; r <<= 1) {
+            if (rows_u % r || nblk % (8 / r)) continue;
+            const double b = (8.0 / r) * xb + r * wb;
+            if (best < 0.0 || b < best) {
+                best = b;
+                R = r;
+            }
+        }
+        if (!R) R = nblk >= 8 ? 1u : 8u;    /* no even grid: whole column blocks
+                                                or whole units per XCD */
+    }
     uint32_t g = items < n_cu ? (uint32_t)((items + 7) & ~(size_t)7) : n_cu;
     hipEvent_t e0 = ev ? ev[0] : nullptr, e1 = ev ? ev[1] : nullptr;
     GHIP_LAUNCH(e0, S > 1 ? nullptr : e1, k_fp8_gemm, dim3(g), dim3(256), PF_LDS, st, codes,
-                scales, x, y, g_part, (uint32_t)M, (uint32_t)N, (uint32_t)K, bm, S, exact_dev);
+                scales, x, y, g_part, (uint32_t)M, (uint32_t)N, (uint32_t)K, bm, S, R,
+                exact_dev);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || S == 1) return e;
     const size_t n = M * N;                          /* N % 256 == 0: n % 4 == 0 */
