@@ -475,7 +475,7 @@ def bench_bf16_gemv(lib, pkg, rt, steps, warmup, M=1, copies=2):
     return {"ms_per_step": ms, "value": nbytes / (ms * 1e-3) / 1e9,
             "bytes": nbytes, "flops": 2 * M * N * K, "kernel": kname,
             "kernel_ms": kt[kname], "kernel_bytes": nbytes,
-            "kernel_flops": 2 * M * N * K,
+            "kernel_flops": 2 * M * N * K, "traffic_key": "k_bf16_gemv@lm_head",
             "launch_ms": {n: round(v, 5) for n, v in kt.items()},
             "config": {"workload": "bf16_gemv (LM head through the bf16_gemm hook, "
                                    "c/bf16.h:712-767)", "N": N, "K": K, "M": M,
@@ -596,9 +596,8 @@ def bench_moe_decode_router(lib, pkg, rt, steps, warmup, rotate=64):
         "ms_per_step": ms, "value": nbytes / (ms * 1e-3) / 1e9,
         "bytes": nbytes, "flops": 2 * k * 3 * inter * dim + 2 * E * dim,
         "kernel": "k_moe_fused", "kernel_ms": t_fused, "kernel_bytes": slabs,
-        "kernel_flops": 2 * k * 3 * inter * dim,
-        "launch_ms": {"router (k_router_logits + k_router_select)": round(t_router, 5),
-                      "k_moe_fused": round(t_fused, 5)},
+        "kernel_flops": 2 * k * 3 * inter * dim, "traffic_key": "k_moe_fused@given_routing",
+        "launch_ms": {"k_router": round(t_router, 5), "k_moe_fused": round(t_fused, 5)},
         "config": {"workload": "moe_decode_router (BASELINE config 2 shapes, routed by "
                                "the reference router c/gmoe.h:191-208)",
                    "experts": E, "topk": k, "dim": dim, "inter": inter,
