@@ -512,7 +512,6 @@ struct ApusGhipStore {
     uint8_t *arena;
     uint32_t *nan_flags;                 /* device [n_experts] */
     GhipMoeDecodeWs ws;
-    uint64_t epoch;                      /* fused decode launches (ws.epoch) */
     /* decode staging for the host-pointer entry */
     uint16_t *d_x, *d_out;
     int32_t *d_idx;
@@ -571,9 +570,6 @@ int apus_ghip_store_open(ApusGhipStore **out, int n_experts, size_t dim,
            || hipMalloc((void **)&s->ws.err, 4) != hipSuccess
            || hipMemset(s->ws.err, 0, 4) != hipSuccess
            || (s->ws.n_cu = G.n_cu) == 0
-           || hipMalloc((void **)&s->ws.sync, 4) != hipSuccess
-           || hipMemset(s->ws.sync, 0, 4) != hipSuccess
-           || (s->ws.epoch = &s->epoch) == NULL
            || hipMalloc((void **)&s->ws.h, GHIP_MAX_TOPK * inter * 2) != hipSuccess
            || hipMalloc((void **)&s->d_x, dim * 2) != hipSuccess
            || hipMalloc((void **)&s->d_out, dim * 2) != hipSuccess
@@ -596,7 +592,6 @@ void apus_ghip_store_close(ApusGhipStore *s) {
     hipFree(s->nan_flags);
     hipFree(s->ws.route);
     hipFree(s->ws.err);
-    hipFree(s->ws.sync);
     hipFree(s->ws.h);
     hipFree(s->d_x);
     hipFree(s->d_out);

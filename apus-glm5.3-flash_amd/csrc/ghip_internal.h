@@ -48,8 +48,6 @@ typedef struct {
     uint16_t *h;          /* device [max topk, inter] bf16 */
     uint32_t *err;        /* device u32: nonzero after an invalid expert id */
     uint32_t n_cu;        /* persistent grid bound: the device's CU count */
-    uint32_t *sync;       /* device u32: the fused kernel's monotone counter */
-    uint64_t *epoch;      /* host: fused launches so far on this workspace */
 } GhipMoeDecodeWs;
 
 /* Streaming GEMV set-up (dynamic-LDS limits, persistent grid bound). */

@@ -15,14 +15,13 @@
  *            in-workgroup -- no float atomics, no cross-workgroup
  *            reduction, deterministic.
  *
- * k_moe_fused runs all three in one persistent launch (up to 8 kept slots):
- * h crosses the device through agent-scope atomic stores and loads and one
- * monotone arrival counter with a bounded wait. Release/acquire fences are
- * avoided on purpose: on gfx950 each one is an L2 write-back or invalidate,
- * which cost ~10x the weight streaming in a first fenced version.
- * k_moe_gateup + k_moe_down are the two-launch form (more than 8 slots, or
- * a store without the arrival counter): the kernel boundary orders the h
- * handoff.
+ * Two stream-ordered launches: k_moe_gateup (route + gate/up + SwiGLU ->
+ * h in HBM) and k_moe_down (h staged in LDS, down + combine); the kernel
+ * boundary orders the h handoff. A one-launch form that handed h across
+ * the device with coherent atomics and an arrival counter measured slower
+ * (50.7-53.3 us against 46.7-48.3 us per config-2 step): its atomic h
+ * stores and loads and the device-wide wait cost more than a kernel
+ * boundary.
  *
  * Weight streaming: each wave pulls its 16-row chunks (128-wide k, one
  * scale block) through a wave-private LDS ring with direct global->LDS
@@ -230,7 +229,6 @@ __device__ __forceinline__ void md_route(const float *__restrict__ logits,
 #define GU_STG 4096              /* bytes per stage */
 #define DN_R 6                   /* down ring stages per wave (one chunk each) */
 #define DN_STG 2048
-#define FU_SPIN (1u << 22)       /* bound on the fused kernel's phase wait */
 
 /* LDS that both kernels share (static, per workgroup) */
 struct MdShared {
@@ -419,90 +417,7 @@ __device__ __forceinline__ void md_combine(const MdShared &sh, uint32_t r0,
 }
 
 /* ------------------------------------------------------------------------ */
-/* fused decode: one persistent launch                                      */
-/* ------------------------------------------------------------------------ */
-
-/* Phases A and B, then a device-wide handoff of h, then phase C. One
- * workgroup per CU (LDS use keeps it at one), so all workgroups are
- * resident and the wait completes. h crosses XCDs (separate L2s) without
- * fences: it is written and read with agent-scope atomics (coherent
- * accesses), each workgroup waits for its h stores to complete before
- * bumping the counter, and readers load h only after the counter reads
- * complete. The counter is monotone per store (target = (epoch + 1) * G, the
- * host counts launches), so it is never reset; the wait is bounded and
- * reports a timeout in err (bit 4) instead of hanging. Each workgroup
- * issues its down weights' first ring stages before waiting. nsel <= 8. */
-__global__ __launch_bounds__(GU_NW * 64, 1) void k_moe_fused(
-    GhipBank bank, const uint16_t *__restrict__ x, const float *__restrict__ logits,
-    const int32_t *__restrict__ idx, const float *__restrict__ w, int topk, float limit,
-    uint32_t *__restrict__ hw, uint32_t *__restrict__ route_out, uint32_t *__restrict__ err,
-    uint32_t *__restrict__ sync, uint32_t target, uint16_t *__restrict__ out) {
-    extern __shared__ __attribute__((aligned(1024))) uint8_t gl[];
-    __shared__ MdShared sh;
-    const uint32_t dim = bank.dim, inter = bank.inter;
-    const uint32_t tid = threadIdx.x;
-    uint16_t *xs = (uint16_t *)gl;
-    uint8_t *gu_ring = gl + ((dim * 2u + 1023u) & ~1023u);
-    md_phase_route(bank, x, logits, idx, w, topk, xs, sh, err);
-    if (blockIdx.x == 0 && tid < GHIP_MOE_ROUTE_WORDS) route_out[tid] = sh.rt[tid];
-    /* h pairs packed by adjacent lanes into agent-scope 32-bit stores */
-    md_phase_gateup(bank, xs, gu_ring, sh, limit, [&](uint32_t q, uint32_t row, uint32_t hv) {
-        const uint32_t hi = __shfl_down(hv, 1, 64);
-        if ((row & 1u) == 0)
-            __hip_atomic_store(hw + (((size_t)q * inter + row) >> 1), hv | (hi << 16),
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    });
-    /* this workgroup's h stores are complete before it is counted */
-    GHIP_VMCNT(0);
-    __syncthreads();
-    if (tid == 0) __hip_atomic_fetch_add(sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    /* down: this workgroup's row groups; the first one's weights start
-     * streaming before the wait */
-    const uint32_t rgs = dim / MD_T;
-    uint8_t *hsb = gl;                                       /* h [8][inter] */
-    uint8_t *dn_ring = gl + (size_t)MD_NW * inter * 2u;
-    if (blockIdx.x < rgs) md_down_prologue(bank, sh, blockIdx.x * MD_T, 0u, dn_ring);
-    if (tid == 0) {
-        uint32_t spins = 0;
-        while (__hip_atomic_load(sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-            __builtin_amdgcn_s_sleep(1);
-            if (++spins == FU_SPIN) {
-                atomicOr(err, 4u);
-                break;
-            }
-        }
-    }
-    __syncthreads();
-    const uint32_t nsel = __builtin_amdgcn_readfirstlane(sh.rt[RT_NSEL]);
-    /* h of all slots: 64-bit coherent loads, all issued before any use */
-    const uint32_t dwords = nsel * inter / 4;
-    for (uint32_t i0 = tid; i0 < dwords; i0 += GU_NW * 64 * 8) {
-        uint64_t v[8];
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const uint32_t i = i0 + u * GU_NW * 64;
-            v[u] = i < dwords ? __hip_atomic_load((const uint64_t *)hw + i, __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_AGENT)
-                              : 0ull;
-        }
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const uint32_t i = i0 + u * GU_NW * 64;
-            if (i < dwords) ((uint64_t *)hsb)[i] = v[u];
-        }
-    }
-    __syncthreads();
-    for (uint32_t rg = blockIdx.x; rg < rgs; rg += gridDim.x) {
-        if (rg != blockIdx.x) md_down_prologue(bank, sh, rg * MD_T, 0u, dn_ring);
-        md_phase_down(bank, sh, rg * MD_T, 0u, (const uint16_t *)hsb, dn_ring);
-        __syncthreads();
-        md_combine(sh, rg * MD_T, out);
-        __syncthreads();
-    }
-}
-
-/* ------------------------------------------------------------------------ */
-/* two-launch decode (routings with more than 8 kept slots)                 */
+/* the two launches                                                         */
 /* ------------------------------------------------------------------------ */
 
 __global__ __launch_bounds__(GU_NW * 64, 1) void k_moe_gateup(
@@ -753,18 +668,6 @@ extern "C" hipError_t ghip_launch_moe_decode(const GhipBank *bank,
     hipEvent_t e0 = ev ? ev[0] : nullptr, e1 = ev ? ev[1] : nullptr;
     hipEvent_t e2 = ev ? ev[2] : nullptr, e3 = ev ? ev[3] : nullptr;
     hipError_t e;
-    if (topk <= MD_NW && ws->sync && ws->epoch) {
-        /* one persistent launch: grid = CUs (all resident) */
-        const size_t lds = lds_gu > lds_dn ? lds_gu : lds_dn;
-        const uint32_t G = ws->n_cu;
-        const uint32_t target = (uint32_t)((*ws->epoch + 1) * G);
-        GHIP_LAUNCH(e0, e1, k_moe_fused, dim3(G), dim3(GU_NW * 64), lds, st, *bank, x,
-                    logits, idx, w, topk, limit, (uint32_t *)ws->h, ws->route, ws->err,
-                    ws->sync, target, out);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
-        (*ws->epoch)++;
-        return hipSuccess;
-    }
     uint32_t groups = ((uint32_t)topk * (inter / MD_T) + GU_IPW - 1) / GU_IPW;
     if (groups > ws->n_cu) groups = ws->n_cu;             /* persistent */
     GHIP_LAUNCH(e0, e1, k_moe_gateup, dim3(groups), dim3(GU_NW * 64), lds_gu, st, *bank,
@@ -776,9 +679,8 @@ extern "C" hipError_t ghip_launch_moe_decode(const GhipBank *bank,
 }
 
 extern "C" hipError_t ghip_moe_decode_init(void) {
-    const void *ks[3] = {(const void *)k_moe_gateup, (const void *)k_moe_down,
-                         (const void *)k_moe_fused};
-    for (int i = 0; i < 3; i++) {
+    const void *ks[2] = {(const void *)k_moe_gateup, (const void *)k_moe_down};
+    for (int i = 0; i < 2; i++) {
         hipError_t e = hipFuncSetAttribute(ks[i], hipFuncAttributeMaxDynamicSharedMemorySize,
                                            MD_LDS_MAX);
         if (e != hipSuccess) return e;

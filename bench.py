@@ -76,7 +76,6 @@ def kernel_times(lib, rt, step, first, steps, n_ev, pairs):
         lib.apus_ghip_set_trace_events(arr, n_ev)
         step(first + i)
     lib.apus_ghip_set_trace_events(None, 0)
-    # events a step leaves unrecorded (the fused decode's 2..3) do not wait
     rt.synchronize()
     return {name: sum(evs[i][a].elapsed_ms(evs[i][b]) for i in range(steps)) / steps
             for name, (a, b) in pairs.items()}
@@ -141,22 +140,15 @@ def bench_moe_decode(lib, pkg, rt, steps, warmup, rotate=64):
     e1.synchronize()
     wall = time.perf_counter() - t0
     ms = e0.elapsed_ms(e1) / steps
-    fused = k <= 8          # top-k <= 8 runs as one fused launch (backend_hip.h)
     kt = kernel_times(lib, rt, step, warmup + steps, steps, 4,
-                      {"k_moe_fused": (0, 1)} if fused else
                       {"k_moe_gateup": (0, 1), "k_moe_down": (2, 3)})
     nbytes, flops, gu_bytes = moe_algorithmic_bytes(E, k, dim, inter)
     gbs = nbytes / (ms * 1e-3) / 1e9
     lib.apus_ghip_store_close(store)
-    if fused:
-        # the whole step is that launch
-        kern = {"kernel": "k_moe_fused", "kernel_ms": kt["k_moe_fused"],
-                "kernel_bytes": nbytes, "kernel_flops": flops,
-                "launch_ms": {"k_moe_fused": round(kt["k_moe_fused"], 5)}}
-    else:
-        kern = {"kernel": "k_moe_gateup", "kernel_ms": kt["k_moe_gateup"],
-                "kernel_bytes": gu_bytes, "kernel_flops": 2 * k * 2 * inter * dim,
-                "launch_ms": {n: round(v, 5) for n, v in kt.items()}}
+    # the dominant launch: routing + gate/up (2/3 of the weight bytes)
+    kern = {"kernel": "k_moe_gateup", "kernel_ms": kt["k_moe_gateup"],
+            "kernel_bytes": gu_bytes, "kernel_flops": 2 * k * 2 * inter * dim,
+            "launch_ms": {n: round(v, 5) for n, v in kt.items()}}
     return {
         "ms_per_step": ms, "value": gbs, "wall_s": wall,
         "bytes": nbytes, "flops": flops, **kern,
@@ -574,30 +566,31 @@ def bench_moe_decode_router(lib, pkg, rt, steps, warmup, rotate=64):
     e1.record(st)
     e1.synchronize()
     ms = e0.elapsed_ms(e1) / steps
-    # per-launch times: the router pair and the fused decode launch, each
-    # with its own dispatch-packet events
+    # per-launch times: the router and the two decode launches, each with
+    # its own dispatch-packet events
     n = steps
     evs = [[rt.Event() for _ in range(6)] for _ in range(n)]
     arr2, arr4 = ctypes.c_void_p * 2, ctypes.c_void_p * 4
     for i in range(n):
         lib.apus_ghip_set_trace_events(arr2(*[e.handle for e in evs[i][:2]]), 2)
         router(warmup + steps + i)
-        # the decode entry point takes four (the fused launch uses the first two)
         lib.apus_ghip_set_trace_events(arr4(*[e.handle for e in evs[i][2:]]), 4)
         decode(warmup + steps + i)
     lib.apus_ghip_set_trace_events(None, 0)
     rt.synchronize()
     t_router = sum(e[0].elapsed_ms(e[1]) for e in evs) / n
-    t_fused = sum(e[2].elapsed_ms(e[3]) for e in evs) / n
+    t_gu = sum(e[2].elapsed_ms(e[3]) for e in evs) / n
+    t_dn = sum(e[4].elapsed_ms(e[5]) for e in evs) / n
     lib.apus_ghip_store_close(store)
-    slabs = moe_algorithmic_bytes(E, k, dim, inter)[0] - E * 4     # no logits
-    nbytes = slabs + E * dim * 2 + E * 4
+    full, _, gu_bytes = moe_algorithmic_bytes(E, k, dim, inter)
+    nbytes = full - E * 4 + E * dim * 2 + E * 4         # gate_w + bias, no logits
     return {
         "ms_per_step": ms, "value": nbytes / (ms * 1e-3) / 1e9,
         "bytes": nbytes, "flops": 2 * k * 3 * inter * dim + 2 * E * dim,
-        "kernel": "k_moe_fused", "kernel_ms": t_fused, "kernel_bytes": slabs,
-        "kernel_flops": 2 * k * 3 * inter * dim, "traffic_key": "k_moe_fused@given_routing",
-        "launch_ms": {"k_router": round(t_router, 5), "k_moe_fused": round(t_fused, 5)},
+        "kernel": "k_moe_gateup", "kernel_ms": t_gu, "kernel_bytes": gu_bytes - E * 4,
+        "kernel_flops": 2 * k * 2 * inter * dim, "traffic_key": "k_moe_gateup@given_routing",
+        "launch_ms": {"k_router": round(t_router, 5), "k_moe_gateup": round(t_gu, 5),
+                      "k_moe_down": round(t_dn, 5)},
         "config": {"workload": "moe_decode_router (BASELINE config 2 shapes, routed by "
                                "the reference router c/gmoe.h:191-208)",
                    "experts": E, "topk": k, "dim": dim, "inter": inter,

@@ -214,11 +214,10 @@ int apus_ghip_moe_router_dev(const uint16_t *x, const uint16_t *gate_w,
                              int32_t *idx, float *w, void *stream);
 
 /* --- routed MoE decode (one token): SwiGLU experts + ordered combine,
- * c/gmoe.h:210-227 + 307-320 without the router and shared expert. Up to 8
- * kept slots: one persistent launch (routing, gate/up GEMVs with the
- * SwiGLU epilogue, a device-wide handoff of the activations, down GEMVs
- * with the ascending-expert bf16-per-add combine); more slots: two
- * stream-ordered launches split at the handoff.
+ * c/gmoe.h:210-227 + 307-320 without the router and shared expert. Two
+ * stream-ordered launches: routing + gate/up GEMVs with the SwiGLU epilogue
+ * (activations to HBM), then down GEMVs with the ascending-expert
+ * bf16-per-add combine.
  * Routing either given (idx/w [topk]) or computed on the device from
  * logits [n_experts] f32: stable top-k (ties -> lower id), w = softmax over
  * the k selected logits. Host-pointer variant is synchronous. */
@@ -259,9 +258,7 @@ int apus_ghip_moe_prefill_dev(ApusGhipStore *s, const uint16_t *x, size_t T,
  * set, launches carry start/stop events in their dispatch packets
  * (hipExtLaunchKernelGGL), so an event pair spans exactly one kernel:
  * apus_ghip_moe_decode_dev (n >= 4) times the routing + gate/up launch
- * with events[0..1] and the down launch with events[2..3] (when it runs as
- * one fused launch, top-k <= 8, events[0..1] time that launch and
- * events[2..3] are not recorded);
+ * with events[0..1] and the down launch with events[2..3];
  * apus_ghip_fp8blk_linear_dev, apus_ghip_bf16_gemm_dev and
  * apus_ghip_moe_router_dev (n >= 2) start events[0] with their first launch
  * and stop events[1] with their last; apus_ghip_moe_prefill_dev
