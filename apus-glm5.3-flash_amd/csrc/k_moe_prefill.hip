@@ -663,54 +663,72 @@ __global__ __launch_bounds__(256) void k_splitk_sum(const float *__restrict__ pa
 /* ordered combine                                                          */
 /* ------------------------------------------------------------------------ */
 
-/* One thread per 8 output columns of one token: the token's kept pairs in
- * ascending expert id, contrib = bf16(bf16(o) * w), y = bf16(y + contrib),
- * y from +0 (c/gmoe.h:307-320). */
+/* Workgroup (t, c) combines columns [2048c, 2048c + 2048) of token t, 8
+ * per thread: the token's kept pairs in ascending expert id,
+ * contrib = bf16(bf16(o) * w), y = bf16(y + contrib), y from +0
+ * (c/gmoe.h:307-320). One wave orders the token's pairs once into LDS
+ * (instead of every thread re-reading and re-sorting them); then each
+ * thread loads its rows of O in batches of 8 and adds them in that order. */
 __global__ __launch_bounds__(256) void k_pf_combine(
     const uint16_t *__restrict__ O, const int32_t *__restrict__ pos,
     const int32_t *__restrict__ idx, const float *__restrict__ w, uint32_t T,
     uint32_t topk, uint32_t dim, uint16_t *__restrict__ out) {
-    const uint32_t per = dim >> 3;
-    const size_t gid = (size_t)blockIdx.x * 256 + threadIdx.x;
-    const size_t t = gid / per;
-    if (t >= T) return;
-    const uint32_t d = (uint32_t)(gid - t * per) * 8;
-    int32_t ke[PF_MAXK], ks[PF_MAXK];
-    float kw[PF_MAXK];
-#pragma unroll
-    for (int j = 0; j < PF_MAXK; j++) {
-        const bool v = (uint32_t)j < topk;
-        const size_t p = t * topk + j;
-        const int32_t s = v ? pos[p] : -1;
-        ke[j] = s >= 0 ? idx[p] : 0x7fffffff;
-        ks[j] = s;
-        kw[j] = v ? w[p] : 0.0f;
+    __shared__ int32_t srow[PF_MAXK];
+    __shared__ float sw[PF_MAXK];
+    __shared__ uint32_t sn;
+    const uint32_t cpt = (dim + 2047) / 2048;          /* workgroups per token */
+    const uint32_t t = blockIdx.x / cpt, c = blockIdx.x - t * cpt;
+    const uint32_t tid = threadIdx.x;
+    if (tid < 64) {
+        /* lane j holds pair j; a kept pair's rank among the kept pairs by
+         * expert id is its slot in the ordered list (ids of kept pairs are
+         * distinct: repeats were dropped by the permutation) */
+        const uint32_t j = tid;
+        const size_t p = (size_t)t * topk + j;
+        const int32_t s = j < topk ? pos[p] : -1;
+        const int32_t e = s >= 0 ? idx[p] : 0x7fffffff;
+        const float wj = j < topk ? w[p] : 0.0f;
+        uint32_t rank = 0;
+        for (uint32_t q = 0; q < topk; q++) {
+            const int32_t eq = __shfl(e, (int)q, 64);
+            rank += eq < e;
+        }
+        const uint64_t kept = __ballot(s >= 0);
+        if (s >= 0) {
+            srow[rank] = s;
+            sw[rank] = wj;
+        }
+        if (tid == 0) sn = (uint32_t)__popcll(kept);
     }
+    __syncthreads();
+    const uint32_t d = c * 2048 + tid * 8;
+    if (t >= T || d >= dim) return;
+    const uint32_t n = sn;
     float y[8];
 #pragma unroll
     for (int q = 0; q < 8; q++) y[q] = 0.0f;
-    int32_t prev = -1;
-    for (uint32_t r = 0; r < topk; r++) {
-        int32_t best = 0x7fffffff, bs = -1;
-        float bw = 0.0f;
+    for (uint32_t r0 = 0; r0 < n; r0 += 8) {
+        ghip_u32x4 v[8];
 #pragma unroll
-        for (int j = 0; j < PF_MAXK; j++)
-            if (ke[j] > prev && ke[j] < best) { best = ke[j]; bs = ks[j]; bw = kw[j]; }
-        if (bs < 0) break;
-        prev = best;
-        const ghip_u32x4 v = *(const ghip_u32x4 *)(O + (size_t)bs * dim + d);
+        for (int r = 0; r < 8; r++)
+            if (r0 + r < n) v[r] = *(const ghip_u32x4 *)(O + (size_t)srow[r0 + r] * dim + d);
 #pragma unroll
-        for (int q = 0; q < 8; q++) {
-            const uint32_t bits = (v[q >> 1] >> (16 * (q & 1))) & 0xffffu;
-            const float c = ghip_bf16_round(ghip_bf16_f32(bits) * bw);
-            y[q] = ghip_bf16_round(y[q] + c);
+        for (int r = 0; r < 8; r++) {
+            if (r0 + r >= n) break;
+            const float wr = sw[r0 + r];
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const uint32_t bits = (v[r][q >> 1] >> (16 * (q & 1))) & 0xffffu;
+                const float cq = ghip_bf16_round(ghip_bf16_f32(bits) * wr);
+                y[q] = ghip_bf16_round(y[q] + cq);
+            }
         }
     }
     ghip_u32x4 r;
 #pragma unroll
     for (int q = 0; q < 4; q++)
         r[q] = ghip_bf16_bits(y[2 * q]) | (ghip_bf16_bits(y[2 * q + 1]) << 16);
-    *(ghip_u32x4 *)(out + t * dim + d) = r;
+    *(ghip_u32x4 *)(out + (size_t)t * dim + d) = r;
 }
 
 /* ------------------------------------------------------------------------ */
@@ -773,8 +791,8 @@ extern "C" hipError_t ghip_launch_moe_prefill(const GhipBank *bank,
                 ws->h, ws->perm, (const uint4 *)ws->tiles, ws->hdr, dim / 256,
                 (uint32_t)topk, limit, ws->o);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    const size_t nthr = T * (size_t)(dim / 8);
-    GHIP_LAUNCH(e6, e7, k_pf_combine, dim3((uint32_t)((nthr + 255) / 256)), dim3(256),
+    const size_t nblk_c = T * (size_t)((dim + 2047) / 2048);
+    GHIP_LAUNCH(e6, e7, k_pf_combine, dim3((uint32_t)nblk_c), dim3(256),
                 0, st, ws->o, ws->pos, idx, w, (uint32_t)T, (uint32_t)topk, dim, out);
     return hipGetLastError();
 }
