@@ -127,18 +127,36 @@ __global__ __launch_bounds__(1024) void k_pf_scan(
     uint4 *__restrict__ tiles, uint32_t *__restrict__ hdr) {
     __shared__ uint32_t sh[16];
     const uint32_t e = threadIdx.x;
+    /* the chunk counts are read in batches of 16 independent loads (one
+     * memory round trip per batch, not per chunk): a total pass, then the
+     * block scan, then a pass that writes each chunk's start row */
     uint32_t tot = 0;
     if (e < E)
-        for (uint32_t c = 0; c < nch; c++) {
-            const uint32_t v = cnt[(size_t)c * E + e];
-            cnt[(size_t)c * E + e] = tot;
-            tot += v;
+        for (uint32_t c0 = 0; c0 < nch; c0 += 16) {
+            uint32_t v[16];
+#pragma unroll
+            for (uint32_t u = 0; u < 16; u++)
+                v[u] = c0 + u < nch ? cnt[(size_t)(c0 + u) * E + e] : 0u;
+#pragma unroll
+            for (uint32_t u = 0; u < 16; u++) tot += v[u];
         }
     const uint32_t nt = (tot + PF_BM - 1) / PF_BM;
     const uint32_t base = pf_block_scan(tot, sh) - tot;
     const uint32_t tb = pf_block_scan(nt, sh) - nt;
     if (e < E) {
-        for (uint32_t c = 0; c < nch; c++) cnt[(size_t)c * E + e] += base;
+        uint32_t run = base;
+        for (uint32_t c0 = 0; c0 < nch; c0 += 16) {
+            uint32_t v[16];
+#pragma unroll
+            for (uint32_t u = 0; u < 16; u++)
+                v[u] = c0 + u < nch ? cnt[(size_t)(c0 + u) * E + e] : 0u;
+#pragma unroll
+            for (uint32_t u = 0; u < 16; u++)
+                if (c0 + u < nch) {
+                    cnt[(size_t)(c0 + u) * E + e] = run;
+                    run += v[u];
+                }
+        }
         for (uint32_t i = 0; i < nt; i++) {
             const uint32_t r0 = i * PF_BM;
             const uint32_t rows = tot - r0 < PF_BM ? tot - r0 : PF_BM;
