@@ -29,7 +29,10 @@ def floor_of(eo, w, idx):
             if idx[t, j] in seen:
                 keep[t, j] = False
             seen.add(idx[t, j])
-    c = O.bf16_to_f32(O.f32_to_bf16(O.bf16_to_f32(eo) * w[:, :, None]))
+    # non-finite expert outputs (inf x 0 weight) only feed masked or
+    # excluded entries: compute their products quietly
+    with np.errstate(invalid="ignore", over="ignore"):
+        c = O.bf16_to_f32(O.f32_to_bf16(O.bf16_to_f32(eo) * w[:, :, None]))
     c = np.where(keep[:, :, None], np.abs(c.astype(np.float64)), 0.0)
     return c.sum(1)
 

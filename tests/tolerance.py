@@ -35,7 +35,7 @@ def compare(got, ref, floor):
     got = np.asarray(got, np.uint16).ravel()
     ref = np.asarray(ref, np.uint16).ravel()
     floor = np.asarray(floor, np.float64)
-    floor = (np.full(ref.shape, float(floor)) if floor.size == 1
+    floor = (np.full(ref.shape, float(floor.reshape(-1)[0])) if floor.size == 1
              else floor.ravel())
     assert floor.shape == ref.shape, "floor must match the output size"
     ulp = np.abs(bf16_ord(got) - bf16_ord(ref))
