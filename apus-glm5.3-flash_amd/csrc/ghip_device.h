@@ -260,10 +260,14 @@ __device__ __forceinline__ void ghip_wait_stages(uint32_t m) {
     }
 }
 
-/* Wave-uniform F32 read through the constant address space: a scalar load
- * (lgkmcnt), so it never waits behind a stream of vector loads. */
+/* Wave-uniform reads through the constant address space: scalar loads
+ * (lgkmcnt), so they never wait behind a stream of vector loads. The data
+ * must not change while the kernel runs. */
 __device__ __forceinline__ float ghip_sload(const float *p, uint32_t i) {
     return ((const __attribute__((address_space(4))) float *)p)[i];
+}
+__device__ __forceinline__ uint32_t ghip_sload_u32(const uint32_t *p, uint32_t i) {
+    return ((const __attribute__((address_space(4))) uint32_t *)p)[i];
 }
 
 /* ---- streaming 16-row GEMV chunks through LDS ---------------------------

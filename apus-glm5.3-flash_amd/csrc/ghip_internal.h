@@ -65,7 +65,7 @@ typedef struct {
     size_t stride;               /* bytes between consecutive slabs */
     size_t off_gw, off_gs, off_uw, off_us, off_dw, off_ds;
     uint32_t n_experts, dim, inter;
-    const uint32_t *nan_flags;   /* device [n_experts] u32 or NULL */
+    const uint32_t *nan_flags;   /* device [n_experts] u32 (required by decode) or NULL */
 } GhipBank;
 
 /* K3: routed MoE decode for one token (routing + gate/up + SwiGLU, down +

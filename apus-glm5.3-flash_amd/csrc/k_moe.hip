@@ -298,7 +298,6 @@ __device__ __forceinline__ void md_phase_gateup(const GhipBank &bank, const uint
             const uint8_t *wu = slab + bank.off_uw + (size_t)r0 * dim;
             const float *sg = (const float *)(slab + bank.off_gs) + (size_t)(r0 >> 7) * nkb;
             const float *su = (const float *)(slab + bank.off_us) + (size_t)(r0 >> 7) * nkb;
-            const bool exact = bank.nan_flags && bank.nan_flags[e];
             auto issue = [&](uint32_t t) {
                 uint8_t *buf = ring + (t % GU_R) * GU_STG;
                 ghip_cdma_issue(wg, c0 + t, d, buf);
@@ -307,6 +306,10 @@ __device__ __forceinline__ void md_phase_gateup(const GhipBank &bank, const uint
 #pragma unroll
             for (uint32_t i = 0; i + 1 < GU_R; i++)
                 if (i < nc) issue(i);
+            /* the expert's NaN-code flag is read after the ring's first
+             * stages are on their way, so its round trip overlaps theirs */
+            __builtin_amdgcn_sched_barrier(0);
+            const bool exact = ghip_sload_u32(bank.nan_flags, e) != 0u;
             ghip_f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
             for (uint32_t t = 0; t < nc; t++) {
                 /* own DMA of stage t landed; stage t-1's buffer is free
@@ -380,7 +383,7 @@ __device__ __forceinline__ void md_phase_down(const GhipBank &bank, MdShared &sh
         const uint8_t *slab = bank.base + (size_t)e * bank.stride;
         const uint8_t *rows = slab + bank.off_dw + (size_t)r0 * inter;
         const float *srow = (const float *)(slab + bank.off_ds) + (size_t)(r0 >> 7) * nkb;
-        const bool exact = bank.nan_flags && bank.nan_flags[e];
+        const bool exact = ghip_sload_u32(bank.nan_flags, e) != 0u;
         const ghip_cdma d = ghip_cdma_offsets(lane, inter);
         uint8_t *ring = ring_base + wv * (DN_R * DN_STG);
         ghip_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -650,7 +653,7 @@ extern "C" hipError_t ghip_launch_moe_decode(const GhipBank *bank,
                                              const GhipMoeDecodeWs *ws,
                                              const hipEvent_t *ev,
                                              hipStream_t st) {
-    if (!bank || !ws || !x || !out) return hipErrorInvalidValue;
+    if (!bank || !bank->nan_flags || !ws || !x || !out) return hipErrorInvalidValue;
     const uint32_t dim = bank->dim, inter = bank->inter;
     if (topk <= 0 || topk > MD_MAXK || (uint32_t)topk > bank->n_experts)
         return hipErrorInvalidValue;
