@@ -87,33 +87,50 @@ __device__ __forceinline__ uint32_t rt_wave_red(uint32_t k) {
 
 /* Stable top-k by one wave (c/gmoe.h:175-189: larger first, ties to the
  * lower index): slot s of lane l holds the key of index l + 64 s (0 =
- * empty). Each of the k rounds takes the largest key (a lane-local max and
- * one DPP wave max); the lanes holding it name their lowest index, and a
- * second wave reduction (min index) runs only when more than one lane
- * does. Lane j < k returns pick j's index and its key in mykey. */
+ * empty). Each lane first sorts its R keys in descending order (a bubble
+ * network that swaps only on a strictly larger key, so equal keys keep
+ * the lower index first). Each of the k rounds then takes one 32-bit DPP
+ * wave max of the lanes' heads; the winning lane drops its head. When
+ * more than one lane holds the max, a second wave reduction picks the
+ * lowest index among them. Lane j < k returns pick j's index and its key
+ * in mykey. */
 template <int R>
 __device__ __forceinline__ int rt_select(uint32_t (&key)[R], int topk, uint32_t &mykey) {
     const uint32_t lane = threadIdx.x & 63u;
+    uint32_t ss[R];
+#pragma unroll
+    for (int s = 0; s < R; s++) ss[s] = (uint32_t)s;
+#pragma unroll
+    for (int i = 0; i < R - 1; i++)
+#pragma unroll
+        for (int j = 0; j < R - 1 - i; j++) {
+            const bool sw = key[j + 1] > key[j];
+            const uint32_t ka = key[j], kb = key[j + 1], sa = ss[j], sb = ss[j + 1];
+            key[j] = sw ? kb : ka;
+            key[j + 1] = sw ? ka : kb;
+            ss[j] = sw ? sb : sa;
+            ss[j + 1] = sw ? sa : sb;
+        }
     int myid = -1;
     mykey = 0u;
     for (int j = 0; j < topk; j++) {
-        uint32_t lm = key[0];
-#pragma unroll
-        for (int s = 1; s < R; s++) lm = key[s] > lm ? key[s] : lm;
-        const uint32_t wm = rt_wave_red<true>(lm);
-        uint32_t cand = 0xffffffffu;
-#pragma unroll
-        for (int s = R - 1; s >= 0; s--)
-            if (key[s] == wm) cand = lane + 64u * s;
-        const uint64_t bal = __ballot(cand != 0xffffffffu);
+        const uint32_t wm = rt_wave_red<true>(key[0]);
+        const uint64_t bal = __ballot(key[0] == wm);
         uint32_t widx;
-        if (__popcll(bal) == 1)
-            widx = (uint32_t)__builtin_amdgcn_readlane((int)cand, (int)__builtin_ctzll(bal));
-        else
-            widx = rt_wave_red<false>(cand);
+        if (__popcll(bal) == 1) {
+            const int wl = (int)__builtin_ctzll(bal);
+            widx = (uint32_t)wl + 64u * (uint32_t)__builtin_amdgcn_readlane((int)ss[0], wl);
+        } else {
+            widx = rt_wave_red<false>(key[0] == wm ? lane + 64u * ss[0] : 0xffffffffu);
+        }
+        if (lane == (widx & 63u)) {
 #pragma unroll
-        for (int s = 0; s < R; s++)
-            if (lane + 64u * s == widx) key[s] = 0u;
+            for (int s = 0; s + 1 < R; s++) {
+                key[s] = key[s + 1];
+                ss[s] = ss[s + 1];
+            }
+            key[R - 1] = 0u;
+        }
         if ((int)lane == j) {
             myid = (int)widx;
             mykey = wm;
