@@ -12,18 +12,20 @@
  *   k_pf_scan     one workgroup: exclusive offsets per (chunk, expert), the
  *                 expert-sorted row ranges and the tile list.
  *   k_pf_scatter  stable scatter (token order inside each expert).
- *   k_pf_gemm<0>  gate/up: H[s] = SwiGLU(bf16(x Wg^T), bf16(x Wu^T)) for the
+ *   k_pf_gemm<0, NW>  gate/up: H[s] = SwiGLU(bf16(x Wg^T), bf16(x Wu^T)) for the
  *                 sorted pair rows s of each tile; x rows gathered by token.
- *   k_pf_gemm<1>  down: O[s] = bf16(H[s] Wd^T).
+ *   k_pf_gemm<1, NW>  down: O[s] = bf16(H[s] Wd^T).
  *   k_pf_combine  out[t] = ascending-expert, bf16-per-add sum of
  *                 bf16(O[s] * w) over the token's pairs (c/gmoe.h:307-320).
  *
- * GEMM tile (both modes). A workgroup of 4 waves owns one tile of up to 256
- * expert-sorted rows and one column block; K is walked in 64-wide stages
- * (half an F32 scale block). Each wave owns two 32-column weight slots (gate
- * and up columns [c, c+32) in mode 0, so the SwiGLU epilogue is lane-local;
- * two 128-apart down column groups in mode 1) for all tile rows,
- * accumulating 2 x NRB v_mfma_f32_32x32x16_bf16 blocks in AGPRs. Both
+ * GEMM tile (both modes). A workgroup of 4 waves (NW = 4) owns one tile of
+ * up to 256 expert-sorted rows and one column block; K is walked in
+ * 64-wide stages (half an F32 scale block). Each wave owns two 32-column
+ * weight slots (gate and up columns [c, c+32) in mode 0, so the SwiGLU
+ * epilogue is lane-local; two 128-apart down column groups in mode 1) for
+ * all tile rows, accumulating 2 x NRB v_mfma_f32_32x32x16_bf16 blocks.
+ * With NW = 8 (two waves per SIMD) the same tile is split into two row
+ * halves, so one wave's MFMAs run while the other issues its DMA. Both
  * operands stream HBM -> LDS by direct DMA (global_load_lds) through a ring
  * of stages, the activation rows gathered by token in mode 0; the FP8 codes
  * are dequantized in registers when read from LDS, bit-exact
@@ -263,10 +265,21 @@ struct PfTile {
  * (b) is followed by MFMA work that hides the latency of the next stage's
  * first LDS reads. Scales come from the per-tile table in LDS (sct: one
  * {slot 0, slot 1} pair per 128-wide k block), not from memory. */
-template <int MODE, int NRB, bool EXACT>
+template <int MODE, int NRB, bool EXACT, int NW>
 __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
                                         const ghip_f32x2 *sct) {
-    constexpr uint32_t LPS = NRB + 4;            /* DMA loads per thread per stage */
+    /* NW = 4 waves (one per SIMD) or 8 (two per SIMD). Wave wv computes
+     * column group cw = wv & 3 over row half hr = wv >> 2 of the tile (8
+     * waves) or over all its rows (4 waves): NRBW row blocks. A stage's DMA
+     * is QA + 16 one-KB loads dealt round-robin to the waves (with 8 waves
+     * a 1-block tile loads its A rows twice, so every wave issues the same
+     * count: identical bytes to the same LDS place). */
+    static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+    constexpr uint32_t NRBW = NW == 8 ? (NRB >= 2 ? NRB / 2 : 1) : NRB;
+    constexpr uint32_t QA = NW == 8 && NRB < 2 ? 8 : 4 * NRB;
+    constexpr uint32_t NA = QA / NW;              /* A loads per wave per stage */
+    constexpr uint32_t NWL = 16 / NW;             /* weight loads per wave per stage */
+    constexpr uint32_t LPS = NA + NWL;            /* DMA loads per wave per stage */
     /* ring depth: as many stages as the ring holds, so tiles with few rows
      * keep more weight bytes in flight (3, 4, 6, 7 stages for 8, 4, 2, 1
      * row blocks) */
@@ -281,16 +294,19 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
     asm volatile("" : "+v"(tid));
     const uint32_t lane = tid & 63;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t cw = wv & 3u, hr = NW == 8 ? wv >> 2 : 0u;
     const uint32_t n = lane & 31, h = lane >> 5;
     const uint32_t K = t.K, nst = t.KS / PF_BK;
 
     /* --- DMA sources: a wave-uniform base (SGPRs; stage j adds j*64
      * elements) plus a 32-bit per-lane offset, so each load is one
      * SGPR-based global_load_lds with no per-load 64-bit address math ---- */
-    uint32_t aofs[NRB];
+    uint32_t aofs[NA], alds[NA];
 #pragma unroll
-    for (int i = 0; i < NRB; i++) {
-        const uint32_t r = 32 * i + 8 * wv + (lane >> 3);
+    for (int i = 0; i < (int)NA; i++) {
+        const uint32_t q = wv + NW * i, qq = NW == 8 && NRB < 2 ? (q & 3u) : q;
+        alds[i] = qq * 1024u;
+        const uint32_t r = 8 * qq + (lane >> 3);
         const uint32_t rc = r < t.rows ? r : t.rows - 1;
         const uint32_t src = MODE == 0 ? (uint32_t)t.perm[t.row0 + rc] / t.topk
                                        : t.row0 + rc;
@@ -300,13 +316,13 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
     /* weight load i of wave wv, lane l: LDS weight row 64i + 16wv + l/4,
      * i.e. slot (wv >> 1) & 1 (uniform), column 32i + 16(wv & 1) + l/4 of
      * that slot's block, piece (l & 3) ^ ((l >> 4) & 3) */
-    const uint32_t wslot = (wv >> 1) & 1u;
+    const uint32_t wslot = (cw >> 1) & 1u;
     const uint8_t *wbase = (wslot ? t.w1 : t.w0) + (size_t)(wslot ? t.cb1 : t.cb0) * K;
-    uint32_t wofs[4];
+    uint32_t wofs[NWL];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const uint32_t col = 32u * i + 16u * (wv & 1u) + (lane >> 2);
-        wofs[i] = col * K + 16u * ((lane & 3u) ^ ((lane >> 4) & 3u));
+    for (int b = 0; b < (int)NWL; b++) {
+        const uint32_t col = 32u * ((wv + NW * b) >> 2) + 16u * (cw & 1u) + (lane >> 2);
+        wofs[b] = col * K + 16u * ((lane & 3u) ^ ((lane >> 4) & 3u));
     }
     const uint8_t *abase = (const uint8_t *)t.act;
     /* part P (of 4) of stage j's loads into ring buffer b % NS: load q of
@@ -319,11 +335,12 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
         const uint8_t *aj = abase + (size_t)j * PF_BK * 2;
         const uint8_t *wj = wbase + (size_t)j * PF_BK;
 #pragma unroll
-        for (int i = 0; i < NRB; i++)
-            if (i % 4 == P) ghip_dma16(aj + aofs[i], st + (4 * i + wv) * 1024);
+        for (int i = 0; i < (int)NA; i++)
+            if (i % 4 == P) ghip_dma16(aj + aofs[i], st + alds[i]);
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-            if ((NRB + i) % 4 == P) ghip_dma16(wj + wofs[i], st + ASTG + (4 * i + wv) * 1024);
+        for (int b = 0; b < (int)NWL; b++)
+            if (((int)NA + b) % 4 == P)
+                ghip_dma16(wj + wofs[b], st + ASTG + (wv + NW * b) * 1024);
     };
     auto issue = [&](uint32_t j, uint32_t b) {
         issue_part(std::integral_constant<int, 0>{}, j, b);
@@ -340,13 +357,15 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
 #pragma unroll
     for (int u = 0; u < 2; u++) {
         const uint32_t ph = ((2 * h + u) ^ ((n >> 2) & 3)) * 16;
-        boff0[u] = ASTG + (64 * wv + n) * 64 + ph;
-        boff1[u] = ASTG + (64 * wv + 32 + n) * 64 + ph;
+        boff0[u] = ASTG + (64 * cw + n) * 64 + ph;
+        boff1[u] = ASTG + (64 * cw + 32 + n) * 64 + ph;
     }
 
-    ghip_f32x16 a0[NRB], a1[NRB];
+    ghip_f32x16 a0[NRBW], a1[NRBW];
+    /* this wave's first row block in the stage's A rows */
+    const uint32_t arow0 = NW == 8 && NRB >= 2 ? hr * NRBW * 32u * 128u : 0u;
 #pragma unroll
-    for (int rb = 0; rb < NRB; rb++)
+    for (int rb = 0; rb < (int)NRBW; rb++)
 #pragma unroll
         for (int i = 0; i < 16; i++) { a0[rb][i] = 0.0f; a1[rb][i] = 0.0f; }
 
@@ -362,7 +381,7 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
     __builtin_amdgcn_s_barrier();
     ghip_u32x4 q0[2], q1[2];
     ghip_f32x2 sc;
-    ghip_bf16x8 av[NRB], an[NRB], b0, b1, nb0, nb1;
+    ghip_bf16x8 av[NRBW], an[NRBW], b0, b1, nb0, nb1;
     {
         const uint8_t *st = lds;
         sc = sct[0];
@@ -372,8 +391,8 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
             q1[u] = *(const ghip_u32x4 *)(st + boff1[u]);
         }
 #pragma unroll
-        for (int rb = 0; rb < NRB; rb++)
-            av[rb] = *(const ghip_bf16x8 *)(st + rb * 32 * 128 + aoff[0]);
+        for (int rb = 0; rb < (int)NRBW; rb++)
+            av[rb] = *(const ghip_bf16x8 *)(st + arow0 + rb * 32 * 128 + aoff[0]);
         b0 = pf_deq8<EXACT>(q0[0][0], q0[0][1], sc[0]);
         b1 = pf_deq8<EXACT>(q1[0][0], q1[0][1], sc[1]);
     }
@@ -404,8 +423,8 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
                  * in registers */
                 const int u = (s + 1) >> 1, v = 2 * ((s + 1) & 1);
 #pragma unroll
-                for (int rb = 0; rb < NRB; rb++)
-                    an[rb] = *(const ghip_bf16x8 *)(st + rb * 32 * 128 + aoff[s + 1]);
+                for (int rb = 0; rb < (int)NRBW; rb++)
+                    an[rb] = *(const ghip_bf16x8 *)(st + arow0 + rb * 32 * 128 + aoff[s + 1]);
                 nb0 = pf_deq8<EXACT>(q0[u][v], q0[u][v + 1], sc[0]);
                 nb1 = pf_deq8<EXACT>(q1[u][v], q1[u][v + 1], sc[1]);
             } else if (NEXT) {
@@ -427,13 +446,13 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
                     q1[u] = *(const ghip_u32x4 *)(sn + boff1[u]);
                 }
 #pragma unroll
-                for (int rb = 0; rb < NRB; rb++)
-                    an[rb] = *(const ghip_bf16x8 *)(sn + rb * 32 * 128 + aoff[0]);
+                for (int rb = 0; rb < (int)NRBW; rb++)
+                    an[rb] = *(const ghip_bf16x8 *)(sn + arow0 + rb * 32 * 128 + aoff[0]);
                 nb0 = pf_deq8<EXACT>(q0[0][0], q0[0][1], sc[0]);
                 nb1 = pf_deq8<EXACT>(q1[0][0], q1[0][1], sc[1]);
             }
 #pragma unroll
-            for (int rb = 0; rb < NRB; rb++) {
+            for (int rb = 0; rb < (int)NRBW; rb++) {
                 a0[rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[rb], b0, a0[rb], 0, 0, 0);
                 a1[rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[rb], b1, a1[rb], 0, 0, 0);
             }
@@ -443,19 +462,19 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
                 /* 5 + NRB LDS reads (scales, B codes, A rows), then the
                  * dequant of the next step's B */
 #pragma unroll
-                for (int i = 0; i < 16; i++) {
+                for (int i = 0; i < 2 * (int)NRBW; i++) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   /* MFMA */
                     if (i < 2) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0); /* DS read */
                     if (i == 2) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                    if (i >= 3 && i < 3 + NRB) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                    if (i >= 5) __builtin_amdgcn_sched_group_barrier(0x002, 4, 0); /* VALU */
+                    if (i >= 3 && i < 3 + (int)NRBW) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    if (i >= (NW == 8 ? 3 : 5)) __builtin_amdgcn_sched_group_barrier(0x002, 4, 0); /* VALU */
                 }
             } else if (s < 3) {
 #pragma unroll
-                for (int i = 0; i < 16; i++) {
+                for (int i = 0; i < 2 * (int)NRBW; i++) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    if (i < NRB) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+                    if (i < (int)NRBW) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, NW == 8 ? 4 : 2, 0);
                 }
             }
             /* step boundary: a scheduling region per step, so the next
@@ -463,7 +482,7 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
              * pulled down next to their consumers */
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int rb = 0; rb < NRB; rb++) av[rb] = an[rb];
+            for (int rb = 0; rb < (int)NRBW; rb++) av[rb] = an[rb];
             b0 = nb0;
             b1 = nb1;
         }
@@ -473,12 +492,12 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
 
     /* epilogue: lane (n, h), register i of row block rb holds output row
      * rb*32 + 8*(i/4) + 4*h + i%4, column n of each slot */
-    const uint32_t c0 = t.cb0 + 32 * wv + n, c1 = t.cb1 + 32 * wv + n;
+    const uint32_t c0 = t.cb0 + 32 * cw + n, c1 = t.cb1 + 32 * cw + n;
 #pragma unroll
-    for (int rb = 0; rb < NRB; rb++) {
+    for (int rb = 0; rb < (int)NRBW; rb++) {
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            const uint32_t r = rb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+            const uint32_t r = (hr * NRBW + rb) * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
             if (r < t.rows) {
                 uint16_t *o = t.out + (size_t)(t.row0 + r) * t.N;
                 if (MODE == 0) {
@@ -505,8 +524,8 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
  * Grid: G (multiple of 8) >= tiles * nblk; 256 threads. The body is chosen
  * once per tile: 8, 4, 2 or 1 row blocks (the smallest that holds the
  * tile), or the exact-decode body for an expert with NaN codes. */
-template <int MODE>
-__global__ __launch_bounds__(256, 1) void k_pf_gemm(
+template <int MODE, int NW>
+__global__ __launch_bounds__(NW * 64, 1) void k_pf_gemm(
     GhipBank bank, const uint16_t *__restrict__ act,
     const int32_t *__restrict__ perm, const uint4 *__restrict__ tiles,
     const uint32_t *__restrict__ hdr, uint32_t nblk, uint32_t topk,
@@ -555,18 +574,18 @@ __global__ __launch_bounds__(256, 1) void k_pf_gemm(
          * here and made visible by the body's prologue barrier (the previous
          * item's trailing barrier ordered all reads of the old table) */
         ghip_f32x2 *sct = (ghip_f32x2 *)(pf_lds + PF_RING);
-        for (uint32_t b = threadIdx.x; b < nkb; b += 256) {
+        for (uint32_t b = threadIdx.x; b < nkb; b += NW * 64) {
             ghip_f32x2 v;
             v[0] = t.sr0[b];
             v[1] = t.sr1[b];
             sct[b] = v;
         }
         const uint32_t nrb = (t.rows + 31) >> 5;
-        if (bank.nan_flags && bank.nan_flags[e]) pf_tile<MODE, PF_RB, true>(t, pf_lds, sct);
-        else if (nrb > 4) pf_tile<MODE, 8, false>(t, pf_lds, sct);
-        else if (nrb > 2) pf_tile<MODE, 4, false>(t, pf_lds, sct);
-        else if (nrb > 1) pf_tile<MODE, 2, false>(t, pf_lds, sct);
-        else              pf_tile<MODE, 1, false>(t, pf_lds, sct);
+        if (bank.nan_flags && bank.nan_flags[e]) pf_tile<MODE, PF_RB, true, NW>(t, pf_lds, sct);
+        else if (nrb > 4) pf_tile<MODE, 8, false, NW>(t, pf_lds, sct);
+        else if (nrb > 2) pf_tile<MODE, 4, false, NW>(t, pf_lds, sct);
+        else if (nrb > 1) pf_tile<MODE, 2, false, NW>(t, pf_lds, sct);
+        else              pf_tile<MODE, 1, false, NW>(t, pf_lds, sct);
         /* every wave is done with the LDS ring before the next item's
          * prologue refills it */
         __builtin_amdgcn_s_barrier();
@@ -642,17 +661,17 @@ __global__ __launch_bounds__(256, 1) void k_fp8_gemm(
         }
         const uint32_t nrb = (t.rows + 31) >> 5;
         if (S > 1) {
-            if (exact) pf_tile<2, PF_RB, true>(t, pf_lds, sct);
-            else if (nrb > 4) pf_tile<2, 8, false>(t, pf_lds, sct);
-            else if (nrb > 2) pf_tile<2, 4, false>(t, pf_lds, sct);
-            else if (nrb > 1) pf_tile<2, 2, false>(t, pf_lds, sct);
-            else              pf_tile<2, 1, false>(t, pf_lds, sct);
+            if (exact) pf_tile<2, PF_RB, true, 4>(t, pf_lds, sct);
+            else if (nrb > 4) pf_tile<2, 8, false, 4>(t, pf_lds, sct);
+            else if (nrb > 2) pf_tile<2, 4, false, 4>(t, pf_lds, sct);
+            else if (nrb > 1) pf_tile<2, 2, false, 4>(t, pf_lds, sct);
+            else              pf_tile<2, 1, false, 4>(t, pf_lds, sct);
         } else {
-            if (exact) pf_tile<1, PF_RB, true>(t, pf_lds, sct);
-            else if (nrb > 4) pf_tile<1, 8, false>(t, pf_lds, sct);
-            else if (nrb > 2) pf_tile<1, 4, false>(t, pf_lds, sct);
-            else if (nrb > 1) pf_tile<1, 2, false>(t, pf_lds, sct);
-            else              pf_tile<1, 1, false>(t, pf_lds, sct);
+            if (exact) pf_tile<1, PF_RB, true, 4>(t, pf_lds, sct);
+            else if (nrb > 4) pf_tile<1, 8, false, 4>(t, pf_lds, sct);
+            else if (nrb > 2) pf_tile<1, 4, false, 4>(t, pf_lds, sct);
+            else if (nrb > 1) pf_tile<1, 2, false, 4>(t, pf_lds, sct);
+            else              pf_tile<1, 1, false, 4>(t, pf_lds, sct);
         }
         __builtin_amdgcn_s_barrier();
     }
@@ -801,11 +820,20 @@ extern "C" hipError_t ghip_launch_moe_prefill(const GhipBank *bank,
     const size_t lds = PF_LDS;
     (void)mt;
     const uint32_t g0 = ws->n_cu, g1 = ws->n_cu;
-    GHIP_LAUNCH(e2, e3, k_pf_gemm<0>, dim3(g0), dim3(256), lds, st, *bank,
-                x, ws->perm, (const uint4 *)ws->tiles, ws->hdr, inter / 128,
-                (uint32_t)topk, limit, ws->h);
+    /* gate/up with two waves per SIMD when the tiles are mostly full (on
+     * average at least half a 256-row tile per expert): their MFMAs cover
+     * each other's DMA issue; sparse routings, mostly short tiles, and the
+     * down GEMM keep one wave per SIMD */
+    if (P >= (size_t)E * (PF_BM / 2))
+        GHIP_LAUNCH(e2, e3, (k_pf_gemm<0, 8>), dim3(g0), dim3(512), lds, st, *bank,
+                    x, ws->perm, (const uint4 *)ws->tiles, ws->hdr, inter / 128,
+                    (uint32_t)topk, limit, ws->h);
+    else
+        GHIP_LAUNCH(e2, e3, (k_pf_gemm<0, 4>), dim3(g0), dim3(256), lds, st, *bank,
+                    x, ws->perm, (const uint4 *)ws->tiles, ws->hdr, inter / 128,
+                    (uint32_t)topk, limit, ws->h);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    GHIP_LAUNCH(e4, e5, k_pf_gemm<1>, dim3(g1), dim3(256), lds, st, *bank,
+    GHIP_LAUNCH(e4, e5, (k_pf_gemm<1, 4>), dim3(g1), dim3(256), lds, st, *bank,
                 ws->h, ws->perm, (const uint4 *)ws->tiles, ws->hdr, dim / 256,
                 (uint32_t)topk, limit, ws->o);
     if ((e = hipGetLastError()) != hipSuccess) return e;
@@ -918,12 +946,12 @@ extern "C" hipError_t ghip_launch_fp8_gemm(const uint8_t *codes, const float *sc
 
 extern "C" hipError_t ghip_moe_prefill_init(void) {
     const int lds = PF_LDS;
-    hipError_t e = hipFuncSetAttribute((const void *)k_pf_gemm<0>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-    if (e != hipSuccess) return e;
-    e = hipFuncSetAttribute((const void *)k_fp8_gemm,
-                            hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-    if (e != hipSuccess) return e;
-    return hipFuncSetAttribute((const void *)k_pf_gemm<1>,
-                               hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    const void *ks[4] = {(const void *)k_pf_gemm<0, 8>, (const void *)k_pf_gemm<0, 4>,
+                         (const void *)k_pf_gemm<1, 4>, (const void *)k_fp8_gemm};
+    for (int i = 0; i < 4; i++) {
+        hipError_t e = hipFuncSetAttribute(ks[i], hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           lds);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
