@@ -820,11 +820,12 @@ extern "C" hipError_t ghip_launch_moe_prefill(const GhipBank *bank,
     const size_t lds = PF_LDS;
     (void)mt;
     const uint32_t g0 = ws->n_cu, g1 = ws->n_cu;
-    /* gate/up with two waves per SIMD when the tiles are mostly full (on
-     * average at least half a 256-row tile per expert): their MFMAs cover
-     * each other's DMA issue; sparse routings, mostly short tiles, and the
-     * down GEMM keep one wave per SIMD */
-    if (P >= (size_t)E * (PF_BM / 2))
+    /* two waves per SIMD when the tiles are mostly full (on average at
+     * least half a 256-row tile per expert): one wave's MFMAs cover the
+     * other's DMA issue; sparse routings (mostly short tiles) keep one wave
+     * per SIMD, which wastes no MFMAs on a half-empty row split */
+    const bool full = P >= (size_t)E * (PF_BM / 2);
+    if (full)
         GHIP_LAUNCH(e2, e3, (k_pf_gemm<0, 8>), dim3(g0), dim3(512), lds, st, *bank,
                     x, ws->perm, (const uint4 *)ws->tiles, ws->hdr, inter / 128,
                     (uint32_t)topk, limit, ws->h);
@@ -833,9 +834,14 @@ extern "C" hipError_t ghip_launch_moe_prefill(const GhipBank *bank,
                     x, ws->perm, (const uint4 *)ws->tiles, ws->hdr, inter / 128,
                     (uint32_t)topk, limit, ws->h);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    GHIP_LAUNCH(e4, e5, (k_pf_gemm<1, 4>), dim3(g1), dim3(256), lds, st, *bank,
-                ws->h, ws->perm, (const uint4 *)ws->tiles, ws->hdr, dim / 256,
-                (uint32_t)topk, limit, ws->o);
+    if (full)
+        GHIP_LAUNCH(e4, e5, (k_pf_gemm<1, 8>), dim3(g1), dim3(512), lds, st, *bank,
+                    ws->h, ws->perm, (const uint4 *)ws->tiles, ws->hdr, dim / 256,
+                    (uint32_t)topk, limit, ws->o);
+    else
+        GHIP_LAUNCH(e4, e5, (k_pf_gemm<1, 4>), dim3(g1), dim3(256), lds, st, *bank,
+                    ws->h, ws->perm, (const uint4 *)ws->tiles, ws->hdr, dim / 256,
+                    (uint32_t)topk, limit, ws->o);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     const size_t nblk_c = T * (size_t)((dim + 2047) / 2048);
     GHIP_LAUNCH(e6, e7, k_pf_combine, dim3((uint32_t)nblk_c), dim3(256),
@@ -946,9 +952,10 @@ extern "C" hipError_t ghip_launch_fp8_gemm(const uint8_t *codes, const float *sc
 
 extern "C" hipError_t ghip_moe_prefill_init(void) {
     const int lds = PF_LDS;
-    const void *ks[4] = {(const void *)k_pf_gemm<0, 8>, (const void *)k_pf_gemm<0, 4>,
-                         (const void *)k_pf_gemm<1, 4>, (const void *)k_fp8_gemm};
-    for (int i = 0; i < 4; i++) {
+    const void *ks[5] = {(const void *)k_pf_gemm<0, 8>, (const void *)k_pf_gemm<0, 4>,
+                         (const void *)k_pf_gemm<1, 8>, (const void *)k_pf_gemm<1, 4>,
+                         (const void *)k_fp8_gemm};
+    for (int i = 0; i < 5; i++) {
         hipError_t e = hipFuncSetAttribute(ks[i], hipFuncAttributeMaxDynamicSharedMemorySize,
                                            lds);
         if (e != hipSuccess) return e;
