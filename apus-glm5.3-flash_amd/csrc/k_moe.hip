@@ -147,12 +147,22 @@ template <int R>
 __device__ __forceinline__ void md_route_softmax(const float *__restrict__ logits, int topk,
                                                  int E, uint32_t *rt) {
     const int lane = threadIdx.x & 63;
-    uint32_t key[R];
+    /* all R loads are issued before any is used: the index is clamped
+     * rather than the load predicated, which would wait for each load
+     * inside its own branch (R serial memory round trips) */
+    float v[R];
 #pragma unroll
     for (int s = 0; s < R; s++) {
         const int i = lane + 64 * s;
-        key[s] = i < E ? rt_key(logits[i]) : 0u;
+        v[s] = logits[i < E ? i : E - 1];
     }
+    /* an unconditional use pins each load here (the compiler would
+     * otherwise sink a load into the branch that consumes it) */
+#pragma unroll
+    for (int s = 0; s < R; s++) asm volatile("" ::"v"(v[s]));
+    uint32_t key[R];
+#pragma unroll
+    for (int s = 0; s < R; s++) key[s] = lane + 64 * s < E ? rt_key(v[s]) : 0u;
     uint32_t mk;
     const int myid = rt_select<R>(key, topk, mk);
     const float mylog = rt_val(mk);
@@ -266,10 +276,16 @@ __device__ __forceinline__ void md_phase_route(const GhipBank &bank,
                                                uint32_t *__restrict__ err) {
     const uint32_t tid = threadIdx.x;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    /* the first GU_NW * 64 pieces of x are loaded before the routing, so
+     * the routing wave's piece does not cost a round trip after it */
+    const uint32_t n16 = bank.dim >> 3;
+    const ghip_u32x4 x0 = ((const ghip_u32x4 *)x)[tid < n16 ? tid : n16 - 1];
     if (wv == 0)
         md_route(logits, idx, w, topk, (int)bank.n_experts, sh.rt, sh.te, sh.tw,
                  blockIdx.x == 0 ? err : nullptr);
-    for (uint32_t i = tid; i < (bank.dim >> 3); i += GU_NW * 64)
+    asm volatile("" ::"v"(x0));
+    if (tid < n16) ((ghip_u32x4 *)xs)[tid] = x0;
+    for (uint32_t i = tid + GU_NW * 64; i < n16; i += GU_NW * 64)
         ((ghip_u32x4 *)xs)[i] = ((const ghip_u32x4 *)x)[i];
     /* nothing of the routing (its error-flag atomic included) stays in
      * flight into the streaming loops, whose vmcnt waits count only DMA */
@@ -475,10 +491,30 @@ __global__ __launch_bounds__(MD_NW * 64, 1) void k_moe_down(
     const uint32_t r0 = blockIdx.x * MD_T;
     for (uint32_t base = 0; base < nsel; base += MD_NW) {
         const uint32_t m = nsel - base < MD_NW ? nsel - base : MD_NW;
-        for (uint32_t i = tid; i < m * inter / 8; i += MD_NW * 64)
-            ((ghip_u32x4 *)hs)[i] = ((const ghip_u32x4 *)(h + (size_t)base * inter))[i];
-        __syncthreads();
+        /* the weight ring's first stages, then h, all in flight together;
+         * h loads go four per thread with a clamped index, so none waits
+         * behind another (a load-then-store loop costs a round trip per
+         * iteration) */
         md_down_prologue(bank, sh, r0, base, ring);
+        const uint32_t n16 = m * inter / 8;
+        const ghip_u32x4 *hsrc = (const ghip_u32x4 *)(h + (size_t)base * inter);
+        for (uint32_t i0 = tid; i0 < n16; i0 += 4 * MD_NW * 64) {
+            ghip_u32x4 v[4];
+#pragma unroll
+            for (uint32_t u = 0; u < 4; u++) {
+                const uint32_t i = i0 + u * MD_NW * 64;
+                v[u] = hsrc[i < n16 ? i : n16 - 1];
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < 4; u++) asm volatile("" ::"v"(v[u]));
+#pragma unroll
+            for (uint32_t u = 0; u < 4; u++) {
+                const uint32_t i = i0 + u * MD_NW * 64;
+                if (i < n16) ((ghip_u32x4 *)hs)[i] = v[u];
+            }
+        }
+        GHIP_VMCNT(0);
+        __syncthreads();
         md_phase_down(bank, sh, r0, base, hs, ring);
         __syncthreads();
     }
@@ -542,16 +578,27 @@ __device__ __forceinline__ void rt_sigmoid_select(Logit lg, const float *__restr
                                                   int32_t *__restrict__ idx,
                                                   float *__restrict__ w) {
     const int lane = threadIdx.x & 63;
+    /* logits and biases of all R slots are loaded (clamped index, no
+     * predicated load) before any is used: one memory round trip */
+    float lv[R], bv[R];
+#pragma unroll
+    for (int s = 0; s < R; s++) {
+        const uint32_t i = (uint32_t)lane + 64u * s, ic = i < E ? i : E - 1u;
+        lv[s] = lg(ic);
+        bv[s] = bias[ic];
+    }
+#pragma unroll
+    for (int s = 0; s < R; s++) asm volatile("" ::"v"(lv[s]), "v"(bv[s]));
     uint32_t key[R];
 #pragma unroll
     for (int s = 0; s < R; s++) {
         const uint32_t i = (uint32_t)lane + 64u * s;
         key[s] = 0u;
         if (i < E) {
-            const float v = ghip_sigmoid_np(lg(i));
+            const float v = ghip_sigmoid_np(lv[s]);
             sc[i] = v;
             if (scores) scores[i] = v;
-            key[s] = rt_key(v + bias[i]);
+            key[s] = rt_key(v + bv[s]);
         }
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);           /* lgkmcnt(0) */

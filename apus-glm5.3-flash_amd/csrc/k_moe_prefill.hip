@@ -122,10 +122,12 @@ __device__ __forceinline__ uint32_t pf_block_scan(uint32_t v, uint32_t *sh) {
 
 /* One workgroup of 1024 threads, thread e = expert e. cnt becomes the
  * exclusive start offset (in the expert-sorted order) of each (chunk,
- * expert); tiles[] = {expert, first sorted row, rows, 0}; hdr gets the tile
+ * expert); tiles[] = {expert, first sorted row, rows, NaN-code flag of the
+ * expert (nan_flags[e] != 0; 0 without nan_flags)}; hdr gets the tile
  * count and the number of valid pairs. */
 __global__ __launch_bounds__(1024) void k_pf_scan(
     uint32_t *__restrict__ cnt, uint32_t nch, uint32_t E,
+    const uint32_t *__restrict__ nan_flags,
     uint4 *__restrict__ tiles, uint32_t *__restrict__ hdr) {
     __shared__ uint32_t sh[16];
     const uint32_t e = threadIdx.x;
@@ -146,6 +148,7 @@ __global__ __launch_bounds__(1024) void k_pf_scan(
     const uint32_t base = pf_block_scan(tot, sh) - tot;
     const uint32_t tb = pf_block_scan(nt, sh) - nt;
     if (e < E) {
+        const uint32_t nanf = nan_flags && nan_flags[e] ? 1u : 0u;
         uint32_t run = base;
         for (uint32_t c0 = 0; c0 < nch; c0 += 16) {
             uint32_t v[16];
@@ -162,7 +165,7 @@ __global__ __launch_bounds__(1024) void k_pf_scan(
         for (uint32_t i = 0; i < nt; i++) {
             const uint32_t r0 = i * PF_BM;
             const uint32_t rows = tot - r0 < PF_BM ? tot - r0 : PF_BM;
-            tiles[tb + i] = make_uint4(e, base + r0, rows, 0u);
+            tiles[tb + i] = make_uint4(e, base + r0, rows, nanf);
         }
     }
     if (e == 1023) {
@@ -267,7 +270,7 @@ struct PfTile {
  * {slot 0, slot 1} pair per 128-wide k block), not from memory. */
 template <int MODE, int NRB, bool EXACT, int NW>
 __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
-                                        const ghip_f32x2 *sct) {
+                                        ghip_f32x2 *sct) {
     /* NW = 4 waves (one per SIMD) or 8 (two per SIMD). Wave wv computes
      * column group cw = wv & 3 over row half hr = wv >> 2 of the tile (8
      * waves) or over all its rows (4 waves): NRBW row blocks. A stage's DMA
@@ -298,6 +301,16 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
     const uint32_t n = lane & 31, h = lane >> 5;
     const uint32_t K = t.K, nst = t.KS / PF_BK;
 
+    /* the tile's scale table ({slot 0, slot 1} per 128-wide k block): this
+     * thread's entry is loaded first (clamped index, unpredicated), so its
+     * round trip overlaps the row-permutation loads below; it is stored
+     * before the DMA prologue is issued (a wait behind the DMA would hold
+     * the tile's start until the whole prologue landed) */
+    const uint32_t nsc = t.KS >> 7, sb = tid < nsc ? tid : nsc - 1;
+    ghip_f32x2 sv;
+    sv[0] = t.sr0[sb];
+    sv[1] = t.sr1[sb];
+
     /* --- DMA sources: a wave-uniform base (SGPRs; stage j adds j*64
      * elements) plus a 32-bit per-lane offset, so each load is one
      * SGPR-based global_load_lds with no per-load 64-bit address math ---- */
@@ -312,6 +325,13 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
                                        : t.row0 + rc;
         const uint32_t p = (lane & 7) ^ ((r >> 1) & 7);
         aofs[i] = src * K * 2u + 16u * p;
+    }
+    if (tid < nsc) sct[tid] = sv;
+    for (uint32_t b = tid + NW * 64; b < nsc; b += NW * 64) {
+        ghip_f32x2 v;
+        v[0] = t.sr0[b];
+        v[1] = t.sr1[b];
+        sct[b] = v;
     }
     /* weight load i of wave wv, lane l: LDS weight row 64i + 16wv + l/4,
      * i.e. slot (wv >> 1) & 1 (uniform), column 32i + 16(wv & 1) + l/4 of
@@ -540,9 +560,12 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pf_gemm(
     const uint32_t items = ntx * nblk;
     const uint32_t K = MODE == 0 ? bank.dim : bank.inter;
     const uint32_t nkb = K >> 7;
+    /* the next item's tile record is loaded while this item runs */
+    uint4 tdn = c < items ? tiles[x + 8 * (c / nblk)] : make_uint4(0u, 0u, 0u, 0u);
     for (uint32_t k = c; k < items; k += per) {
-        const uint32_t tile = x + 8 * (k / nblk), nb = k % nblk;
-        const uint4 td = tiles[tile];
+        const uint32_t nb = k % nblk;
+        const uint4 td = tdn;
+        if (k + per < items) tdn = tiles[x + 8 * ((k + per) / nblk)];
         const uint32_t e = td.x;
         PfTile t;
         t.act = act;
@@ -570,18 +593,12 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pf_gemm(
             t.sr0 = (const float *)(slab + bank.off_ds) + (size_t)(2 * nb) * nkb;
             t.sr1 = (const float *)(slab + bank.off_ds) + (size_t)(2 * nb + 1) * nkb;
         }
-        /* the tile's scale table: {slot 0, slot 1} per k block, written
-         * here and made visible by the body's prologue barrier (the previous
-         * item's trailing barrier ordered all reads of the old table) */
+        /* the tile's scale table is filled by the body and made visible by
+         * its prologue barrier (the previous item's trailing barrier ordered
+         * all reads of the old table); td.w = the expert's NaN-code flag */
         ghip_f32x2 *sct = (ghip_f32x2 *)(pf_lds + PF_RING);
-        for (uint32_t b = threadIdx.x; b < nkb; b += NW * 64) {
-            ghip_f32x2 v;
-            v[0] = t.sr0[b];
-            v[1] = t.sr1[b];
-            sct[b] = v;
-        }
         const uint32_t nrb = (t.rows + 31) >> 5;
-        if (bank.nan_flags && bank.nan_flags[e]) pf_tile<MODE, PF_RB, true, NW>(t, pf_lds, sct);
+        if (td.w) pf_tile<MODE, PF_RB, true, NW>(t, pf_lds, sct);
         else if (nrb > 4) pf_tile<MODE, 8, false, NW>(t, pf_lds, sct);
         else if (nrb > 2) pf_tile<MODE, 4, false, NW>(t, pf_lds, sct);
         else if (nrb > 1) pf_tile<MODE, 2, false, NW>(t, pf_lds, sct);
@@ -653,12 +670,6 @@ __global__ __launch_bounds__(256, 1) void k_fp8_gemm(
         t.sr0 = scales + (size_t)(2 * nb) * nkb + kb0;
         t.sr1 = scales + (size_t)(2 * nb + 1) * nkb + kb0;
         ghip_f32x2 *sct = (ghip_f32x2 *)(pf_lds + PF_RING);
-        for (uint32_t b = threadIdx.x; b < kb1 - kb0; b += 256) {
-            ghip_f32x2 v;
-            v[0] = t.sr0[b];
-            v[1] = t.sr1[b];
-            sct[b] = v;
-        }
         const uint32_t nrb = (t.rows + 31) >> 5;
         if (S > 1) {
             if (exact) pf_tile<2, PF_RB, true, 4>(t, pf_lds, sct);
@@ -812,7 +823,7 @@ extern "C" hipError_t ghip_launch_moe_prefill(const GhipBank *bank,
                 (uint32_t)P, (uint32_t)topk, E, ws->cnt, ws->eid, ws->hdr);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(k_pf_scan, dim3(1), dim3(1024), 0, st, ws->cnt, nch, E,
-                       (uint4 *)ws->tiles, ws->hdr);
+                       bank->nan_flags, (uint4 *)ws->tiles, ws->hdr);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     GHIP_LAUNCH(nullptr, e1, k_pf_scatter, dim3(nch), dim3(1024), 16 * E * 4, st,
                 ws->eid, (uint32_t)P, E, ws->cnt, ws->perm, ws->pos);
