@@ -14,7 +14,9 @@ the four DSA FP8 projections at M = 2048 prefill rows (the fp8blk_linear
 hook's MFMA GEMM path), in TFLOP/s. --workload bf16_gemv runs the LM head
 through the bf16_gemm hook; --workload moe_decode_router runs config 2 routed
 by the reference's sigmoid/bias router on the GPU; --workload store_load
-fills the HBM expert store from a converted v2 container.
+fills the HBM expert store from a converted v2 container; --workload
+library_gemm times the vendor library (torch -> hipBLASLt, BF16) on the
+prefill shapes, a practical MFMA reference rather than this build.
 
 Prints ONE JSON line (rank 0). Extra objects: "roofline" (dominant kernel,
 HIP-event timed on its stream) and "cpu_baseline" (the reference CPU path,
@@ -927,6 +929,55 @@ def bench_copy(rt, steps, warmup, nbytes=256 << 20):
                        "bytes_read": nbytes, "bytes_written": nbytes}}
 
 
+def bench_library_gemm(steps, warmup):
+    """The vendor library on the prefill shapes, as a practical MFMA
+    reference: torch (hipBLASLt) BF16 x BF16 products with no dequant, no
+    gather and no epilogue. Batched: config 4's gate/up and down shapes
+    (288 experts x 228 rows, the uniform routing's mean); dense: two large
+    GEMMs. Both operands contiguous (batched bf16 products with a
+    transposed right operand are avoided on this platform). The first
+    shape is the line's value."""
+    import torch
+    dev = "cuda:0"
+    shapes = [("grouped gate/up 288x[228,4096]x[4096,4096]", 288, 228, 4096, 4096),
+              ("grouped down 288x[228,2048]x[2048,4096]", 288, 228, 4096, 2048),
+              ("dense [65536,4096]x[4096,4096]", 1, 65536, 4096, 4096),
+              ("dense [8192,4096]x[4096,4096]", 1, 8192, 4096, 4096)]
+    g = torch.Generator(device=dev)
+    g.manual_seed(0x11B)
+    res = {}
+    first = None
+    for name, G, M, N, K in shapes:
+        a = torch.randn(G, M, K, device=dev, dtype=torch.bfloat16, generator=g)
+        b = torch.randn(G, K, N, device=dev, dtype=torch.bfloat16, generator=g)
+        fn = (lambda: torch.bmm(a, b)) if G > 1 else (lambda: a[0] @ b[0])
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        flops = 2.0 * G * M * N * K
+        res[name] = {"ms": round(ms, 4), "tflops": round(flops / (ms * 1e-3) / 1e12, 1)}
+        if first is None:
+            first = (name, ms, flops)
+        del a, b
+    name, ms, flops = first
+    return {"ms_per_step": ms, "value": flops / (ms * 1e-3) / 1e12, "unit": "TFLOP/s",
+            "bytes": 0, "flops": flops, "kernel": "hipBLASLt " + name,
+            "kernel_ms": ms, "kernel_bytes": 0, "kernel_flops": flops,
+            "launch_ms": {n: v["ms"] for n, v in res.items()},
+            "traffic_key": "none", "data": "synthetic (torch.randn, seeded)",
+            "config": {"workload": "library_gemm (hipBLASLt via torch, BF16, "
+                                   "prefill shapes; a reference, not this build)",
+                       "results": res}}
+
+
 # --------------------------------------------------------------------------
 
 def roofline_of(r):
@@ -1005,7 +1056,7 @@ def line_of(metric, r, cpu, steps, warmup):
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (include/apus_synth.h generator, seeded)",
+        "data": r.get("data", "synthetic (include/apus_synth.h generator, seeded)"),
         "config": r["config"],
         "roofline": roofline_of(r),
         "cpu_baseline": cpu,
@@ -1020,12 +1071,16 @@ def line_of(metric, r, cpu, steps, warmup):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=None,
+                    help="timed steps (default per workload: 2000 for the "
+                         "decode GEMVs, 5 for prefill, 200 otherwise)")
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed warmup steps (default per workload: 500 for "
+                         "the decode GEMVs, 2 for prefill, 20 otherwise)")
     ap.add_argument("--workload", default="moe_decode",
                     choices=["moe_decode", "dense_gemv", "dense_gemm", "bf16_gemv",
                              "moe_decode_router", "store_load", "prefill_zipf",
-                             "prefill_stack", "copy"])
+                             "prefill_stack", "copy", "library_gemm"])
     ap.add_argument("--m", type=int, default=1,
                     help="dense_gemv / bf16_gemv rows (1, 2, 4)")
     ap.add_argument("--prefill-steps", type=int, default=0,
@@ -1036,11 +1091,31 @@ def main():
     ap.add_argument("--no-prefill", action="store_true",
                     help="moe_decode only: skip the prefill half of the metric")
     args = ap.parse_args()
+    # The decode steps are tens of microseconds of GPU work each, launched
+    # from a Python loop: a long warmup lets the launches build a lead over
+    # the GPU, so the timed steps measure the device, not Python's jitter
+    # (same kernel times; 20 warmup steps read ~7% lower step rates).
+    dflt = {"moe_decode": (2000, 500), "moe_decode_router": (2000, 500),
+            "dense_gemv": (2000, 500), "bf16_gemv": (2000, 500),
+            "prefill_zipf": (5, 2), "prefill_stack": (5, 2),
+            "library_gemm": (10, 3)}
+    d_steps, d_warm = dflt.get(args.workload, (200, 20))
+    if args.steps is None:
+        args.steps = d_steps
+    if args.warmup is None:
+        args.warmup = d_warm
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
               "(the sharding design is described in DESIGN.md); run --gpus 1",
               file=sys.stderr)
         sys.exit(2)
+    if args.workload == "library_gemm":
+        # torch brings its own HIP runtime: this workload runs before (and
+        # without) this build's library, so only one runtime owns the device
+        r = bench_library_gemm(args.steps, args.warmup)
+        print(json.dumps(line_of("hipBLASLt BF16 GEMM TFLOP/s (library reference on "
+                                 "the prefill shapes)", r, None, args.steps, args.warmup)))
+        return
     pkg, rt = load_pkg()
     lib = pkg.load()
     err = ctypes.create_string_buffer(256)
