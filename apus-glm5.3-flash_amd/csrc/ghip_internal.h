@@ -97,9 +97,11 @@ hipError_t ghip_launch_moe_router(const uint16_t *x, const uint16_t *gate_w,
 #define PF_HDR_NTILES 0
 #define PF_HDR_NPAIRS 1
 #define PF_HDR_ERR 2
-#define PF_HDR_WORDS 4
+#define PF_HDR_Q 16           /* 2 x 8 item-queue counters (GEMM, XCD) */
+#define PF_HDR_WORDS 32
 typedef struct {
-    uint32_t *hdr;        /* PF_HDR_WORDS u32: tiles, kept pairs, error */
+    uint32_t *hdr;        /* PF_HDR_WORDS u32: tiles, kept pairs, error,
+                             the GEMMs' per-XCD item counters; zeroed per call */
     uint32_t *cnt;        /* [chunks, n_experts] histograms -> offsets */
     uint32_t *tiles;      /* [max_tiles] x {expert, row0, rows, 0} */
     int32_t *eid;         /* [pairs] expert of a kept pair, else -1 */

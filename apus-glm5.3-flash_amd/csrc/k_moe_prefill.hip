@@ -541,31 +541,77 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
  *         out = H [P, inter] (sorted rows), SwiGLU epilogue.
  * MODE 1: act = H [P, inter] (sorted rows); out = O [P, dim] (sorted rows),
  *         bf16 expert outputs.
- * Grid: G (multiple of 8) >= tiles * nblk; 256 threads. The body is chosen
- * once per tile: 8, 4, 2 or 1 row blocks (the smallest that holds the
- * tile), or the exact-decode body for an expert with NaN codes. */
+ * Grid: G (multiple of 8) workgroups of NW * 64 threads, one per CU. The
+ * body is chosen once per tile: 8, 4, 2 or 1 row blocks (the smallest that
+ * holds the tile), or the exact-decode body for an expert with NaN codes.
+ *
+ * Items (tile, column block) are grouped by XCD: XCD x owns tiles x, x + 8,
+ * ... and its workgroups share each tile's column blocks, so a tile's
+ * gathered activation rows are read into one L2. With NW = 8 (routings
+ * that fill tiles: items of one size) an XCD's workgroups take its items
+ * round-robin. With NW = 4 (sparse routings: tiles of 1 to 256 rows, items
+ * of very different cost) they take them from the XCD's queue, a counter
+ * in hdr that every grab bumps, and, once it is empty, from the other XCDs'
+ * queues in turn: no workgroup idles while another still holds a backlog.
+ * A grab past a queue's end moves on to the next queue, so every workgroup
+ * leaves the loop after at most one failed grab per queue. */
 template <int MODE, int NW>
 __global__ __launch_bounds__(NW * 64, 1) void k_pf_gemm(
     GhipBank bank, const uint16_t *__restrict__ act,
     const int32_t *__restrict__ perm, const uint4 *__restrict__ tiles,
-    const uint32_t *__restrict__ hdr, uint32_t nblk, uint32_t topk,
+    uint32_t *__restrict__ hdr, uint32_t nblk, uint32_t topk,
     float limit, uint16_t *__restrict__ out) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t pf_lds[];
     /* persistent: one workgroup per CU; workgroup b runs on XCD b % 8 and
      * that XCD takes tiles x, x+8, ...; its workgroups share each tile's
      * column blocks (same activation rows, one L2) */
+    __shared__ uint32_t s_item;
     const uint32_t ntiles = hdr[PF_HDR_NTILES];
     const uint32_t x = blockIdx.x & 7u, c = blockIdx.x >> 3, per = gridDim.x >> 3;
     const uint32_t ntx = ntiles > x ? (ntiles - x + 7) >> 3 : 0;
     const uint32_t items = ntx * nblk;
     const uint32_t K = MODE == 0 ? bank.dim : bank.inter;
     const uint32_t nkb = K >> 7;
-    /* the next item's tile record is loaded while this item runs */
-    uint4 tdn = c < items ? tiles[x + 8 * (c / nblk)] : make_uint4(0u, 0u, 0u, 0u);
-    for (uint32_t k = c; k < items; k += per) {
-        const uint32_t nb = k % nblk;
-        const uint4 td = tdn;
-        if (k + per < items) tdn = tiles[x + 8 * ((k + per) / nblk)];
+    constexpr bool DYN = NW == 4;
+    constexpr uint32_t NONE = 0xffffffffu;
+    /* dynamic items: thread 0 grabs (queue y, index i) and publishes the
+     * tile index * nblk + column block in s_item (NONE when every queue is
+     * empty); yq = queues found empty so far (thread 0 only) */
+    uint32_t *qc = hdr + PF_HDR_Q + 8u * MODE;
+    uint32_t yq = 0;
+    auto grab = [&]() -> uint32_t {
+        while (yq < 8u) {
+            const uint32_t y = (x + yq) & 7u;
+            const uint32_t ny = ntiles > y ? (ntiles - y + 7) >> 3 : 0;
+            const uint32_t i = __hip_atomic_fetch_add(qc + y, 1u, __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT);
+            if (i < ny * nblk) return (y + 8u * (i / nblk)) * nblk + i % nblk;
+            yq++;
+        }
+        return NONE;
+    };
+    if constexpr (DYN) {
+        if (threadIdx.x == 0) s_item = grab();
+        __syncthreads();
+    }
+    /* static items: the next item's tile record is loaded while this item
+     * runs */
+    uint4 tdn = make_uint4(0u, 0u, 0u, 0u);
+    if (!DYN && c < items) tdn = tiles[x + 8 * (c / nblk)];
+    for (uint32_t k = c;; k += per) {
+        uint32_t nb;
+        uint4 td;
+        if constexpr (DYN) {
+            const uint32_t it = __builtin_amdgcn_readfirstlane(s_item);
+            if (it == NONE) break;
+            nb = it % nblk;
+            td = tiles[it / nblk];
+        } else {
+            if (k >= items) break;
+            nb = k % nblk;
+            td = tdn;
+            if (k + per < items) tdn = tiles[x + 8 * ((k + per) / nblk)];
+        }
         const uint32_t e = td.x;
         PfTile t;
         t.act = act;
@@ -603,8 +649,13 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pf_gemm(
         else if (nrb > 2) pf_tile<MODE, 4, false, NW>(t, pf_lds, sct);
         else if (nrb > 1) pf_tile<MODE, 2, false, NW>(t, pf_lds, sct);
         else              pf_tile<MODE, 1, false, NW>(t, pf_lds, sct);
+        if constexpr (DYN) {
+            /* every wave has read s_item (the body holds barriers) */
+            if (threadIdx.x == 0) s_item = grab();
+            __builtin_amdgcn_s_waitcnt(0xc07f);  /* lgkmcnt(0): s_item written */
+        }
         /* every wave is done with the LDS ring before the next item's
-         * prologue refills it */
+         * prologue refills it (and, dynamic, s_item is published) */
         __builtin_amdgcn_s_barrier();
     }
     /* the last tile's trailing refills land before the workgroup's LDS is
