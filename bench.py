@@ -781,9 +781,9 @@ def cpu_store_load(lib, n_experts=8, budget_s=8.0):
 # --------------------------------------------------------------------------
 
 PREFILL = {
-    "prefill_zipf": dict(layers=1, T=2048, zipf=1.1, seed=0xC3,
+    "prefill_zipf": dict(layers=1, T=2048, zipf=1.1, seed=0xC3, steps=40, warmup=5,
                          desc="BASELINE config 3: 288 experts, T=2048, Zipf(1.1) top-8"),
-    "prefill_stack": dict(layers=16, T=8192, zipf=0.0, seed=0xC4,
+    "prefill_stack": dict(layers=16, T=8192, zipf=0.0, seed=0xC4, steps=5, warmup=2,
                           desc="BASELINE config 4: 16 layers x 288 experts, "
                                "T=8192 per layer, uniform top-8"),
 }
@@ -1035,7 +1035,8 @@ def run_workload(name, lib, pkg, rt, args, cpu_leg):
                 cpu_store_load(lib) if cpu_leg else None)
     if name in PREFILL:
         steps = args.prefill_steps if args.prefill_steps else args.steps
-        r = bench_prefill(lib, pkg, rt, steps, min(args.warmup, 2), name)
+        r = bench_prefill(lib, pkg, rt, steps, min(args.warmup, PREFILL[name]["warmup"]),
+                          name)
         return ("prefill grouped-GEMM TFLOP/s", r,
                 cpu_moe_prefill(lib, PREFILL[name]["layers"], PREFILL[name]["T"])
                 if cpu_leg else None)
@@ -1097,7 +1098,7 @@ def main():
     # (same kernel times; 20 warmup steps read ~7% lower step rates).
     dflt = {"moe_decode": (2000, 500), "moe_decode_router": (2000, 500),
             "dense_gemv": (2000, 500), "bf16_gemv": (2000, 500),
-            "prefill_zipf": (5, 2), "prefill_stack": (5, 2),
+            "prefill_zipf": (40, 5), "prefill_stack": (5, 2),
             "library_gemm": (10, 3)}
     d_steps, d_warm = dflt.get(args.workload, (200, 20))
     if args.steps is None:
@@ -1128,15 +1129,17 @@ def main():
     if args.workload == "moe_decode" and not args.no_prefill:
         # the metric's second half ("...; prefill grouped-GEMM
         # TFLOP/s (%MFMA)"): configs 4 and 3, each a full step of its own
-        if not args.prefill_steps:
-            args.prefill_steps = 5
+        # per config: 5 steps of config 4 (16 layers, ~60 ms each), 40 of
+        # config 3 (one layer, ~2 ms each)
+        fixed = args.prefill_steps
         line["prefill"] = []
         for name in ("prefill_stack", "prefill_zipf"):
+            args.prefill_steps = fixed or PREFILL[name]["steps"]
             m2, r2, _ = run_workload(name, lib, pkg, rt, args, False)
             c2 = (cpu_moe_prefill(lib, PREFILL[name]["layers"], PREFILL[name]["T"], cpu)
                   if cpu else None)
             line["prefill"].append(line_of(m2, r2, c2, args.prefill_steps,
-                                           min(args.warmup, 2)))
+                                           min(args.warmup, PREFILL[name]["warmup"])))
             print("bench: %s done (%.4f ms/step)" % (name, r2["ms_per_step"]),
                   file=sys.stderr, flush=True)
     print(json.dumps(line))
