@@ -145,6 +145,12 @@ static int ghip_init(void) {
     G.pf.n_cu = G.n_cu;
     G.pf_inited = 1;
     HIPCHK(hipMalloc((void **)&G.d_flag, 256));
+    {
+        /* word 0: the per-call NaN-scan flag; word 1: a constant 1 (the
+         * exact-decode flag of exact = 1), written synchronously here */
+        const uint32_t w01[2] = {0u, 1u};
+        HIPCHK(hipMemcpy(G.d_flag, w01, sizeof w01, hipMemcpyHostToDevice));
+    }
     HIPCHK(hipMalloc((void **)&G.d_flags, GHIP_SCAN_SLOTS * sizeof(uint32_t)));
     HIPCHK(hipMemset(G.d_flags, 0, GHIP_SCAN_SLOTS * sizeof(uint32_t)));
     G.device = dev;
@@ -433,17 +439,9 @@ static int hook_fp8blk_linear(const uint8_t *codes, const float *scales,
 
 static const uint32_t *exact_flag_dev(const uint8_t *codes, size_t n,
                                       int exact, hipStream_t st, int *rc) {
-    static const uint32_t *one = NULL;
     *rc = 0;
     if (exact == 0) return NULL;
-    if (exact > 0) {
-        if (!one) {
-            uint32_t *p = G.d_flag + 1;
-            if (ghip_launch_fill_u32(p, 1, 1u, st) != hipSuccess) { *rc = 1; return NULL; }
-            one = p;
-        }
-        return one;
-    }
+    if (exact > 0) return G.d_flag + 1;        /* set to 1 once, at init */
     if (ghip_launch_fill_u32(G.d_flag, 1, 0u, st) != hipSuccess
         || ghip_launch_nan_scan(codes, n, G.d_flag, st) != hipSuccess) {
         *rc = 1;
@@ -748,7 +746,7 @@ int apus_ghip_store_load_container(ApusGhipStore *s, const char *dir, int layer,
         return 1;
     }
     for (int i = 0; i < n; i++)
-        if (recs[i].expert >= s->n_experts) {
+        if (recs[i].expert < 0 || recs[i].expert >= s->n_experts) {
             ghip_seterr("store_load_container: record (layers.%d, %d) past the store's %d "
                         "experts", layer, recs[i].expert, s->n_experts);
             if (err && errcap) snprintf(err, errcap, "%s", g_err);
@@ -1080,8 +1078,9 @@ int apus_ghip_moe_prefill_reserve(const ApusGhipStore *s, size_t tokens,
     const size_t P = tokens * (size_t)topk;
     if (P == 0) return 0;
     const uint32_t E = (uint32_t)s->n_experts;
+    _Static_assert(PF_HDR_Q + 16 <= PF_HDR_WORDS, "prefill header holds the queues");
     const size_t need[8] = {
-        16 * sizeof(uint32_t),
+        PF_HDR_WORDS * sizeof(uint32_t),
         ghip_moe_prefill_chunks(P) * E * sizeof(uint32_t),
         ghip_moe_prefill_max_tiles(P, E) * 4 * sizeof(uint32_t),
         P * sizeof(int32_t), P * sizeof(int32_t), P * sizeof(int32_t),

@@ -21,6 +21,11 @@
 #include "backend_hip.h"
 #include "ghip_internal.h"
 
+/* v is a non-negative integer <= max (JSON numbers are read as doubles) */
+static int jn_index(double v, double max) {
+    return v >= 0.0 && v <= max && v == (double)(uint64_t)v;
+}
+
 /* ---- a small JSON reader --------------------------------------------- */
 
 typedef enum { JN_NULL, JN_BOOL, JN_NUM, JN_STR, JN_ARR, JN_OBJ } JKind;
@@ -265,7 +270,12 @@ int ghip_container_layer(const char *dir, int layer, size_t slab_bytes,
         int l = -1;
         if (!blk || blk->kind != JN_STR || sscanf(blk->str, "layers.%d", &l) != 1 || !ex
             || ex->kind != JN_NUM || !sh || sh->kind != JN_STR || !off || off->kind != JN_NUM
-            || !nb || nb->kind != JN_NUM || ex->num < 0 || off->num < 0) {
+            || !nb || nb->kind != JN_NUM || !jn_index(ex->num, (double)INT32_MAX)
+            || !jn_index(off->num, 9007199254740992.0)
+            || !jn_index(nb->num, 9007199254740992.0)) {
+            /* the expert id must be an int (c/gcache.h:911-913 parses it as a
+             * long and bounds it); offsets and sizes integral and exact in a
+             * double */
             cerr(err, errcap, "container: bad slab record %zu", i);
             rc = 1;
             break;

@@ -635,10 +635,11 @@ __device__ __forceinline__ void rt_sigmoid_select(Logit lg, const float *__restr
 
 /* The whole router in one launch: workgroup b's waves compute gate logits
  * 4b..4b+3 and store them with agent-scope (device-coherent) stores; each
- * workgroup waits for its stores, then bumps a counter; the workgroup that
- * arrives last resets the counter and selects from the logits (read with
- * agent-scope loads, so logits written on other XCDs are seen), with no
- * second launch and no fences. The counter starts at 0 and every launch
+ * workgroup waits for its stores, then bumps a counter with an agent-scope
+ * release; the workgroup that arrives last takes an agent-scope acquire,
+ * resets the counter and selects from the logits (read with agent-scope
+ * loads, so logits written on other XCDs are seen), with no second
+ * launch. The counter starts at 0 and every launch
  * leaves it at 0; launches that overlap on one device race. */
 __global__ __launch_bounds__(256) void k_router(const uint16_t *__restrict__ gate_w,
                                                 const uint16_t *__restrict__ x, uint32_t E,
@@ -658,11 +659,14 @@ __global__ __launch_bounds__(256) void k_router(const uint16_t *__restrict__ gat
     }
     GHIP_VMCNT(0);                                /* own logit stores complete */
     __syncthreads();
+    /* the arrival is a release (this workgroup's logit stores happen
+     * before it); the last workgroup acquires before reading the logits */
     if (tid == 0)
-        last = __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+        last = __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT)
                == gridDim.x - 1;
     __syncthreads();
     if (!last || tid >= 64) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     if (tid == 0) __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     auto lg = [&](uint32_t i) {
         return __uint_as_float(__hip_atomic_load((const uint32_t *)logits_ws + i,

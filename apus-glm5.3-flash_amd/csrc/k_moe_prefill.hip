@@ -389,14 +389,16 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
 #pragma unroll
         for (int i = 0; i < 16; i++) { a0[rb][i] = 0.0f; a1[rb][i] = 0.0f; }
 
-    /* prologue: NS - 1 buffers in flight (a tile shorter than the ring
-     * fills the spare buffers with copies of its last stage, so every wait
-     * count below is one constant), then stage 0's step-0 operands; stage
-     * j's steps load stage j + NS - 1 into the buffer freed by stage j - 1 */
+    /* prologue: up to NS - 1 stages in flight, then stage 0's step-0
+     * operands; stage j's steps load stage j + NS - 1 (while it exists)
+     * into the buffer freed by stage j - 1. No load is issued past the
+     * tile's last stage, so none is left in flight when the tile ends: the
+     * next item (possibly another body with another LDS layout) starts on
+     * a quiet ring. */
 #pragma unroll
     for (uint32_t i = 0; i + 1 < NS; i++)
-        issue(i < nst ? i : nst - 1, i);      /* i >= nst: an unused buffer */
-    GHIP_VMCNT(LPS * (NS - 2));
+        if (i < nst) issue(i, i);
+    ghip_wait_stages<LPS, NS - 2>(nst - 1);
     __builtin_amdgcn_s_waitcnt(0xc07f);          /* lgkmcnt(0): scale table */
     __builtin_amdgcn_s_barrier();
     ghip_u32x4 q0[2], q1[2];
@@ -418,26 +420,21 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
     }
 
     /* one stage; NEXT: stage j+1 exists (its barrier, the refill of the
-     * freed buffer and its step-0 reads run in step 3). Branch-free inside,
+     * freed buffer and its step-0 reads run in step 3); REFILL: stage
+     * j + NS - 1 exists and is loaded during this one. Branch-free inside,
      * so each step is one scheduling region in which the next operands' LDS
-     * reads and dequant interleave with the MFMAs. Past the last stage the
-     * refill re-reads stage nst-1 (L2-hot) into the freed buffer, which no
-     * later stage of the tile reads: the wait counts stay uniform and the
-     * loop needs no second variant. */
-    auto stage = [&](uint32_t j, auto next_c) {
+     * reads and dequant interleave with the MFMAs. */
+    auto stage = [&](uint32_t j, auto next_c, auto refill_c) {
         constexpr bool NEXT = decltype(next_c)::value;
+        constexpr bool REFILL = decltype(refill_c)::value;
         const uint8_t *st = lds + (j % NS) * STG;
-        /* the stage loaded during this one (a copy of the last stage past
-         * the end: its buffer, freed by stage j - 1, is read by no later
-         * stage of the tile) */
-        const uint32_t ld = j + NS - 1 < nst ? j + NS - 1 : nst - 1;
-        const uint32_t lb = j + NS - 1;
+        const uint32_t ld = j + NS - 1;
 #pragma unroll
         for (int s = 0; s < 4; s++) {
-            if (s == 0) issue_part(std::integral_constant<int, 0>{}, ld, lb);
-            if (s == 1) issue_part(std::integral_constant<int, 1>{}, ld, lb);
-            if (s == 2) issue_part(std::integral_constant<int, 2>{}, ld, lb);
-            if (s == 3) issue_part(std::integral_constant<int, 3>{}, ld, lb);
+            if (REFILL && s == 0) issue_part(std::integral_constant<int, 0>{}, ld, ld);
+            if (REFILL && s == 1) issue_part(std::integral_constant<int, 1>{}, ld, ld);
+            if (REFILL && s == 2) issue_part(std::integral_constant<int, 2>{}, ld, ld);
+            if (REFILL && s == 3) issue_part(std::integral_constant<int, 3>{}, ld, ld);
             if (s < 3) {
                 /* step s+1 of this stage: A rows from LDS, B codes already
                  * in registers */
@@ -452,9 +449,10 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
                  * may stay in flight), own reads of stage j done; then a
                  * bare barrier (no fence: a fence would drain the DMA
                  * ring) after which buffer j % NS is free for stage j+NS.
-                 * NS + j stages' worth of loads are issued by now, in
-                 * order; stage j+1 is the (j+2)-th */
-                GHIP_VMCNT(LPS * (NS - 2));
+                 * Stages up to min(j + NS - 1, nst - 1) are issued by now,
+                 * in order: min(NS - 2, nst - 2 - j) of them after j+1 */
+                if (REFILL) GHIP_VMCNT(LPS * (NS - 2));
+                else ghip_wait_stages<LPS, NS - 2>(nst - 2 - j);
                 __builtin_amdgcn_s_waitcnt(0xc07f);
                 __builtin_amdgcn_s_barrier();
                 __builtin_amdgcn_sched_barrier(0);
@@ -507,8 +505,10 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
             b1 = nb1;
         }
     };
-    for (uint32_t j = 0; j + 1 < nst; j++) stage(j, std::true_type{});
-    stage(nst - 1, std::false_type{});
+    uint32_t j = 0;
+    for (; j + NS - 1 < nst; j++) stage(j, std::true_type{}, std::true_type{});
+    for (; j + 1 < nst; j++) stage(j, std::true_type{}, std::false_type{});
+    stage(nst - 1, std::false_type{}, std::false_type{});
 
     /* epilogue: lane (n, h), register i of row block rb holds output row
      * rb*32 + 8*(i/4) + 4*h + i%4, column n of each slot */
@@ -658,8 +658,9 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pf_gemm(
          * prologue refills it (and, dynamic, s_item is published) */
         __builtin_amdgcn_s_barrier();
     }
-    /* the last tile's trailing refills land before the workgroup's LDS is
-     * released */
+    /* each tile body waits for every load it issued (none past its last
+     * stage), so nothing is in flight here; kept as a guard before the
+     * workgroup's LDS is released */
     GHIP_VMCNT(0);
 }
 

@@ -38,7 +38,47 @@ PKG = os.path.join(ROOT, "apus-glm5.3-flash_amd")
 HBM_PEAK_GBS = 8000.0            # MI355X HBM3E, AMD published
 BF16_PEAK_TFLOPS = 2500.0        # MI355X dense BF16 MFMA, AMD published
 HOST_LINK_PEAK_GBS = 64.0        # PCIe 5.0 x16, one direction (host -> MI355X)
-CPU_THREADS = 16                 # the GPU box's CPU share per GPU
+
+
+def _cpu_threads():
+    """Threads for the CPU baseline: the CPUs this process may run on,
+    capped at 16 (the GPU box's CPU share per GPU, whatever nproc shows)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+CPU_THREADS = _cpu_threads()
+
+
+def cpu_common(O, use_ref):
+    """cores (the threads the timed CPU path actually ran on: the reference
+    pool's count, which APUS_THREADS sets, c/pool.h:95-104) and the host
+    facts of cpu_info()."""
+    cores = O.ref().ref_pool_threads() if use_ref else CPU_THREADS
+    return {"cores": int(cores), **cpu_info()}
+
+
+def cpu_info():
+    """Host facts the CPU baseline is quoted with: model, nproc, the CPUs
+    this process may use and the threads the baseline used."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        aff = None
+    return {"cpu_model": model, "host_nproc": os.cpu_count(), "affinity_cpus": aff,
+            "threads": CPU_THREADS}
 
 
 def load_pkg():
@@ -218,7 +258,7 @@ def cpu_moe_decode(lib, budget_s=12.0):
     per_tok = t_tok / ntok
     return {
         "value": nbytes / per_tok / 1e9, "unit": "GB/s",
-        "cores": int(os.environ.get("APUS_THREADS", CPU_THREADS)),
+        **cpu_common(O, use_ref),
         "kind": "reference" if use_ref else "port",
         "sample": ("%d decode tokens x 8 experts on pre-dequantized BF16 payloads "
                    "(%.1f ms/token); dequant-on-fill of the 8 experts %.1f ms "
@@ -306,7 +346,7 @@ def cpu_dense_gemv(lib, M=1, budget_s=10.0):
         n += 1
     nbytes = N * K + sc.size * 4 + M * K * 2 + M * N * 2
     return {"value": nbytes / (t / n) / 1e9, "unit": "GB/s",
-            "cores": int(os.environ.get("APUS_THREADS", CPU_THREADS)),
+            **cpu_common(O, use_ref),
             "kind": "reference" if use_ref else "port",
             "sample": "%d calls of dequant_mt + gemm_mt (c/gdsa.h:532-533), "
                       "M=%d, %.1f ms/call" % (n, M, t / n * 1e3)}
@@ -418,7 +458,7 @@ def cpu_dense_gemm(lib, M=2048, budget_s=10.0):
         n += 1
     tflops = 2 * Ms * N * K / (t / n) / 1e12
     return {"value": tflops, "unit": "TFLOP/s",
-            "cores": int(os.environ.get("APUS_THREADS", CPU_THREADS)),
+            **cpu_common(O, use_ref),
             "kind": "reference" if use_ref else "port",
             "sample": "%d calls of dequant_mt + gemm_mt on q_b [16384, 1536], %d rows, "
                       "%.1f ms/call; %d rows of all four projections would take %.1f s"
@@ -501,7 +541,7 @@ def cpu_bf16_gemv(lib, M=1, budget_s=10.0):
         n += 1
     nbytes = N * K * 2 + M * K * 2 + M * N * 2
     return {"value": nbytes / (t / n) / 1e9, "unit": "GB/s",
-            "cores": int(os.environ.get("APUS_THREADS", CPU_THREADS)),
+            **cpu_common(O, use_ref),
             "kind": "reference" if use_ref else "port",
             "sample": "%d calls of bf16_gemm_mt on the LM head [%d, %d], M=%d, "
                       "%.1f ms/call" % (n, N, K, M, t / n * 1e3)}
@@ -770,7 +810,7 @@ def cpu_store_load(lib, n_experts=8, budget_s=8.0):
         finally:
             os.close(fd)
     return {"value": sb / (t / n) / 1e9, "unit": "GB/s",
-            "cores": int(os.environ.get("APUS_THREADS", CPU_THREADS)),
+            **cpu_common(O, use_ref),
             "kind": "reference" if use_ref else "port",
             "sample": "%d slab fills (pread + dequant-on-fill of the 3 members to BF16), "
                       "%.2f ms/slab" % (n, t / n * 1e3)}

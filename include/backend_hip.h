@@ -129,7 +129,12 @@ int apus_ghip_fp8blk_dequant(const uint8_t *codes, const float *scales,
 
 /* Device-pointer variants (asynchronous on `stream`, a hipStream_t; NULL =
  * the null stream). exact: 0 = fast decode (caller guarantees no 0x7F/0xFF
- * code), 1 = exact integer decode, -1 = scan the codes first and pick. */
+ * code), 1 = exact integer decode, -1 = scan the codes first and pick.
+ * These share process-wide device state: the NaN-scan flag (exact = -1),
+ * the exact-decode flag word and the split-K partial buffer of the GEMM
+ * path (M >= 16). Calls must therefore not overlap in time: issue them on
+ * one stream, and do not run them concurrently with the host-pointer
+ * entry points (which use the backend's own stream). */
 int apus_ghip_fp8blk_dequant_dev(const uint8_t *codes, const float *scales,
                                  uint16_t *out, size_t O, size_t K,
                                  int exact, void *stream);

@@ -141,9 +141,14 @@ def main():
     for i, (m, o, k) in enumerate(GEM_SHAPES):
         w = O.f32_to_bf16(rng.uniform(-2, 2, (o, k)).astype(np.float32))
         x = O.f32_to_bf16(rng.uniform(-2, 2, (m, k)).astype(np.float32))
+        # exact-value corners (/root/reference/tests/m3g/gen_golden.py:138-143):
+        # +0, -0, the smallest bf16 subnormal, and an activation of 1.0
         w.reshape(-1)[0] = 0x0000
         if w.size > 1:
             w.reshape(-1)[1] = 0x8000
+        if w.size > 4:
+            w.reshape(-1)[2] = 0x0001
+        x.reshape(-1)[0] = 0x3F80
         fx[f"gem{i}_w"], fx[f"gem{i}_x"] = w, x
         fx[f"gem{i}_y"] = ref_gemm(w, x)
         man["gemm"].append({"M": m, "O": o, "K": k})

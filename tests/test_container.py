@@ -84,3 +84,18 @@ def test_string_escapes_and_unicode(lib, tmp_path):
     rc, shard, off, err = lookup(lib, d, 3, 2, 64)
     assert rc == 0, err
     assert shard == "apus-A.safetensors"
+
+
+@pytest.mark.parametrize("bad", [4294967296, 2147483648, -1, 1.5, 1e300])
+def test_rejects_expert_id_out_of_int_range(lib, tmp_path, bad):
+    """An expert id that does not fit an int (or is not an integer) is a bad
+    record: cast to int it would wrap negative and index far outside the
+    store (the reference bounds the parsed long, c/gcache.h:911-913)."""
+    d = str(tmp_path)
+    write_container(d, {3: {0: np.zeros(64, np.uint8), 1: np.zeros(64, np.uint8)}}, 64)
+    p = os.path.join(d, "apus.index.json")
+    idx = json.load(open(p))
+    idx["expert_slabs"][1]["expert"] = bad
+    json.dump(idx, open(p, "w"))
+    rc, _, _, err = lookup(lib, d, 3, 0, 64)
+    assert rc == 1 and "bad slab record 1" in err

@@ -235,3 +235,53 @@ def test_hooks_floor_failsoft_and_regions(ghip):
                  "registered")
     ghip.apus_ghip_unregister_region(O.ptr(codes))
     ghip.apus_ghip_unregister_region(O.ptr(scales))
+
+
+def test_fp8_hook_through_table_floors(ghip):
+    """The fp8blk_linear hook called through the table, the analog of
+    tests/m7b/test_gkernels.c:283-324 for the FP8 site (c/gdsa.h:529-531):
+    with APUS_GHIP_FP8_MIN_KB above the weight size, or APUS_GHIP_MAX_M below
+    M, the hook declines (nonzero: the engine runs its CPU kernel) and the
+    offload counter does not move; the direct entry ignores the floors;
+    without floors the hook runs, moves offload_fp8blk by one, and meets
+    the tolerance. Both the GEMV (M = 1) and GEMM (M = 32) paths."""
+    hooks = (ctypes.c_void_p * 2).in_dll(ghip, "apus_ghip_hooks")
+    HookFp8 = ctypes.CFUNCTYPE(ctypes.c_int, *([ctypes.c_void_p] * 4 + [ctypes.c_size_t] * 3))
+    rng = np.random.default_rng(0xF8)
+    N, K = 512, 2048
+    codes = rng.integers(0, 254, (N, K), dtype=np.uint8)
+    codes[codes >= 0x7F] += 1
+    scales = np.exp2(rng.uniform(-10, -6, (N // 128, K // 128))).astype(np.float32)
+    env = {"APUS_GHIP_FP8_MIN_KB": str(N * K // 1024 + 1), "APUS_GHIP_MAX_M": "8"}
+    try:
+        for name, val in env.items():
+            os.environ[name] = val
+            ghip.apus_ghip_disable()
+            assert hooks[1] is None
+            assert ghip.apus_ghip_enable(ctypes.create_string_buffer(256), 256) == 0
+            hook = HookFp8(hooks[1])
+            M = 1 if name == "APUS_GHIP_FP8_MIN_KB" else 32
+            x = O.f32_to_bf16(rng.standard_normal((M, K)).astype(np.float32))
+            y = np.full((M, N), 0xABCD, np.uint16)
+            before = ghip.apus_ghip_offload_fp8blk()
+            assert hook(O.ptr(codes), O.ptr(scales), O.ptr(x), O.ptr(y), M, N, K) != 0, name
+            assert ghip.apus_ghip_offload_fp8blk() == before, name
+            assert np.all(y == 0xABCD), "a declining hook must not write y (%s)" % name
+            y2 = gpu_linear(ghip, codes, scales, x)         # direct: no floors
+            assert_close(y2, O.fp8_linear(codes, scales, x, threads=8),
+                         floor_linear(codes, scales, x), "direct under " + name)
+            del os.environ[name]
+    finally:
+        for name in env:
+            os.environ.pop(name, None)
+        ghip.apus_ghip_disable()
+        assert ghip.apus_ghip_enable(ctypes.create_string_buffer(256), 256) == 0
+    hook = HookFp8(hooks[1])
+    for M in (1, 32):
+        x = O.f32_to_bf16(rng.standard_normal((M, K)).astype(np.float32))
+        y = np.empty((M, N), np.uint16)
+        before = ghip.apus_ghip_offload_fp8blk()
+        assert hook(O.ptr(codes), O.ptr(scales), O.ptr(x), O.ptr(y), M, N, K) == 0
+        assert ghip.apus_ghip_offload_fp8blk() == before + 1
+        assert_close(y, O.fp8_linear(codes, scales, x, threads=8),
+                     floor_linear(codes, scales, x), "hooked fp8 M=%d" % M)

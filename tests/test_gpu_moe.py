@@ -12,7 +12,7 @@ import pytest
 
 import oracle as O
 import gpu_util as G
-from tolerance import assert_close, assert_close_combined
+from tolerance import assert_close, assert_close_combined, record
 
 pytestmark = pytest.mark.gpu
 GOLD = os.path.join(os.path.dirname(__file__), "golden")
@@ -253,9 +253,11 @@ def test_config2_golden(ghip, pkg):
         st = assert_close_combined(G.host(dout, np.uint16, (dim,)), fx["cfg2_out"], fl,
                           "config2 device routing")
         print("config2", st)
+        record("config2_golden_device_routing", st)
         out = np.empty(dim, np.uint16)
         assert ghip.apus_ghip_moe_decode(s, O.ptr(x), O.ptr(idx), O.ptr(w), k,
                                          O.ptr(out)) == 0
-        assert_close_combined(out, fx["cfg2_out"], fl, "config2 host routing")
+        st = assert_close_combined(out, fx["cfg2_out"], fl, "config2 host routing")
+        record("config2_golden_host_routing", st)
     finally:
         ghip.apus_ghip_store_close(s)

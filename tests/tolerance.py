@@ -92,3 +92,19 @@ def assert_close_combined(got, ref, floor, what=""):
     assert st["frac_le1ulp_scaled"] >= ULP_FRAC_MIN and st["max_rel"] <= REL_MAX, \
         "%s: %s" % (what, st)
     return st
+
+
+def record(name, stats, **extra):
+    """Append one parity record (the raw comparison statistics of a GPU test)
+    as a JSON line to the file named by $APUS_PARITY_RECORD, when set; the
+    runs that produce the committed record set it."""
+    import json
+    import os
+    path = os.environ.get("APUS_PARITY_RECORD")
+    if not path:
+        return
+    row = {"test": name}
+    row.update({k: v for k, v in stats.items()})
+    row.update(extra)
+    with open(path, "a") as f:
+        f.write(json.dumps(row) + "\n")
