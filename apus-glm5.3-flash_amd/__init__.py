@@ -77,6 +77,7 @@ SIGNATURES = {
     "apus_ghip_moe_prefill_dev": (c_int, [c_vp, c_vp, c_size, c_vp, c_vp,
                                           c_int, c_vp, c_vp]),
     "apus_ghip_set_trace_events": (None, [ctypes.POINTER(c_vp), c_int]),
+    "apus_ghip_stream_hold": (c_int, [c_vp, ctypes.c_uint32]),
     # include/apus_synth.h
     "apus_synth_mix64": (c_u64, [c_u64]),
     "apus_synth_key": (c_u64, [c_u64, c_u64]),

@@ -465,6 +465,22 @@ int apus_ghip_fp8blk_linear_dev(const uint8_t *codes, const float *scales,
     return 0;
 }
 
+int apus_ghip_stream_hold(void *stream, uint32_t us) {
+    if (ghip_init()) return 1;
+    if (us > 1000000u) {
+        ghip_seterr("stream_hold: %u us is above the 1 s limit", us);
+        return 1;
+    }
+    int khz = 0;
+    HIPCHK(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, G.device));
+    if (khz <= 0) {
+        ghip_seterr("stream_hold: no wall-clock rate");
+        return 1;
+    }
+    HIPCHK(ghip_launch_hold((uint64_t)us * (uint64_t)khz / 1000u, (hipStream_t)stream));
+    return 0;
+}
+
 void apus_ghip_set_trace_events(void *const *events, int n) {
     G.trace_n = 0;
     if (!events || n <= 0) return;

@@ -159,6 +159,10 @@ int ghip_container_layer(const char *dir, int layer, size_t slab_bytes,
 hipError_t ghip_launch_fill_u32(uint32_t *p, size_t n, uint32_t value,
                                 hipStream_t st);
 
+/* Hold stream st for `ticks` wall-clock ticks (hipDeviceAttributeWallClockRate
+ * kHz): one wave that waits and exits, touching no memory. */
+hipError_t ghip_launch_hold(uint64_t ticks, hipStream_t st);
+
 /* Device fill of synthetic FP8 codes (same bytes as apus_synth_fp8_codes). */
 hipError_t ghip_launch_synth_codes(uint8_t *out, size_t n, uint64_t key,
                                    uint64_t offset, hipStream_t st);

@@ -90,3 +90,16 @@ extern "C" hipError_t ghip_launch_fill_u32(uint32_t *p, size_t n, uint32_t value
     hipLaunchKernelGGL(k_fill_u32, dim3(sy_grid(n)), dim3(256), 0, st, p, n, value);
     return hipGetLastError();
 }
+
+/* One wave that waits `ticks` of the constant-rate wall clock and exits:
+ * holds a stream for a fixed time with no memory traffic (a bounded wait:
+ * every launch ends). */
+__global__ __launch_bounds__(64) void k_hold(unsigned long long ticks) {
+    const unsigned long long t0 = (unsigned long long)wall_clock64();
+    while ((unsigned long long)wall_clock64() - t0 < ticks) __builtin_amdgcn_s_sleep(64);
+}
+
+extern "C" hipError_t ghip_launch_hold(uint64_t ticks, hipStream_t st) {
+    hipLaunchKernelGGL(k_hold, dim3(1), dim3(64), 0, st, (unsigned long long)ticks);
+    return hipGetLastError();
+}

@@ -31,6 +31,7 @@ def hip():
             "hipMemcpy": [vp, vp, sz, ctypes.c_int],
             "hipMemcpyAsync": [vp, vp, sz, ctypes.c_int, vp],
             "hipMemset": [vp, ctypes.c_int, sz],
+            "hipMemsetAsync": [vp, ctypes.c_int, sz, vp],
             "hipDeviceSynchronize": [],
             "hipStreamCreate": [ctypes.POINTER(vp)],
             "hipStreamDestroy": [vp],

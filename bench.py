@@ -8,8 +8,16 @@ bf16 combine). Inputs rotate over R tokens/routings so every step streams
 8 experts' weights from HBM. value = algorithmic bytes per step (8 expert
 slabs + x + out + logits = 201,393,280 B) / measured time, in GB/s.
 
---workload dense_gemv runs config 1 (W [16384,4096] FP8, M in {1,2,4}) over
-rotating weight copies (>= 3x the 256 MB MALL). --workload dense_gemm runs
+The default run also carries, in the same line, the dense GEMV configs
+("dense": config 0, W [2048,4096], and config 1, W [16384,4096], at
+M = 1, 2, 4, over rotating weight copies >= 3x the 256 MB MALL) and the
+prefill half of the metric ("prefill": configs 4 and 3). Every object has
+its roofline, its CPU leg, the step against both rooflines and the
+weight-only GB/s of the reference benches.
+
+--workload dense_gemv / dense_gemv_c0 run config 1 / 0 alone (--m for M);
+timed regions start after a lead of unrelated device work, so they measure
+back-to-back device steps, not Python's launch rate. --workload dense_gemm runs
 the four DSA FP8 projections at M = 2048 prefill rows (the fp8blk_linear
 hook's MFMA GEMM path), in TFLOP/s. --workload bf16_gemv runs the LM head
 through the bf16_gemm hook; --workload moe_decode_router runs config 2 routed
@@ -105,6 +113,36 @@ def traffic_from_profiles(kernel):
     return v.get("hbm_bytes_per_launch") if isinstance(v, dict) else None
 
 
+_LIB = None
+
+
+def lead(st, us=2000):
+    """Hold st for `us` microseconds just before the timed region's start
+    event (apus_ghip_stream_hold: one wave waiting on the wall clock, no
+    memory traffic), so Python has enqueued the timed steps before the
+    device reaches them: the timed span is then the device's back-to-back
+    step time, not the host's launch rate (steps of a few to tens of
+    microseconds)."""
+    rc = _LIB.apus_ghip_stream_hold(st.vp, us)
+    if rc:
+        raise RuntimeError("apus_ghip_stream_hold: %s" % _LIB.apus_ghip_last_error())
+
+
+def timed(rt, st, step, first, steps):
+    """Events around exactly `steps` steps enqueued back to back on st
+    (after a synchronize and a lead, see lead()); ms per step."""
+    st.synchronize()
+    rt.synchronize()
+    lead(st, min(20000, max(2000, 15 * steps)))
+    e0, e1 = rt.Event(), rt.Event()
+    e0.record(st)
+    for i in range(steps):
+        step(first + i)
+    e1.record(st)
+    e1.synchronize()
+    return e0.elapsed_ms(e1) / steps
+
+
 def kernel_times(lib, rt, step, first, steps, n_ev, pairs):
     """Average duration (ms) of chosen launches, from start/stop HIP events
     carried by the launches' own dispatch packets on the launch stream
@@ -171,17 +209,9 @@ def bench_moe_decode(lib, pkg, rt, steps, warmup, rotate=64):
 
     for i in range(warmup):
         step(i)
-    st.synchronize()
-    rt.synchronize()
-    e0, e1 = rt.Event(), rt.Event()
     t0 = time.perf_counter()
-    e0.record(st)
-    for i in range(steps):
-        step(warmup + i)
-    e1.record(st)
-    e1.synchronize()
+    ms = timed(rt, st, step, warmup, steps)
     wall = time.perf_counter() - t0
-    ms = e0.elapsed_ms(e1) / steps
     kt = kernel_times(lib, rt, step, warmup + steps, steps, 4,
                       {"k_moe_gateup": (0, 1), "k_moe_down": (2, 3)})
     nbytes, flops, gu_bytes = moe_algorithmic_bytes(E, k, dim, inter)
@@ -193,6 +223,7 @@ def bench_moe_decode(lib, pkg, rt, steps, warmup, rotate=64):
             "launch_ms": {n: round(v, 5) for n, v in kt.items()}}
     return {
         "ms_per_step": ms, "value": gbs, "wall_s": wall,
+        "weight_bytes": k * 3 * inter * dim,
         "bytes": nbytes, "flops": flops, **kern,
         "config": {"workload": "moe_decode (BASELINE config 2)", "experts": E,
                    "topk": k, "dim": dim, "inter": inter, "tokens": 1,
@@ -272,8 +303,16 @@ def cpu_moe_decode(lib, budget_s=12.0):
 # config 1: dense FP8 GEMV at M = 1, 2, 4
 # --------------------------------------------------------------------------
 
-def bench_dense_gemv(lib, pkg, rt, steps, warmup, M=1, copies=12):
-    N, K, seed = 16384, 4096, 0xC1
+DENSE = {0: dict(N=2048, K=4096, seed=0xC0, copies=92),
+         1: dict(N=16384, K=4096, seed=0xC1, copies=12)}
+
+
+def bench_dense_gemv(lib, pkg, rt, steps, warmup, M=1, cfg=1):
+    """BASELINE config 0 (W [2048, 4096]) or 1 (W [16384, 4096]) at M rows:
+    one apus_ghip_fp8blk_linear_dev call per step, rotating over weight
+    copies that together span >= 3x the 256 MB MALL (92 x 8.4 MB, 12 x 67
+    MB), so every step reads its weights from HBM."""
+    N, K, seed, copies = (DENSE[cfg][k] for k in ("N", "K", "seed", "copies"))
     nsb = (N // 128) * (K // 128)
     codes = rt.DevBuf(copies * N * K)
     for c in range(copies):
@@ -301,31 +340,30 @@ def bench_dense_gemv(lib, pkg, rt, steps, warmup, M=1, copies=12):
 
     for i in range(warmup):
         step(i)
-    st.synchronize()
-    e0, e1 = rt.Event(), rt.Event()
-    e0.record(st)
-    for i in range(steps):
-        step(warmup + i)
-    e1.record(st)
-    e1.synchronize()
-    ms = e0.elapsed_ms(e1) / steps
+    ms = timed(rt, st, step, warmup, steps)
     kt = kernel_times(lib, rt, step, warmup + steps, steps, 2,
                       {"k_fp8_gemv": (0, 1)})
     nbytes = N * K + nsb * 4 + M * K * 2 + M * N * 2
     return {"ms_per_step": ms, "value": nbytes / (ms * 1e-3) / 1e9,
+            "weight_bytes": N * K, "traffic_key": "k_fp8_gemv@config%d_M%d" % (cfg, M),
             "bytes": nbytes, "flops": 2 * M * N * K, "kernel": "k_fp8_gemv",
             "kernel_ms": kt["k_fp8_gemv"], "kernel_bytes": nbytes,
             "kernel_flops": 2 * M * N * K,
             "launch_ms": {n: round(v, 5) for n, v in kt.items()},
-            "config": {"workload": "dense_gemv (BASELINE config 1)", "N": N, "K": K,
+            "config": {"workload": "dense_gemv%s (BASELINE config %d)"
+                                   % ("_c0" if cfg == 0 else "", cfg), "N": N, "K": K,
                        "M": M, "weight_copies": copies}}
 
 
-def cpu_dense_gemv(lib, M=1, budget_s=10.0):
+def cpu_dense_gemv(lib, M=1, cfg=1, budget_s=10.0):
+    """The reference's FP8 linear on the CPU (dequant_mt + gemm_mt,
+    c/gdsa.h:532-533) on the config's inputs; also the BF16-only GEMV on
+    pre-dequantized weights (the MoE decode path, c/gmoe.h:215-226) and the
+    scalar anchor on one thread (c/fp8blk.h:115-136 + c/bf16.h:202-217)."""
     os.environ.setdefault("APUS_THREADS", str(CPU_THREADS))
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
-    N, K, seed = 16384, 4096, 0xC1
+    N, K, seed = (DENSE[cfg][k] for k in ("N", "K", "seed"))
     P = O.ptr
     codes = np.empty((N, K), np.uint8)
     lib.apus_synth_fp8_codes(P(codes), codes.size, seed, 10, 0)
@@ -345,11 +383,49 @@ def cpu_dense_gemv(lib, M=1, budget_s=10.0):
         t += time.perf_counter() - t0
         n += 1
     nbytes = N * K + sc.size * 4 + M * K * 2 + M * N * 2
-    return {"value": nbytes / (t / n) / 1e9, "unit": "GB/s",
+    extra = {}
+    if use_ref:
+        wb = np.empty((N, K), np.uint16)
+        O.ref().ref_fp8blk_dequant_mt(P(codes), P(sc), P(wb), N, K)
+        n2, t2 = 0, 0.0
+        while t2 < budget_s / 4 and n2 < 2000:
+            t0 = time.perf_counter()
+            O.ref().ref_bf16_gemm_mt(P(wb), P(x), P(y), M, N, K)
+            t2 += time.perf_counter() - t0
+            n2 += 1
+        extra["bf16_gemv_only"] = {
+            "value": (N * K * 2 + M * K * 2 + M * N * 2) / (t2 / n2) / 1e9, "unit": "GB/s",
+            "sample": "%d calls of apus_bf16_gemm_mt on pre-dequantized BF16 weights "
+                      "(%.2f ms/call)" % (n2, t2 / n2 * 1e3)}
+        extra["scalar_anchor"] = scalar_anchor(O, codes, sc, x)
+    return {"value": nbytes / (t / n) / 1e9, "unit": "GB/s", **extra,
             **cpu_common(O, use_ref),
             "kind": "reference" if use_ref else "port",
             "sample": "%d calls of dequant_mt + gemm_mt (c/gdsa.h:532-533), "
                       "M=%d, %.1f ms/call" % (n, M, t / n * 1e3)}
+
+
+def scalar_anchor(O, codes, sc, x):
+    """The reference's scalar anchors on ONE thread (apus_fp8blk_dequant_scalar
+    then apus_bf16_gemm_scalar, c/fp8blk.h:115-136, c/bf16.h:202-217) on a
+    bounded slice of the weight rows (<= 512), reported per FP8 weight byte
+    (GB/s of the slice's algorithmic bytes)."""
+    P = O.ptr
+    N, K = codes.shape
+    M = x.shape[0]
+    rows = min(N, 512)
+    c = np.ascontiguousarray(codes[:rows])
+    s = np.ascontiguousarray(sc[:(rows + 127) // 128])
+    wb = np.empty((rows, K), np.uint16)
+    y = np.empty((M, rows), np.uint16)
+    t0 = time.perf_counter()
+    O.ref().ref_fp8blk_dequant_scalar(P(c), P(s), P(wb), rows, K)
+    O.ref().ref_bf16_gemm_scalar(P(wb), P(x), P(y), M, rows, K)
+    t = time.perf_counter() - t0
+    nbytes = rows * K + s.size * 4 + M * K * 2 + M * rows * 2
+    return {"value": nbytes / t / 1e9, "unit": "GB/s", "threads": 1,
+            "sample": "scalar dequant + scalar GEMM on %d of %d weight rows, M=%d "
+                      "(%.1f ms)" % (rows, N, M, t * 1e3)}
 
 
 # --------------------------------------------------------------------------
@@ -391,14 +467,7 @@ def bench_dense_gemm(lib, pkg, rt, steps, warmup, M=2048):
 
     for i in range(warmup):
         step(i)
-    st.synchronize()
-    e0, e1 = rt.Event(), rt.Event()
-    e0.record(st)
-    for i in range(steps):
-        step(warmup + i)
-    e1.record(st)
-    e1.synchronize()
-    ms = e0.elapsed_ms(e1) / steps
+    ms = timed(rt, st, step, warmup, steps)
     # per-launch times of each projection (dispatch-packet events)
     per = {}
     for (nm, N, K, codes, d_s, x, y) in mats:
@@ -417,6 +486,7 @@ def bench_dense_gemm(lib, pkg, rt, steps, warmup, M=2048):
     No, Ko = DSA_SHAPES[3][1], DSA_SHAPES[3][2]
     return {
         "ms_per_step": ms, "value": flops / (ms * 1e-3) / 1e12, "unit": "TFLOP/s",
+        "weight_bytes": sum(N * K for (_n, N, K) in DSA_SHAPES),
         "bytes": nbytes, "flops": flops, "kernel": "k_fp8_gemm",
         "kernel_ms": per["o_proj"], "kernel_flops": 2 * M * No * Ko,
         "kernel_bytes": No * Ko + (No // 128) * (Ko // 128) * 4 + M * Ko * 2 + M * No * 2,
@@ -495,18 +565,12 @@ def bench_bf16_gemv(lib, pkg, rt, steps, warmup, M=1, copies=2):
 
     for i in range(warmup):
         step(i)
-    st.synchronize()
-    e0, e1 = rt.Event(), rt.Event()
-    e0.record(st)
-    for i in range(steps):
-        step(warmup + i)
-    e1.record(st)
-    e1.synchronize()
-    ms = e0.elapsed_ms(e1) / steps
+    ms = timed(rt, st, step, warmup, steps)
     kname = "k_fp8_gemv_stream<%d, 2, true>" % min(M, 4)
     kt = kernel_times(lib, rt, step, warmup + steps, steps, 2, {kname: (0, 1)})
     nbytes = N * K * 2 + M * K * 2 + M * N * 2
     return {"ms_per_step": ms, "value": nbytes / (ms * 1e-3) / 1e9,
+            "weight_bytes": N * K * 2,
             "bytes": nbytes, "flops": 2 * M * N * K, "kernel": kname,
             "kernel_ms": kt[kname], "kernel_bytes": nbytes,
             "kernel_flops": 2 * M * N * K, "traffic_key": "k_bf16_gemv@lm_head",
@@ -599,15 +663,11 @@ def bench_moe_decode_router(lib, pkg, rt, steps, warmup, rotate=64):
     for i in range(warmup):
         router(i)
         decode(i)
-    st.synchronize()
-    e0, e1 = rt.Event(), rt.Event()
-    e0.record(st)
-    for i in range(steps):
-        router(warmup + i)
-        decode(warmup + i)
-    e1.record(st)
-    e1.synchronize()
-    ms = e0.elapsed_ms(e1) / steps
+    def both(i):
+        router(i)
+        decode(i)
+
+    ms = timed(rt, st, both, warmup, steps)
     # per-launch times: the router and the two decode launches, each with
     # its own dispatch-packet events
     n = steps
@@ -628,6 +688,7 @@ def bench_moe_decode_router(lib, pkg, rt, steps, warmup, rotate=64):
     nbytes = full - E * 4 + E * dim * 2 + E * 4         # gate_w + bias, no logits
     return {
         "ms_per_step": ms, "value": nbytes / (ms * 1e-3) / 1e9,
+        "weight_bytes": k * 3 * inter * dim + E * dim * 2,
         "bytes": nbytes, "flops": 2 * k * 3 * inter * dim + 2 * E * dim,
         "kernel": "k_moe_gateup", "kernel_ms": t_gu, "kernel_bytes": gu_bytes - E * 4,
         "kernel_flops": 2 * k * 2 * inter * dim, "traffic_key": "k_moe_gateup@given_routing",
@@ -746,6 +807,7 @@ def bench_store_load(lib, pkg, rt, steps, warmup, n_experts=64):
     ms = sum(times) / len(times) * 1e3
     nbytes = n_experts * sb
     return {"ms_per_step": ms, "value": nbytes / (ms * 1e-3) / 1e9,
+            "weight_bytes": nbytes,
             "bytes": nbytes, "flops": 0, "kernel": "store_load_container",
             "kernel_ms": ms, "kernel_bytes": nbytes, "kernel_flops": 0,
             "launch_ms": {"store_load_container": round(ms, 4)},
@@ -872,14 +934,7 @@ def bench_prefill(lib, pkg, rt, steps, warmup, name):
 
     for i in range(warmup):
         step(i)
-    st.synchronize()
-    e0, e1 = rt.Event(), rt.Event()
-    e0.record(st)
-    for i in range(steps):
-        step(warmup + i)
-    e1.record(st)
-    e1.synchronize()
-    ms = e0.elapsed_ms(e1) / steps
+    ms = timed(rt, st, step, warmup, steps)
     # per-launch timing: 8 dispatch-packet events per layer call
     evs = [[rt.Event() for _ in range(8)] for _ in range(L * steps)]
     arr_t = ctypes.c_void_p * 8
@@ -909,9 +964,13 @@ def bench_prefill(lib, pkg, rt, steps, warmup, name):
     gu_bytes = sum(touched) // L * gu_member + P * dim * 2 + P * inter * 2
     return {
         "ms_per_step": ms, "value": flops / (ms * 1e-3) / 1e12, "unit": "TFLOP/s",
+        "weight_bytes": sum(touched) * 3 * inter * dim,
         "bytes": nbytes, "flops": flops, "kernel": "k_pf_gemm_gateup",
         "kernel_ms": kt["k_pf_gemm_gateup"], "kernel_flops": gu_flops,
         "kernel_bytes": gu_bytes, "traffic_key": "k_pf_gemm_gateup@" + name,
+        # config 3 moves ~113 FLOP per HBM byte, below the ~315 FLOP/B ridge:
+        # HBM-bound (config 4, ~447 FLOP/B, is MFMA-bound)
+        "bound": "hbm" if cfg["zipf"] > 0 else "mfma",
         "launch_ms": {n_: round(v, 5) for n_, v in kt.items()},
         "hbm_gbs": nbytes / (ms * 1e-3) / 1e9,
         "config": {"workload": "%s (%s)" % (name, cfg["desc"]), "layers": L,
@@ -924,20 +983,110 @@ def bench_prefill(lib, pkg, rt, steps, warmup, name):
     }
 
 
-def cpu_moe_prefill(lib, L, T, decode_cpu=None):
+def _cpu_prefill_expert(O, P, use_ref, item, idx, x, dim, inter, eo, out, acc):
+    """Dequant-on-fill of one expert (timed into acc["deq"]), then its calls
+    for every sample token routed to it (timed into acc["exp"])."""
+    e, members = item
+    mats = []
+    for (c, sc) in members:
+        o, kk = c.shape
+        pl = np.empty((o, kk), np.uint16)
+        t0 = time.perf_counter()
+        if use_ref:
+            O.ref().ref_fp8blk_dequant_mt(P(c), P(sc), P(pl), o, kk)
+        else:
+            O.lib().apo_fp8blk_dequant_mt(P(c), P(sc), P(pl), o, kk, CPU_THREADS)
+        acc["deq"] += time.perf_counter() - t0
+        mats.append(pl)
+    g, u, d = mats
+    for t in np.nonzero((idx == e).any(1))[0]:
+        t0 = time.perf_counter()
+        if use_ref:
+            O.ref().ref_gmoe_expert(P(g), P(u), P(d), P(x[t]), dim, inter, MOE["limit"],
+                                    P(out))
+        else:
+            out[:] = O.swiglu_expert(g, u, d, x[t], threads=CPU_THREADS)[0]
+        acc["exp"] += time.perf_counter() - t0
+        eo[(int(t), e)] = out.copy()
+
+
+def cpu_moe_prefill(lib, name, ntok=128):
     """The reference has no grouped GEMM: its prefill is the per-token loop
-    (c/gmoe.h:278-320), 8 experts per token on BF16 payloads -- the same
-    per-token work as a decode step. Timed on a bounded token sample (or
-    taken from the decode leg's timing of that same loop) and reported as
-    TFLOP/s (50,331,648 FLOP per (token, expert))."""
-    r = decode_cpu if decode_cpu is not None else cpu_moe_decode(lib)
-    tflops = 8 * 50_331_648 / (r["ms_per_token"] * 1e-3) / 1e12
-    r = dict(r)
-    r["value"], r["unit"] = tflops, "TFLOP/s"
-    r["sample"] = (r["sample"] + "; the reference prefill runs this loop once per "
-                   "token, so %d x %d tokens would take %.1f s"
-                   % (L, T, L * T * r["ms_per_token"] * 1e-3))
-    return r
+    (c/gmoe.h:278-320), each token's selected experts (apus_gmoe_expert on
+    BF16 payloads, c/gmoe.h:210-227) then the ascending-expert bf16-per-add
+    combine (c/gmoe.h:307-320). Timed on a real sample: the first `ntok`
+    tokens of the config's first layer with their own routing and inputs
+    (the bench's generator streams). The expert calls run expert by expert
+    (each expert's payload is dequantized once, then called for each sample
+    token routed to it -- the same calls the per-token loop makes); the
+    dequant-on-fill is timed apart and not in value. value = TFLOP/s of the
+    sample (50,331,648 FLOP per (token, expert)); the full config is
+    extrapolated linearly from it."""
+    os.environ.setdefault("APUS_THREADS", str(CPU_THREADS))
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    P = O.ptr
+    cfg = PREFILL[name]
+    E, k, dim, inter, seed = 288, 8, 4096, 2048, cfg["seed"]
+    T = cfg["T"]
+    use_ref = O.ref_available()
+    idx = np.empty((T, k), np.int32)
+    w = np.empty((T, k), np.float32)
+    lib.apus_synth_route(P(idx), P(w), T, E, k, cfg["zipf"], seed)
+    idx, w = idx[:ntok].copy(), w[:ntok].copy()
+    x = np.empty((ntok, dim), np.uint16)
+    lib.apus_synth_bf16_normal(P(x), x.size, seed, 40, 0)
+    eo = {}
+    out = np.empty(dim, np.uint16)
+    shapes = [(inter, dim), (inter, dim), (dim, inter)]
+
+    def gen(e):
+        """expert e's FP8 members (untimed; the generator is not the reference)"""
+        mm = []
+        for j, (o, kk) in enumerate(shapes):
+            c = np.empty((o, kk), np.uint8)
+            lib.apus_synth_fp8_codes(P(c), c.size, seed,
+                                     lib.apus_synth_expert_stream(0, e, 2 * j), 0)
+            sc = np.empty((O.nblocks(o), O.nblocks(kk)), np.float32)
+            lib.apus_synth_scales(P(sc), sc.size, seed,
+                                  lib.apus_synth_expert_stream(0, e, 2 * j + 1), 1e-4, 1e-2)
+            mm.append((c, sc))
+        return mm
+
+    from concurrent.futures import ThreadPoolExecutor
+    experts = sorted(set(idx.ravel().tolist()))
+    batches = [experts[i:i + CPU_THREADS] for i in range(0, len(experts), CPU_THREADS)]
+    # generation runs in parallel between the timed parts, never beside them
+    acc = {"deq": 0.0, "exp": 0.0}
+    with ThreadPoolExecutor(CPU_THREADS) as ex:
+        for b in batches:
+            for e, members in zip(b, list(ex.map(gen, b))):
+                _cpu_prefill_expert(O, P, use_ref, (e, members), idx, x, dim, inter, eo,
+                                    out, acc)
+    t_deq, t_exp = acc["deq"], acc["exp"]
+    t0 = time.perf_counter()
+    for t in range(ntok):
+        y = np.zeros(dim, np.float32)
+        seen = set()
+        for e, wt in sorted(zip(idx[t].tolist(), w[t].tolist())):
+            if e in seen:
+                continue
+            seen.add(e)
+            c = O.bf16_to_f32(O.f32_to_bf16(O.bf16_to_f32(eo[(t, e)]) * np.float32(wt)))
+            y = O.bf16_to_f32(O.f32_to_bf16(y + c))
+    t_comb = time.perf_counter() - t0
+    pairs = len(eo)
+    tsec = t_exp + t_comb
+    full_pairs = cfg["layers"] * T * k
+    return {"value": pairs * 50_331_648 / tsec / 1e12, "unit": "TFLOP/s", **cpu_common(O, use_ref),
+            "kind": "reference" if use_ref else "port",
+            "sample": ("the first %d tokens of layer 0 with their own routing (%d (token, "
+                       "expert) pairs over %d distinct experts): expert calls %.2f s + "
+                       "combine %.3f s; dequant-on-fill of those experts %.2f s, not in "
+                       "value; the full config (%d pairs) extrapolates linearly to %.0f s"
+                       % (ntok, pairs, len(set(idx.ravel().tolist())), t_exp, t_comb, t_deq,
+                          full_pairs, tsec * full_pairs / pairs)),
+            "dequant_fill_s": t_deq}
 
 
 # --------------------------------------------------------------------------
@@ -1020,9 +1169,22 @@ def bench_library_gemm(steps, warmup):
 
 # --------------------------------------------------------------------------
 
+def mfma_busy_from_profiles(key):
+    """MFMA-busy fraction of a kernel measured with rocprofv3 --pmc
+    (SQ_VALU_MFMA_BUSY_CYCLES over SQ_BUSY_CYCLES x CUs, committed under
+    profiles/mfma_busy.json); None when not measured."""
+    path = os.path.join(ROOT, "profiles", "mfma_busy.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        v = json.load(f).get(key)
+    return v.get("mfma_busy_frac") if isinstance(v, dict) else None
+
+
 def roofline_of(r):
-    traffic = traffic_from_profiles(r.get("traffic_key", r["kernel"]))
-    mfma = r.get("unit") == "TFLOP/s"
+    key = r.get("traffic_key", r["kernel"])
+    traffic = traffic_from_profiles(key)
+    mfma = r.get("unit") == "TFLOP/s" and r.get("bound", "mfma") == "mfma"
     if mfma:
         achieved = r["kernel_flops"] / (r["kernel_ms"] * 1e-3) / 1e12
     else:
@@ -1044,6 +1206,9 @@ def roofline_of(r):
         "avg_launch_ms": round(r["kernel_ms"], 6),
         "launch_ms": r["launch_ms"],
         "mfma_tflops": round(r["kernel_flops"] / (r["kernel_ms"] * 1e-3) / 1e12, 3),
+        "mfma_frac": round(r["kernel_flops"] / (r["kernel_ms"] * 1e-3) / 1e12
+                           / BF16_PEAK_TFLOPS, 4),
+        "mfma_busy_frac_rocprof": mfma_busy_from_profiles(key),
     }
 
 
@@ -1053,10 +1218,11 @@ def run_workload(name, lib, pkg, rt, args, cpu_leg):
         r = bench_moe_decode(lib, pkg, rt, args.steps, args.warmup)
         return ("FP8 MoE decode GEMV HBM GB/s", r,
                 cpu_moe_decode(lib) if cpu_leg else None)
-    if name == "dense_gemv":
-        r = bench_dense_gemv(lib, pkg, rt, args.steps, args.warmup, M=args.m)
+    if name in ("dense_gemv", "dense_gemv_c0"):
+        cfg = 0 if name == "dense_gemv_c0" else 1
+        r = bench_dense_gemv(lib, pkg, rt, args.steps, args.warmup, M=args.m, cfg=cfg)
         return ("FP8 dense decode GEMV HBM GB/s", r,
-                cpu_dense_gemv(lib, M=args.m) if cpu_leg else None)
+                cpu_dense_gemv(lib, M=args.m, cfg=cfg) if cpu_leg else None)
     if name == "dense_gemm":
         r = bench_dense_gemm(lib, pkg, rt, args.steps, args.warmup)
         return ("FP8 dense linear GEMM TFLOP/s (DSA projections, prefill M)", r,
@@ -1078,8 +1244,7 @@ def run_workload(name, lib, pkg, rt, args, cpu_leg):
         r = bench_prefill(lib, pkg, rt, steps, min(args.warmup, PREFILL[name]["warmup"]),
                           name)
         return ("prefill grouped-GEMM TFLOP/s", r,
-                cpu_moe_prefill(lib, PREFILL[name]["layers"], PREFILL[name]["T"])
-                if cpu_leg else None)
+                cpu_moe_prefill(lib, name) if cpu_leg else None)
     r = bench_copy(rt, args.steps, args.warmup)
     return ("device copy HBM GB/s (read + write)", r, None)
 
@@ -1106,6 +1271,23 @@ def line_of(metric, r, cpu, steps, warmup):
         line["hbm"] = {"achieved": round(r["hbm_gbs"], 2), "peak": HBM_PEAK_GBS,
                        "unit": "GB/s", "frac": round(r["hbm_gbs"] / HBM_PEAK_GBS, 4),
                        "algorithmic_bytes_per_step": r["bytes"]}
+    if r.get("flops") and r.get("bytes"):
+        # the step against both rooflines: its time at the binding one
+        # (HBM bytes at 8 TB/s or FLOPs at 2.5 PFLOP/s) over the measured time
+        t_hbm = r["bytes"] / (HBM_PEAK_GBS * 1e9) * 1e3
+        t_mfma = r["flops"] / (BF16_PEAK_TFLOPS * 1e12) * 1e3
+        line["step_roofline"] = {
+            "bound": "hbm" if t_hbm >= t_mfma else "mfma",
+            "min_ms": round(max(t_hbm, t_mfma), 6),
+            "frac": round(max(t_hbm, t_mfma) / r["ms_per_step"], 4),
+            "hbm_frac": round(t_hbm / r["ms_per_step"], 4),
+            "mfma_frac": round(t_mfma / r["ms_per_step"], 4)}
+    if r.get("weight_bytes"):
+        # the reference benches' accounting: weight bytes only (BF16 O*K*2,
+        # tests/m3g/bench_bf16.c:122; FP8 O*K, tests/m7b/bench_gmetal.c:97-99)
+        line["weight_only"] = {"bytes_per_step": r["weight_bytes"],
+                               "gbs": round(r["weight_bytes"] / (r["ms_per_step"] * 1e-3)
+                                            / 1e9, 2)}
     return line
 
 
@@ -1119,7 +1301,8 @@ def main():
                     help="untimed warmup steps (default per workload: 500 for "
                          "the decode GEMVs, 2 for prefill, 20 otherwise)")
     ap.add_argument("--workload", default="moe_decode",
-                    choices=["moe_decode", "dense_gemv", "dense_gemm", "bf16_gemv",
+                    choices=["moe_decode", "dense_gemv", "dense_gemv_c0", "dense_gemm",
+                             "bf16_gemv",
                              "moe_decode_router", "store_load", "prefill_zipf",
                              "prefill_stack", "copy", "library_gemm"])
     ap.add_argument("--m", type=int, default=1,
@@ -1131,13 +1314,16 @@ def main():
                     help="skip the CPU baseline leg")
     ap.add_argument("--no-prefill", action="store_true",
                     help="moe_decode only: skip the prefill half of the metric")
+    ap.add_argument("--no-dense", action="store_true",
+                    help="moe_decode only: skip the config 0/1 dense GEMV objects")
     args = ap.parse_args()
     # The decode steps are tens of microseconds of GPU work each, launched
     # from a Python loop: a long warmup lets the launches build a lead over
     # the GPU, so the timed steps measure the device, not Python's jitter
     # (same kernel times; 20 warmup steps read ~7% lower step rates).
     dflt = {"moe_decode": (2000, 500), "moe_decode_router": (2000, 500),
-            "dense_gemv": (2000, 500), "bf16_gemv": (2000, 500),
+            "dense_gemv": (2000, 500), "dense_gemv_c0": (2000, 500),
+            "bf16_gemv": (2000, 500),
             "prefill_zipf": (40, 5), "prefill_stack": (5, 2),
             "library_gemm": (10, 3)}
     d_steps, d_warm = dflt.get(args.workload, (200, 20))
@@ -1157,8 +1343,10 @@ def main():
         print(json.dumps(line_of("hipBLASLt BF16 GEMM TFLOP/s (library reference on "
                                  "the prefill shapes)", r, None, args.steps, args.warmup)))
         return
+    global _LIB
     pkg, rt = load_pkg()
     lib = pkg.load()
+    _LIB = lib
     err = ctypes.create_string_buffer(256)
     pkg.check(lib.apus_ghip_enable(err, 256), "apus_ghip_enable")
 
@@ -1166,6 +1354,18 @@ def main():
     print("bench: %s done (%.4f ms/step)" % (args.workload, r["ms_per_step"]),
           file=sys.stderr, flush=True)
     line = line_of(metric, r, cpu, args.steps, args.warmup)
+    if args.workload == "moe_decode" and not args.no_dense:
+        # the metric's GEMV half at the dense configs (BASELINE configs 0 and
+        # 1, M = 1, 2, 4), each its own object with roofline and CPU leg.
+        # Steps of a few microseconds: at least 200 timed steps each.
+        line["dense"] = []
+        ds, dw = max(args.steps, 200), max(args.warmup, 20)
+        for cfg, M in ((0, 1), (1, 1), (1, 2), (1, 4)):
+            r2 = bench_dense_gemv(lib, pkg, rt, ds, dw, M=M, cfg=cfg)
+            c2 = cpu_dense_gemv(lib, M=M, cfg=cfg, budget_s=3.0) if cpu else None
+            line["dense"].append(line_of("FP8 dense decode GEMV HBM GB/s", r2, c2, ds, dw))
+            print("bench: config %d M=%d done (%.4f ms/step)" % (cfg, M, r2["ms_per_step"]),
+                  file=sys.stderr, flush=True)
     if args.workload == "moe_decode" and not args.no_prefill:
         # the metric's second half ("...; prefill grouped-GEMM
         # TFLOP/s (%MFMA)"): configs 4 and 3, each a full step of its own
@@ -1176,8 +1376,7 @@ def main():
         for name in ("prefill_stack", "prefill_zipf"):
             args.prefill_steps = fixed or PREFILL[name]["steps"]
             m2, r2, _ = run_workload(name, lib, pkg, rt, args, False)
-            c2 = (cpu_moe_prefill(lib, PREFILL[name]["layers"], PREFILL[name]["T"], cpu)
-                  if cpu else None)
+            c2 = cpu_moe_prefill(lib, name) if cpu else None
             line["prefill"].append(line_of(m2, r2, c2, args.prefill_steps,
                                            min(args.warmup, PREFILL[name]["warmup"])))
             print("bench: %s done (%.4f ms/step)" % (name, r2["ms_per_step"]),

@@ -273,6 +273,12 @@ int apus_ghip_moe_prefill_dev(ApusGhipStore *s, const uint16_t *x, size_t T,
  * thread-safe; the events must outlive their use. */
 void apus_ghip_set_trace_events(void *const *events, int n);
 
+/* Hold `stream` for `us` microseconds (<= 1 s) with one wave that waits on
+ * the wall clock and touches no memory; asynchronous. A benchmark enqueues
+ * it before a timed region's start event so the host has queued the timed
+ * steps before the device reaches them. No reference counterpart. 0 = ok. */
+int apus_ghip_stream_hold(void *stream, uint32_t us);
+
 #ifdef __cplusplus
 }
 #endif
