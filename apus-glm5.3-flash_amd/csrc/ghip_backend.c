@@ -144,6 +144,9 @@ static int ghip_init(void) {
     HIPCHK(ghip_moe_prefill_init());
     G.pf.n_cu = G.n_cu;
     G.pf_inited = 1;
+    /* the allocation-free prefill's scratch: its device address, taken once
+     * here with the device current */
+    HIPCHK(ghip_pf_scratch_init(dev));
     HIPCHK(hipMalloc((void **)&G.d_flag, 256));
     {
         /* word 0: the per-call NaN-scan flag; word 1: a constant 1 (the
@@ -1142,6 +1145,54 @@ int apus_ghip_moe_prefill_dev(ApusGhipStore *s, const uint16_t *x, size_t T,
                                            (hipStream_t)stream);
     if (e != hipSuccess) {
         ghip_seterr("moe_prefill launch: %s", hipGetErrorString(e));
+        return 1;
+    }
+    G.dispatches++;
+    return 0;
+}
+
+int apus_ghip_moe_prefill_dev_noalloc(ApusGhipStore *s, const uint16_t *x, size_t T,
+                                      const int32_t *idx, const float *w, int topk,
+                                      uint16_t *out, void *stream) {
+    /* no allocation and no init here: the store exists, so the library's
+     * init (device, kernel attributes, the scratch address) already ran */
+    if (!s || !G.inited) {
+        ghip_seterr("moe_prefill_noalloc: %s", s ? "library not initialised" : "no store");
+        return 1;
+    }
+    if (topk <= 0 || topk > GHIP_MAX_TOPK) {
+        ghip_seterr("moe_prefill_noalloc: topk %d outside 1..%d", topk, GHIP_MAX_TOPK);
+        return 1;
+    }
+    if (T == 0) return 0;
+    if (s->dim % 256 || s->inter % 128 || s->n_experts > 1024) {
+        ghip_seterr("moe_prefill_noalloc: needs dim %% 256 == 0, inter %% 128 == 0 and "
+                    "<= 1024 experts (dim=%zu inter=%zu E=%d)", s->dim, s->inter,
+                    s->n_experts);
+        return 1;
+    }
+    const size_t P = T * (size_t)topk;
+    const size_t need = ghip_pf_scratch_need(P, (uint32_t)s->n_experts, (uint32_t)s->dim,
+                                             (uint32_t)s->inter);
+    if (need > GHIP_PF_SCRATCH_BYTES) {
+        ghip_seterr("moe_prefill_noalloc: %zu tokens x top-%d need %zu bytes of workspace, "
+                    "above the fixed %zu-byte scratch (use apus_ghip_moe_prefill_dev)",
+                    T, topk, need, (size_t)GHIP_PF_SCRATCH_BYTES);
+        return 1;
+    }
+    GhipMoePrefillWs ws;
+    hipError_t e = ghip_pf_scratch_ws(G.device, P, (uint32_t)s->n_experts, (uint32_t)s->dim,
+                                      (uint32_t)s->inter, G.n_cu, &ws);
+    if (e != hipSuccess) {
+        ghip_seterr("moe_prefill_noalloc: scratch: %s", hipGetErrorString(e));
+        return 1;
+    }
+    GhipBank bk;
+    store_bank(s, &bk);
+    e = ghip_launch_moe_prefill(&bk, x, T, idx, w, topk, s->limit, out, &ws,
+                                G.trace_n >= 8 ? G.trace_ev : NULL, (hipStream_t)stream);
+    if (e != hipSuccess) {
+        ghip_seterr("moe_prefill_noalloc launch: %s", hipGetErrorString(e));
         return 1;
     }
     G.dispatches++;

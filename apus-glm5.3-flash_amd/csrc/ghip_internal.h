@@ -118,6 +118,20 @@ size_t ghip_moe_prefill_chunks(size_t pairs);
 /* Raise the GEMM kernels' dynamic-LDS limit (once per process). */
 hipError_t ghip_moe_prefill_init(void);
 
+/* Allocation-free prefill workspace: a fixed device array of
+ * GHIP_PF_SCRATCH_BYTES per GPU. ghip_pf_scratch_init (once per device, that
+ * device current) takes its device address; ghip_pf_scratch_need is the
+ * bytes a call needs; ghip_pf_scratch_ws carves the workspace of one call
+ * out of it (hipErrorOutOfMemory when it does not fit, hipErrorNotInitialized
+ * before init). */
+#define GHIP_PF_SCRATCH_BYTES ((size_t)32 << 20)
+#define GHIP_MAX_DEVICES 64
+hipError_t ghip_pf_scratch_init(int device);
+size_t ghip_pf_scratch_need(size_t pairs, uint32_t n_experts, uint32_t dim,
+                            uint32_t inter);
+hipError_t ghip_pf_scratch_ws(int device, size_t pairs, uint32_t n_experts, uint32_t dim,
+                              uint32_t inter, uint32_t n_cu, GhipMoePrefillWs *ws);
+
 /* K4: routed MoE prefill for T tokens: permutation, grouped gate/up GEMM
  * with the SwiGLU epilogue, grouped down GEMM, ordered combine (stream
  * ordered on st). x [T, dim], idx/w [T, topk], out [T, dim], all device.

@@ -1013,6 +1013,69 @@ extern "C" hipError_t ghip_launch_fp8_gemm(const uint8_t *codes, const float *sc
     return hipGetLastError();
 }
 
+/* ------------------------------------------------------------------------ */
+/* allocation-free prefill workspace                                        */
+/* ------------------------------------------------------------------------ */
+
+/* The workspace of apus_ghip_moe_prefill_dev_noalloc: a fixed device array
+ * (each GPU the library runs on holds its own copy until the process
+ * ends). Host code never passes `scratch` itself to a kernel (its name is a
+ * host-side stand-in there): ghip_pf_scratch_init takes its device address
+ * once per device, at the library's init, and every use goes through that
+ * address. Every call on a GPU shares the array; calls that overlap in time
+ * on one GPU race. */
+static __device__ __align__(256) uint8_t scratch[GHIP_PF_SCRATCH_BYTES];
+static void *g_scratch_dev[GHIP_MAX_DEVICES];
+
+extern "C" hipError_t ghip_pf_scratch_init(int device) {
+    if (device < 0 || device >= GHIP_MAX_DEVICES) return hipErrorInvalidDevice;
+    if (g_scratch_dev[device]) return hipSuccess;
+    void *p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
+    g_scratch_dev[device] = p;
+    return hipSuccess;
+}
+
+static size_t pf_up256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+extern "C" size_t ghip_pf_scratch_need(size_t pairs, uint32_t n_experts, uint32_t dim,
+                                       uint32_t inter) {
+    return pf_up256(PF_HDR_WORDS * sizeof(uint32_t))
+         + pf_up256(ghip_moe_prefill_chunks(pairs) * n_experts * sizeof(uint32_t))
+         + pf_up256(ghip_moe_prefill_max_tiles(pairs, n_experts) * 4 * sizeof(uint32_t))
+         + 3 * pf_up256(pairs * sizeof(int32_t))
+         + pf_up256(pairs * (size_t)inter * 2) + pf_up256(pairs * (size_t)dim * 2);
+}
+
+extern "C" hipError_t ghip_pf_scratch_ws(int device, size_t pairs, uint32_t n_experts,
+                                         uint32_t dim, uint32_t inter, uint32_t n_cu,
+                                         GhipMoePrefillWs *ws) {
+    if (device < 0 || device >= GHIP_MAX_DEVICES || !g_scratch_dev[device])
+        return hipErrorNotInitialized;
+    if (ghip_pf_scratch_need(pairs, n_experts, dim, inter) > GHIP_PF_SCRATCH_BYTES)
+        return hipErrorOutOfMemory;
+    uint8_t *b = (uint8_t *)g_scratch_dev[device];
+    size_t o = 0;
+    auto take = [&](size_t n) {
+        uint8_t *p = b + o;
+        o += pf_up256(n);
+        return (void *)p;
+    };
+    ws->hdr = (uint32_t *)take(PF_HDR_WORDS * sizeof(uint32_t));
+    ws->cnt = (uint32_t *)take(ghip_moe_prefill_chunks(pairs) * n_experts * sizeof(uint32_t));
+    ws->tiles = (uint32_t *)take(ghip_moe_prefill_max_tiles(pairs, n_experts) * 16);
+    ws->eid = (int32_t *)take(pairs * sizeof(int32_t));
+    ws->perm = (int32_t *)take(pairs * sizeof(int32_t));
+    ws->pos = (int32_t *)take(pairs * sizeof(int32_t));
+    ws->h = (uint16_t *)take(pairs * (size_t)inter * 2);
+    ws->o = (uint16_t *)take(pairs * (size_t)dim * 2);
+    ws->cap_pairs = pairs;
+    ws->n_cu = n_cu;
+    return hipSuccess;
+}
+
 extern "C" hipError_t ghip_moe_prefill_init(void) {
     const int lds = PF_LDS;
     const void *ks[5] = {(const void *)k_pf_gemm<0, 8>, (const void *)k_pf_gemm<0, 4>,

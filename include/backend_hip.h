@@ -258,6 +258,25 @@ int apus_ghip_moe_prefill_dev(ApusGhipStore *s, const uint16_t *x, size_t T,
                               const int32_t *idx, const float *w, int topk,
                               uint16_t *out, void *stream);
 
+/* Allocation-free variant of apus_ghip_moe_prefill_dev. No counterpart in
+ * the reference: it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Same arguments, kernels and results (bitwise) as
+ * apus_ghip_moe_prefill_dev, but the workspace (header and queue counters,
+ * tile list, pair permutation, the H and O pair rows) lives in a fixed
+ * 32 MiB device array of the library instead of the grow-on-demand
+ * workspace: it calls no hipMalloc / hipFree and no allocating library
+ * routine. The call's workspace must fit that array: at dim 4096, inter
+ * 2048, 288 experts that is T * topk <= ~2600 pairs (T <= ~320 tokens at
+ * top-8); larger calls return 1 with the needed size in
+ * apus_ghip_last_error. Needs the library initialised (apus_ghip_enable or
+ * apus_ghip_store_open first). Every call on a GPU shares that GPU's array
+ * (the per-call counters are cleared by each call's own fill kernel), so
+ * calls that overlap in time on one GPU race: order them on one stream. */
+int apus_ghip_moe_prefill_dev_noalloc(ApusGhipStore *s, const uint16_t *x, size_t T,
+                                      const int32_t *idx, const float *w, int topk,
+                                      uint16_t *out, void *stream);
+
 /* --- timing (no reference counterpart; for benchmarks and profilers).
  * events: n caller-created hipEvent_t handles, NULL/0 turns it off. While
  * set, launches carry start/stop events in their dispatch packets

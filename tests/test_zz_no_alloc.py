@@ -1,0 +1,74 @@
+"""The allocation-free prefill entry point (apus_ghip_moe_prefill_dev_noalloc)
+against the existing apus_ghip_moe_prefill_dev on the same inputs: bitwise
+equal outputs on two calls in a row (the second smaller, so the fixed
+workspace holds the first call's leftovers), one call past the fixed
+workspace rejected with a clear error, and a prefill through the regular
+entry point in between that leaves the no-alloc workspace to itself."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle as O
+import gpu_util as G
+from tolerance import assert_close_combined
+from test_gpu_moe import open_store, random_slabs
+from test_gpu_prefill import floor_of, skewed_routing
+
+pytestmark = pytest.mark.gpu
+
+
+def run(ghip, fn, s, x, idx, w):
+    T, k = idx.shape
+    dim = x.shape[1]
+    dx, di, dw, do = G.dev(x), G.dev(idx), G.dev(w), G.empty(T * dim * 2)
+    rc = fn(s, G.vp(dx), T, G.vp(di), G.vp(dw), k, G.vp(do), G.stream())
+    assert rc == 0, ghip.apus_ghip_last_error()
+    return G.host(do, np.uint16, (T, dim))
+
+
+def test_noalloc_prefill_matches_regular(ghip):
+    E, dim, inter = 12, 256, 256
+    rng = np.random.default_rng(0x0A)
+    slabs = random_slabs(E, dim, inter, rng, nan_codes_in=(4,))
+    s = open_store(ghip, E, dim, inter)
+    try:
+        for e, sl in enumerate(slabs):
+            assert ghip.apus_ghip_store_put(s, e, O.ptr(sl), sl.nbytes) == 0
+        cases = []
+        for T, k, hot in ((300, 6, 4), (37, 3, 1)):          # second call smaller
+            x = O.f32_to_bf16(rng.standard_normal((T, dim)).astype(np.float32))
+            idx, w = skewed_routing(rng, T, E, k, hot=hot)
+            cases.append((x, idx, w))
+        got = [run(ghip, ghip.apus_ghip_moe_prefill_dev_noalloc, s, *c) for c in cases]
+        ref = [run(ghip, ghip.apus_ghip_moe_prefill_dev, s, *c) for c in cases]
+        for (x, idx, w), g, r in zip(cases, got, ref):
+            assert np.array_equal(g, r), "T=%d: no-alloc differs from the regular entry" % len(x)
+        # and against the oracle (the tolerance of every prefill test)
+        x, idx, w = cases[1]
+        want, eo = O.moe_forward(slabs, dim, inter, x, idx, w, want_expert_out=True)
+        assert_close_combined(got[1], want, floor_of(eo, w, idx), "no-alloc vs oracle")
+        # repeat the first (larger) call after the smaller one: same bits
+        assert np.array_equal(run(ghip, ghip.apus_ghip_moe_prefill_dev_noalloc, s,
+                                  *cases[0]), ref[0])
+    finally:
+        ghip.apus_ghip_store_close(s)
+
+
+def test_noalloc_prefill_rejects_oversize(ghip):
+    """A call whose workspace exceeds the fixed array is refused before any
+    launch, with the needed size in the error."""
+    E, dim, inter = 8, 4096, 2048
+    s = open_store(ghip, E, dim, inter)
+    try:
+        T, k = 4096, 8                                 # 32768 pairs: ~400 MB
+        x = np.zeros((T, dim), np.uint16)
+        idx = np.tile(np.arange(k, dtype=np.int32), (T, 1))
+        w = np.full((T, k), 0.125, np.float32)
+        dx, di, dw, do = G.dev(x), G.dev(idx), G.dev(w), G.empty(T * dim * 2)
+        rc = ghip.apus_ghip_moe_prefill_dev_noalloc(s, G.vp(dx), T, G.vp(di), G.vp(dw), k,
+                                                    G.vp(do), G.stream())
+        assert rc != 0
+        assert b"fixed" in ghip.apus_ghip_last_error()
+    finally:
+        ghip.apus_ghip_store_close(s)
