@@ -54,6 +54,7 @@ typedef struct {
 static struct {
     int inited, enabled, device;
     uint32_t n_cu;               /* CU count rounded up to the 8 XCDs */
+    uint32_t n_cu_dev;           /* the device's CU count */
     hipStream_t stream;
     /* grow-only staging (device) */
     void *d_w, *d_s, *d_x, *d_y;
@@ -139,6 +140,7 @@ static int ghip_init(void) {
         return 1;
     }
     G.n_cu = (uint32_t)((ncu + 7) / 8 * 8);
+    G.n_cu_dev = (uint32_t)ncu;
     HIPCHK(ghip_moe_decode_init());
     HIPCHK(ghip_linear_init(G.n_cu));
     HIPCHK(ghip_moe_prefill_init());
@@ -582,12 +584,12 @@ int apus_ghip_store_open(ApusGhipStore **out, int n_experts, size_t dim,
     }
     int bad = hipMalloc((void **)&s->nan_flags, (size_t)n_experts * 4) != hipSuccess
            || hipMemset(s->nan_flags, 0, (size_t)n_experts * 4) != hipSuccess
-           || hipMalloc((void **)&s->ws.route, GHIP_MOE_ROUTE_WORDS * 4) != hipSuccess
-           || hipMemset(s->ws.route, 0, GHIP_MOE_ROUTE_WORDS * 4) != hipSuccess
+           || hipMalloc((void **)&s->ws.hw, GHIP_MAX_TOPK * inter * 4) != hipSuccess
+           || hipMemset(s->ws.hw, 0, GHIP_MAX_TOPK * inter * 4) != hipSuccess
+           || (s->ws.hw_inter = (uint32_t)inter) == 0
            || hipMalloc((void **)&s->ws.err, 4) != hipSuccess
            || hipMemset(s->ws.err, 0, 4) != hipSuccess
-           || (s->ws.n_cu = G.n_cu) == 0
-           || hipMalloc((void **)&s->ws.h, GHIP_MAX_TOPK * inter * 2) != hipSuccess
+           || (s->ws.n_cu = G.n_cu_dev) == 0
            || hipMalloc((void **)&s->d_x, dim * 2) != hipSuccess
            || hipMalloc((void **)&s->d_out, dim * 2) != hipSuccess
            || hipMalloc((void **)&s->d_idx, GHIP_MAX_TOPK * 4) != hipSuccess
@@ -607,9 +609,8 @@ void apus_ghip_store_close(ApusGhipStore *s) {
     hipDeviceSynchronize();
     hipFree(s->arena);
     hipFree(s->nan_flags);
-    hipFree(s->ws.route);
+    hipFree(s->ws.hw);
     hipFree(s->ws.err);
-    hipFree(s->ws.h);
     hipFree(s->d_x);
     hipFree(s->d_out);
     hipFree(s->d_idx);
@@ -990,7 +991,7 @@ int apus_ghip_moe_decode_dev(ApusGhipStore *s, const uint16_t *x,
     store_bank(s, &bk);
     hipError_t e = ghip_launch_moe_decode(&bk, x, logits, idx, w, topk,
                                           s->limit, out, &s->ws,
-                                          G.trace_n >= 4 ? G.trace_ev : NULL,
+                                          G.trace_n >= 2 ? G.trace_ev : NULL,
                                           (hipStream_t)stream);
     if (e != hipSuccess) {
         ghip_seterr("moe_decode launch: %s", hipGetErrorString(e));
@@ -1058,7 +1059,8 @@ int apus_ghip_moe_decode(ApusGhipStore *s, const uint16_t *x,
     uint32_t err = 0;
     HIPCHK(hipMemcpy(&err, s->ws.err, 4, hipMemcpyDeviceToHost));
     if (err) {
-        ghip_seterr(err & 4u ? "moe_decode: device-wide phase wait timed out (code %u)"
+        ghip_seterr(err & 4u ? "moe_decode: the gate/up -> down hand-off wait ran out "
+                               "(code %u)"
                              : "moe_decode: invalid expert id in routing (code %u)", err);
         hipMemset(s->ws.err, 0, 4);
         return 1;

@@ -41,22 +41,23 @@ hipError_t ghip_launch_bf16_linear(const uint16_t *w, const uint16_t *x,
                                    uint16_t *y, size_t M, size_t O, size_t K,
                                    const hipEvent_t *ev, hipStream_t st);
 
-/* K3 MoE decode workspace (device): the routing handoff between the
- * launches, the SwiGLU activations, and an error word. */
+/* K3 MoE decode workspace: the SwiGLU activations h handed from the
+ * gate/up phase to the down phase as tagged words (bf16 value in bits
+ * 0..15, the writing launch's tag in 16..31; zero-filled at creation), an
+ * error word, and the host's current tag. */
 typedef struct {
-    uint32_t *route;      /* device, GHIP_MOE_ROUTE_WORDS u32 */
-    uint16_t *h;          /* device [max topk, inter] bf16 */
-    uint32_t *err;        /* device u32: nonzero after an invalid expert id */
-    uint32_t n_cu;        /* persistent grid bound: the device's CU count */
+    uint32_t *hw;         /* device [16 slots, hw_inter] u32 */
+    uint32_t hw_inter;    /* inter the words were sized for */
+    uint32_t *err;        /* device u32: 2 = invalid expert id, 4 = hand-off wait ran out */
+    uint32_t n_cu;        /* grid: one workgroup per CU */
+    uint32_t tag;         /* host: the last launch's tag (0 before the first) */
 } GhipMoeDecodeWs;
 
 /* Streaming GEMV set-up (dynamic-LDS limits, persistent grid bound). */
 hipError_t ghip_linear_init(uint32_t n_cu);
 
-/* Raise the decode kernels' dynamic-LDS limit (once per process). */
+/* Raise the decode kernel's dynamic-LDS limit (once per process). */
 hipError_t ghip_moe_decode_init(void);
-
-#define GHIP_MOE_ROUTE_WORDS 64
 
 /* Expert bank view for the kernels: slab s of expert e at base + e*stride;
  * member byte offsets inside a slab (c/gcache.h:852-861 order). */
@@ -68,14 +69,16 @@ typedef struct {
     const uint32_t *nan_flags;   /* device [n_experts] u32 (required by decode) or NULL */
 } GhipBank;
 
-/* K3: routed MoE decode for one token (routing + gate/up + SwiGLU, down +
- * ordered combine: two launches on st; ev: NULL or 4 events timing them). Either logits (device f32
+/* K3: routed MoE decode for one token (routing, gate/up + SwiGLU, down +
+ * ordered combine) as one cooperative launch on st (ws->n_cu workgroups);
+ * ev: NULL or 2 events recorded around it. Either logits (device f32
  * [n_experts]; top-k + softmax on the device) or idx/w (device [topk]) must
- * be given. out: device [dim] bf16. */
+ * be given. out: device [dim] bf16. Advances ws->arrived. Launches that
+ * share a workspace must not overlap in time. */
 hipError_t ghip_launch_moe_decode(const GhipBank *bank, const uint16_t *x,
                                   const float *logits, const int32_t *idx,
                                   const float *w, int topk, float limit,
-                                  uint16_t *out, const GhipMoeDecodeWs *ws,
+                                  uint16_t *out, GhipMoeDecodeWs *ws,
                                   const hipEvent_t *ev, hipStream_t st);
 
 /* Router with the reference semantics (c/gmoe.h:191-208): gate logits (a

@@ -1,33 +1,35 @@
 /*
- * k_moe.hip — K3: routed-MoE decode for one token (gfx950).
+ * k_moe.hip — K3: routed-MoE decode for one token (gfx950), and the router.
  *
- * Three phases, shared by both launch forms:
- *   route    one wave: the harness routing (stable top-k of f32 logits,
- *            ties -> lower id, softmax over the k selected) or given idx/w,
- *            a repeated id keeping its first slot (c/gmoe.h:309-312), kept
- *            slots sorted by id; workgroup 0 publishes the record.
+ * The decode is ONE cooperative persistent launch (one workgroup per CU, all
+ * co-resident) with three phases:
+ *   route    one wave per workgroup (every workgroup routes redundantly, so
+ *            none waits for another): the harness routing (stable top-k of
+ *            f32 logits, ties -> lower id) or given idx/w, a repeated id
+ *            keeping its first slot (c/gmoe.h:309-312). Only the selected
+ *            ids are needed to start streaming; the softmax weights and the
+ *            ascending-id combine order are computed later, while the
+ *            workgroup waits for the device-wide hand-off.
  *   gate/up  per (slot q, 16 rows) the g and u GEMVs over dim with the FP8
  *            dequant fused (bit-exact weights) and the SwiGLU epilogue of
- *            c/gmoe.h:217-225 -> h[q].
+ *            c/gmoe.h:217-225 -> h[q] in HBM.
  *   down     per 16 output rows: wave q computes slot q's down GEMV
- *            (h[q] . Wd^T, full inter in-wave), then the ascending-expert
+ *            (h[q] . Wd^T over all of inter), then the ascending-expert
  *            combine y = bf16(y + bf16(bf16(o)*w)) (c/gmoe.h:307-320) runs
- *            in-workgroup -- no float atomics, no cross-workgroup
- *            reduction, deterministic.
- *
- * Two stream-ordered launches: k_moe_gateup (route + gate/up + SwiGLU ->
- * h in HBM) and k_moe_down (h staged in LDS, down + combine); the kernel
- * boundary orders the h handoff. A one-launch form that handed h across
- * the device with coherent atomics and an arrival counter measured slower
- * (50.7-53.3 us against 46.7-48.3 us per config-2 step): its atomic h
- * stores and loads and the device-wide wait cost more than a kernel
- * boundary.
+ *            in-workgroup -- no float atomics, no cross-workgroup reduction,
+ *            deterministic.
+ * Hand-off of h between the phases: each workgroup, after its gate/up work,
+ * makes its h stores visible device-wide (agent-scope release) and bumps a
+ * monotone arrival counter; before reading h it issues the first stages of
+ * its down weight ring, then waits (bounded) until the counter shows every
+ * workgroup of this launch, and acquires. The down weights are therefore
+ * already streaming when h becomes readable; there is no kernel boundary.
  *
  * Weight streaming: each wave pulls its 16-row chunks (128-wide k, one
  * scale block) through a wave-private LDS ring with direct global->LDS
- * loads, so the bytes in flight are not bounded by registers; the GEMV
- * inner step (ghip_chunk_mfma) dequantizes in registers and reduces over k
- * on MFMA with the activation (x or h) from LDS as the A operand.
+ * loads, so the bytes in flight are not bounded by registers; the GEMV inner
+ * step (ghip_chunk_mfma) dequantizes in registers and reduces over k on
+ * MFMA with the activation (x or h) from LDS as the A operand.
  */
 #include "ghip_device.h"
 #include "ghip_internal.h"
@@ -35,12 +37,8 @@
 #define MD_NW 8                  /* waves per workgroup */
 #define MD_T 16                  /* rows per tile (one MFMA group) */
 #define MD_MAXK 16               /* max routed slots */
-#define MD_LDS_MAX (144 * 1024)  /* dynamic LDS limit set for both GEMV kernels */
-
-/* routing workspace (u32 words): [0] nsel, [1..16] ids, [17..32] weights */
-#define RT_NSEL 0
-#define RT_IDS 1
-#define RT_W (1 + MD_MAXK)
+#define MD_LDS_MAX (144 * 1024)  /* dynamic LDS limit of the decode kernel */
+#define MD_SPIN_MAX (1u << 18)   /* bounded wait for the device-wide hand-off */
 
 /* ------------------------------------------------------------------------ */
 /* routing                                                                  */
@@ -139,13 +137,12 @@ __device__ __forceinline__ int rt_select(uint32_t (&key)[R], int topk, uint32_t 
     return myid;
 }
 
-/* the harness routing from logits: stable top-k, softmax over the k
- * selected in slot order (m = slot 0's logit, e_j = expf(l_j - m),
- * s = e_0 + e_1 + ... ascending j, w = e / s); kept slots placed by
- * ascending id. R logits per lane. */
+/* Selection of the harness routing from logits by one wave: the stable
+ * top-k (ties -> lower id). Lane j < topk returns pick j's id and its logit
+ * (selection order). R logits per lane. */
 template <int R>
-__device__ __forceinline__ void md_route_softmax(const float *__restrict__ logits, int topk,
-                                                 int E, uint32_t *rt) {
+__device__ __forceinline__ int md_select(const float *__restrict__ logits, int topk, int E,
+                                         float &mylog) {
     const int lane = threadIdx.x & 63;
     /* all R loads are issued before any is used: the index is clamped
      * rather than the load predicated, which would wait for each load
@@ -165,56 +162,57 @@ __device__ __forceinline__ void md_route_softmax(const float *__restrict__ logit
     for (int s = 0; s < R; s++) key[s] = lane + 64 * s < E ? rt_key(v[s]) : 0u;
     uint32_t mk;
     const int myid = rt_select<R>(key, topk, mk);
-    const float mylog = rt_val(mk);
-    const float m = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
-                                                  __builtin_bit_cast(int, mylog), 0));
-    const float ej = expf(mylog - m);
-    float ssum = 0.0f;
-    for (int j = 0; j < topk; j++)
-        ssum = ssum + __builtin_bit_cast(float, __builtin_amdgcn_readlane(
-                                                     __builtin_bit_cast(int, ej), j));
-    const float wj = ej / ssum;
-    /* distinct ids: place slot j by its rank among the k ids */
-    int pos = 0;
-    for (int j = 0; j < topk; j++)
-        pos += __builtin_amdgcn_readlane(myid, j) < myid;
-    if (lane < MD_MAXK) {
-        rt[RT_IDS + lane] = 0u;
-        rt[RT_W + lane] = 0u;
-    }
-    __builtin_amdgcn_wave_barrier();
-    if (lane < topk) {
-        rt[RT_IDS + pos] = (uint32_t)myid;
-        rt[RT_W + pos] = __float_as_uint(wj);
-    }
-    if (lane == 0) rt[RT_NSEL] = (uint32_t)topk;
-    __builtin_amdgcn_s_waitcnt(0xc07f);           /* lgkmcnt(0) */
-    __builtin_amdgcn_wave_barrier();
+    mylog = rt_val(mk);
+    return myid;
 }
 
-/* Routing by one wave into rt[] (an LDS route record: RT_NSEL, RT_IDS,
- * RT_W words). Either the harness routing from logits (md_route_softmax)
- * or given idx/w; a repeated id keeps its first slot (c/gmoe.h:309-312),
- * kept slots are placed by ascending expert id (the combine order). */
-__device__ __forceinline__ void md_route(const float *__restrict__ logits,
-                                         const int32_t *__restrict__ idx,
-                                         const float *__restrict__ w, int topk, int E,
-                                         uint32_t *rt, int32_t *te, float *tw,
-                                         uint32_t *__restrict__ err) {
+#define GU_NW 8                  /* waves per workgroup (two per SIMD) */
+#define GU_IPW 4                 /* items per workgroup pass (2 waves each) */
+#define GU_R 4                   /* ring stages per wave (gate + up chunk) */
+#define GU_STG 4096              /* bytes per stage */
+#define DN_R 6                   /* down ring stages per wave (one chunk each) */
+#define DN_STG 2048
+
+/* Per-workgroup shared state (static LDS). Slots: the kept routing picks
+ * in selection order (logits) or given order (idx); sel[q] is slot q's
+ * expert, wt[q] its weight, ord[i] the slot of the i-th smallest expert id
+ * (the combine order). */
+struct MdShared {
+    int32_t sel[MD_MAXK];
+    float wt[MD_MAXK];
+    uint32_t ord[MD_MAXK];
+    float lg[MD_MAXK];           /* logits path: slot q's logit */
+    int32_t te[MD_MAXK];
+    float tw[MD_MAXK];
+    uint32_t nsel, go;
+    float red[GU_IPW][2][2][16];
+    float oq[MD_MAXK][16];
+};
+
+/* Phase A, wave 0 only: the routing picks into sh.sel / sh.nsel. Given
+ * idx/w: a repeated id keeps its first slot (c/gmoe.h:309-312), invalid ids
+ * are dropped and flagged; kept slots stay in the given order, with their
+ * weights and the ascending-id order. Logits: the selected ids and their
+ * logits (weights and order come later, md_route_finish). */
+__device__ __forceinline__ void md_route_ids(const float *__restrict__ logits,
+                                             const int32_t *__restrict__ idx,
+                                             const float *__restrict__ w, int topk, int E,
+                                             MdShared &sh, uint32_t *__restrict__ err) {
     const int lane = threadIdx.x & 63;
     if (logits) {
-        if (E <= 5 * 64) md_route_softmax<5>(logits, topk, E, rt);
-        else md_route_softmax<8>(logits, topk, E, rt);
+        float mylog;
+        const int myid = E <= 5 * 64 ? md_select<5>(logits, topk, E, mylog)
+                                     : md_select<8>(logits, topk, E, mylog);
+        if (lane < topk) {
+            sh.sel[lane] = myid;
+            sh.lg[lane] = mylog;
+        }
+        if (lane == 0) sh.nsel = (uint32_t)topk;
         return;
     }
-    if (lane < topk) {
-        te[lane] = idx[lane];
-        tw[lane] = w[lane];
-    }
-    __builtin_amdgcn_s_waitcnt(0xc07f);           /* lgkmcnt(0) */
-    __builtin_amdgcn_wave_barrier();
-    const int e = lane < topk ? te[lane] : -1;
-    const float wj = lane < topk ? tw[lane] : 0.0f;
+    /* given routing: the loads of all slots first (one round trip) */
+    const int e = lane < topk ? idx[lane] : -1;
+    const float wj = lane < topk ? w[lane] : 0.0f;
     bool keep = lane < topk;
     if (keep && (e < 0 || e >= E)) {
         keep = false;
@@ -224,73 +222,38 @@ __device__ __forceinline__ void md_route(const float *__restrict__ logits,
     for (int q = 0; q < topk; q++)
         if (q < lane && __builtin_amdgcn_readlane(e, q) == e) keep = false;
     const uint64_t kept = __ballot(keep);
-    int pos = 0;
+    const int slot = (int)__popcll(kept & ((1ull << lane) - 1ull));
+    int rank = 0;
     for (int q = 0; q < topk; q++)
-        pos += ((kept >> q) & 1u) && __builtin_amdgcn_readlane(e, q) < e;
-    const uint32_t nsel = (uint32_t)__popcll(kept);
-    if (lane < MD_MAXK) {                 /* clear, then place kept slots */
-        rt[RT_IDS + lane] = 0u;
-        rt[RT_W + lane] = 0u;
-    }
-    __builtin_amdgcn_wave_barrier();
+        rank += ((kept >> q) & 1u) && __builtin_amdgcn_readlane(e, q) < e;
     if (keep) {
-        rt[RT_IDS + pos] = (uint32_t)e;
-        rt[RT_W + pos] = __float_as_uint(wj);
+        sh.sel[slot] = e;
+        sh.wt[slot] = wj;
+        sh.ord[rank] = (uint32_t)slot;
     }
-    if (lane == 0) rt[RT_NSEL] = nsel;
-    __builtin_amdgcn_s_waitcnt(0xc07f);           /* lgkmcnt(0) */
-    __builtin_amdgcn_wave_barrier();
+    if (lane == 0) sh.nsel = (uint32_t)__popcll(kept);
 }
 
-/* ------------------------------------------------------------------------ */
-/* weight streaming (both GEMV kernels)                                     */
-/* ------------------------------------------------------------------------ */
-
-/* ------------------------------------------------------------------------ */
-/* gate/up + SwiGLU                                                         */
-/* ------------------------------------------------------------------------ */
-
-#define GU_NW 8                  /* waves per workgroup (two per SIMD) */
-#define GU_IPW 4                 /* items per workgroup pass (2 waves each) */
-#define GU_R 4                   /* ring stages per wave (gate + up chunk) */
-#define GU_STG 4096              /* bytes per stage */
-#define DN_R 6                   /* down ring stages per wave (one chunk each) */
-#define DN_STG 2048
-
-/* LDS that both kernels share (static, per workgroup) */
-struct MdShared {
-    uint32_t rt[GHIP_MOE_ROUTE_WORDS];
-    int32_t te[MD_MAXK];
-    float tw[MD_MAXK];
-    float red[GU_IPW][2][2][16];
-    float oq[MD_MAXK][16];
-};
-
-/* Phase A: routing (wave 0 into sh.rt) and x into LDS, then a barrier. */
-__device__ __forceinline__ void md_phase_route(const GhipBank &bank,
-                                               const uint16_t *__restrict__ x,
-                                               const float *__restrict__ logits,
-                                               const int32_t *__restrict__ idx,
-                                               const float *__restrict__ w, int topk,
-                                               uint16_t *xs, MdShared &sh,
-                                               uint32_t *__restrict__ err) {
-    const uint32_t tid = threadIdx.x;
-    const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    /* the first GU_NW * 64 pieces of x are loaded before the routing, so
-     * the routing wave's piece does not cost a round trip after it */
-    const uint32_t n16 = bank.dim >> 3;
-    const ghip_u32x4 x0 = ((const ghip_u32x4 *)x)[tid < n16 ? tid : n16 - 1];
-    if (wv == 0)
-        md_route(logits, idx, w, topk, (int)bank.n_experts, sh.rt, sh.te, sh.tw,
-                 blockIdx.x == 0 ? err : nullptr);
-    asm volatile("" ::"v"(x0));
-    if (tid < n16) ((ghip_u32x4 *)xs)[tid] = x0;
-    for (uint32_t i = tid + GU_NW * 64; i < n16; i += GU_NW * 64)
-        ((ghip_u32x4 *)xs)[i] = ((const ghip_u32x4 *)x)[i];
-    /* nothing of the routing (its error-flag atomic included) stays in
-     * flight into the streaming loops, whose vmcnt waits count only DMA */
-    GHIP_VMCNT(0);
-    __syncthreads();
+/* Logits path, wave 0, after phase A: softmax over the k selected logits in
+ * slot order (m = slot 0's logit, e_q = expf(l_q - m), s = e_0 + e_1 + ...
+ * ascending q, w = e / s) and the ascending-id order. */
+__device__ __forceinline__ void md_route_finish(MdShared &sh, int topk) {
+    const int lane = threadIdx.x & 63;
+    const int myid = lane < topk ? sh.sel[lane] : 0x7fffffff;
+    const float mylog = lane < topk ? sh.lg[lane] : 0.0f;
+    const float m = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                                  __builtin_bit_cast(int, mylog), 0));
+    const float ej = expf(mylog - m);
+    float ssum = 0.0f;
+    for (int j = 0; j < topk; j++)
+        ssum = ssum + __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                                     __builtin_bit_cast(int, ej), j));
+    int rank = 0;
+    for (int j = 0; j < topk; j++) rank += __builtin_amdgcn_readlane(myid, j) < myid;
+    if (lane < topk) {
+        sh.wt[lane] = ej / ssum;
+        sh.ord[rank] = (uint32_t)lane;
+    }
 }
 
 /* Phase B: items = (slot q, 16 rows): gate and up GEMVs over dim and the
@@ -298,16 +261,15 @@ __device__ __forceinline__ void md_phase_route(const GhipBank &bank,
  * w streams item (w / 2)'s half (w % 2) of K through a wave-private
  * GU_R-stage LDS ring filled by direct DMA (no registers hold loads in
  * flight, no barriers inside the stream); the halves are summed in LDS in a
- * fixed order (deterministic). put(q, row, hval) stores one h value (lanes
- * 0..15 of the even wave of each item call it together). */
-template <typename Put>
+ * fixed order (deterministic). The 16 h values of an item go to hw[q] in
+ * HBM as tagged words (lanes 0..15 of the item's even wave). */
 __device__ __forceinline__ void md_phase_gateup(const GhipBank &bank, const uint16_t *xs,
                                                 uint8_t *ring_base, MdShared &sh,
-                                                float limit, Put put) {
+                                                float limit, uint32_t *hw, uint32_t tag) {
     const uint32_t dim = bank.dim, inter = bank.inter;
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t nsel = __builtin_amdgcn_readfirstlane(sh.rt[RT_NSEL]);
+    const uint32_t nsel = __builtin_amdgcn_readfirstlane(sh.nsel);
     const uint32_t tiles = inter / MD_T, items = nsel * tiles;
     const uint32_t groups = (items + GU_IPW - 1) / GU_IPW;
     uint8_t *ring = ring_base + wv * (GU_R * GU_STG);
@@ -325,7 +287,7 @@ __device__ __forceinline__ void md_phase_gateup(const GhipBank &bank, const uint
         if (live) {
             q = it / tiles;
             r0 = (it - q * tiles) * MD_T;
-            const uint32_t e = __builtin_amdgcn_readfirstlane(sh.rt[RT_IDS + q]);
+            const uint32_t e = (uint32_t)__builtin_amdgcn_readfirstlane(sh.sel[q]);
             const uint8_t *slab = bank.base + (size_t)e * bank.stride;
             const uint8_t *wg = slab + bank.off_gw + (size_t)r0 * dim;
             const uint8_t *wu = slab + bank.off_uw + (size_t)r0 * dim;
@@ -372,29 +334,32 @@ __device__ __forceinline__ void md_phase_gateup(const GhipBank &bank, const uint
         if (live && half == 0 && lane < 16) {     /* fixed order: half 0 + half 1 */
             const float gs = sh.red[slot][0][0][lane] + sh.red[slot][1][0][lane];
             const float us = sh.red[slot][0][1][lane] + sh.red[slot][1][1][lane];
-            put(q, r0 + lane,
-                ghip_swiglu(ghip_bf16_round(gs), ghip_bf16_round(us), limit));
+            const uint32_t hv = ghip_swiglu(ghip_bf16_round(gs), ghip_bf16_round(us), limit);
+            /* the value and this launch's tag in one word, stored
+             * device-coherently: the word itself tells a reader on any XCD
+             * that it is this launch's value */
+            __hip_atomic_store(hw + (size_t)q * inter + r0 + lane, (tag << 16) | hv,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         __syncthreads();
     }
 }
 
 /* Phase C, down + ordered combine for the 16 output rows at r0: wave q
- * streams expert slot q's 16 rows of Wd over inter through its own
- * DN_R-stage DMA ring with h of slot base + q (in LDS at hs + q * inter)
- * as the A operand and leaves the expert output in sh.oq; md_combine then
- * runs the ordered combine in-workgroup: no atomics, no cross-workgroup
- * reduction, deterministic. md_down_prologue issues the first DN_R - 1
- * stages (so they stream while the caller waits for h). */
+ * streams slot base + q's 16 rows of Wd over inter through its own
+ * DN_R-stage DMA ring with h of that slot (in LDS at hs + q * inter) as the
+ * A operand and leaves the expert output in sh.oq; md_combine then runs the
+ * ordered combine in-workgroup. md_down_prologue issues the first DN_R - 1
+ * stages (so they stream while the workgroup waits for h). */
 __device__ __forceinline__ void md_down_prologue(const GhipBank &bank, const MdShared &sh,
                                                  uint32_t r0, uint32_t base,
                                                  uint8_t *ring_base) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t nsel = __builtin_amdgcn_readfirstlane(sh.rt[RT_NSEL]);
+    const uint32_t nsel = __builtin_amdgcn_readfirstlane(sh.nsel);
     if (base + wv >= nsel) return;
     const uint32_t inter = bank.inter, nch = inter >> 7;
-    const uint32_t e = __builtin_amdgcn_readfirstlane(sh.rt[RT_IDS + base + wv]);
+    const uint32_t e = (uint32_t)__builtin_amdgcn_readfirstlane(sh.sel[base + wv]);
     const uint8_t *rows = bank.base + (size_t)e * bank.stride + bank.off_dw + (size_t)r0 * inter;
     const ghip_cdma d = ghip_cdma_offsets(lane, inter);
     uint8_t *ring = ring_base + wv * (DN_R * DN_STG);
@@ -410,9 +375,9 @@ __device__ __forceinline__ void md_phase_down(const GhipBank &bank, MdShared &sh
     const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t n = lane & 15u, g = lane >> 4;
     const uint32_t inter = bank.inter, nch = inter >> 7, nkb = inter >> 7;
-    const uint32_t nsel = __builtin_amdgcn_readfirstlane(sh.rt[RT_NSEL]);
+    const uint32_t nsel = __builtin_amdgcn_readfirstlane(sh.nsel);
     if (base + wv < nsel) {
-        const uint32_t e = __builtin_amdgcn_readfirstlane(sh.rt[RT_IDS + base + wv]);
+        const uint32_t e = (uint32_t)__builtin_amdgcn_readfirstlane(sh.sel[base + wv]);
         const uint8_t *slab = bank.base + (size_t)e * bank.stride;
         const uint8_t *rows = slab + bank.off_dw + (size_t)r0 * inter;
         const float *srow = (const float *)(slab + bank.off_ds) + (size_t)(r0 >> 7) * nkb;
@@ -434,94 +399,153 @@ __device__ __forceinline__ void md_phase_down(const GhipBank &bank, MdShared &sh
     }
 }
 
-/* the ascending-expert combine of the nsel expert outputs in sh.oq (slot
- * order = ascending expert id): y = bf16(y + bf16(bf16(o) * w)), from +0
- * (c/gmoe.h:307-320). Call after a barrier. */
+/* the ascending-expert combine of the nsel expert outputs in sh.oq: y =
+ * bf16(y + bf16(bf16(o) * w)), from +0 (c/gmoe.h:307-320). Call after a
+ * barrier. */
 __device__ __forceinline__ void md_combine(const MdShared &sh, uint32_t r0,
                                            uint16_t *__restrict__ out) {
     const uint32_t tid = threadIdx.x;
     if (tid < 16) {
-        const uint32_t nsel = sh.rt[RT_NSEL];
+        const uint32_t nsel = sh.nsel;
         float y = 0.0f;
-        for (uint32_t q = 0; q < nsel; q++) {
+        for (uint32_t i = 0; i < nsel; i++) {
+            const uint32_t q = sh.ord[i];
             float eo = ghip_bf16_round(sh.oq[q][tid]);
-            float c = ghip_bf16_round(eo * __uint_as_float(sh.rt[RT_W + q]));
+            float c = ghip_bf16_round(eo * sh.wt[q]);
             y = ghip_bf16_round(y + c);
         }
         out[r0 + tid] = (uint16_t)ghip_bf16_bits(y);
     }
 }
 
-/* ------------------------------------------------------------------------ */
-/* the two launches                                                         */
-/* ------------------------------------------------------------------------ */
-
-__global__ __launch_bounds__(GU_NW * 64, 1) void k_moe_gateup(
-    GhipBank bank, const uint16_t *__restrict__ x, const float *__restrict__ logits,
-    const int32_t *__restrict__ idx, const float *__restrict__ w, int topk,
-    float limit, uint16_t *__restrict__ h, uint32_t *__restrict__ route_out,
-    uint32_t *__restrict__ err) {
-    extern __shared__ __attribute__((aligned(1024))) uint8_t gl[];
-    __shared__ MdShared sh;
-    const uint32_t dim = bank.dim, inter = bank.inter;
-    uint16_t *xs = (uint16_t *)gl;
-    md_phase_route(bank, x, logits, idx, w, topk, xs, sh, err);
-    if (blockIdx.x == 0 && threadIdx.x < GHIP_MOE_ROUTE_WORDS)
-        route_out[threadIdx.x] = sh.rt[threadIdx.x];
-    md_phase_gateup(bank, xs, gl + ((dim * 2u + 1023u) & ~1023u), sh, limit,
-                    [&](uint32_t q, uint32_t row, uint32_t hv) {
-                        h[(size_t)q * inter + row] = (uint16_t)hv;
-                    });
+/* h of slots [base, base + m) into LDS (hs [m][inter] bf16) from the tagged
+ * words hw (value in bits 0..15, the writing launch's tag in 16..31). Every
+ * thread loads its words with device-coherent loads and re-polls the ones
+ * that do not carry this launch's tag yet (their gate/up item is still
+ * running on another CU), all waves at most MD_SPIN_MAX rounds. Returns
+ * false (after a workgroup barrier, the same in every thread) when a word
+ * is still missing then. */
+__device__ __forceinline__ bool md_stage_h(const uint32_t *hw, uint32_t base, uint32_t m,
+                                           uint32_t inter, uint32_t tag, uint16_t *hs,
+                                           MdShared &sh) {
+    constexpr uint32_t NT = MD_NW * 64, PER = 8;
+    const uint32_t tid = threadIdx.x, n = m * inter;
+    const uint32_t *src = hw + (size_t)base * inter;
+    bool ok = true;
+    for (uint32_t i0 = 0; i0 < n; i0 += NT * PER) {
+        uint32_t v[PER];
+#pragma unroll
+        for (uint32_t u = 0; u < PER; u++) {
+            const uint32_t i = i0 + u * NT + tid;
+            v[u] = __hip_atomic_load(src + (i < n ? i : n - 1), __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+        }
+        /* the wave polls until all its words carry the tag (uniform exit) */
+        for (uint32_t it = 0;; it++) {
+            uint32_t miss = 0;
+#pragma unroll
+            for (uint32_t u = 0; u < PER; u++) {
+                const uint32_t i = i0 + u * NT + tid;
+                miss |= (i < n && (v[u] >> 16) != tag) ? 1u << u : 0u;
+            }
+            if (!__builtin_amdgcn_readfirstlane((uint32_t)(__ballot(miss != 0u) != 0ull)))
+                break;
+            if (it >= MD_SPIN_MAX) {
+                ok = false;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(4);
+#pragma unroll
+            for (uint32_t u = 0; u < PER; u++)
+                if ((miss >> u) & 1u)
+                    v[u] = __hip_atomic_load(src + i0 + u * NT + tid, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < PER; u++) {
+            const uint32_t i = i0 + u * NT + tid;
+            if (i < n) hs[i] = (uint16_t)v[u];
+        }
+        if (!ok) break;
+    }
+    if (tid == 0) sh.go = 1u;
+    __syncthreads();
+    if (!ok) sh.go = 0u;
+    __syncthreads();
+    return __builtin_amdgcn_readfirstlane(sh.go) != 0u;
 }
 
-/* One workgroup per 16 output rows; h of up to 8 slots in LDS per pass
- * (slots past 8 run in a second pass with h restaged), then the combine
- * over all slots. */
-__global__ __launch_bounds__(MD_NW * 64, 1) void k_moe_down(
-    GhipBank bank, const uint16_t *__restrict__ h, const uint32_t *__restrict__ route,
-    uint16_t *__restrict__ out) {
+/* ------------------------------------------------------------------------ */
+/* the decode launch                                                        */
+/* ------------------------------------------------------------------------ */
+
+/* One launch of gridDim.x workgroups (one per CU), 8 waves each. hw: the
+ * tagged h words ([max topk][inter] u32), tag: this launch's tag (1..65535;
+ * the host clears hw whenever the tag wraps, so no stale word carries a
+ * live tag). Every workgroup must be resident at once (one per CU, as the
+ * LDS use makes it): a workgroup whose wait for h runs out (MD_SPIN_MAX
+ * polls, a concurrently running kernel holding CUs can cause it) flags
+ * err |= 4 and skips its down rows instead of hanging. */
+__global__ __launch_bounds__(MD_NW * 64, 1) void k_moe_decode(
+    GhipBank bank, const uint16_t *__restrict__ x, const float *__restrict__ logits,
+    const int32_t *__restrict__ idx, const float *__restrict__ w, int topk, float limit,
+    uint32_t *hw, uint32_t tag, uint32_t *__restrict__ err, uint16_t *__restrict__ out) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t dl[];
     __shared__ MdShared sh;
-    const uint32_t tid = threadIdx.x, inter = bank.inter;
-    if (tid < GHIP_MOE_ROUTE_WORDS) sh.rt[tid] = route[tid];
-    __syncthreads();
-    const uint32_t nsel = sh.rt[RT_NSEL];
-    uint16_t *hs = (uint16_t *)dl;
-    uint8_t *ring = dl + (size_t)MD_NW * inter * 2u;
-    const uint32_t r0 = blockIdx.x * MD_T;
-    for (uint32_t base = 0; base < nsel; base += MD_NW) {
-        const uint32_t m = nsel - base < MD_NW ? nsel - base : MD_NW;
-        /* the weight ring's first stages, then h, all in flight together;
-         * h loads go four per thread with a clamped index, so none waits
-         * behind another (a load-then-store loop costs a round trip per
-         * iteration) */
-        md_down_prologue(bank, sh, r0, base, ring);
-        const uint32_t n16 = m * inter / 8;
-        const ghip_u32x4 *hsrc = (const ghip_u32x4 *)(h + (size_t)base * inter);
-        for (uint32_t i0 = tid; i0 < n16; i0 += 4 * MD_NW * 64) {
-            ghip_u32x4 v[4];
-#pragma unroll
-            for (uint32_t u = 0; u < 4; u++) {
-                const uint32_t i = i0 + u * MD_NW * 64;
-                v[u] = hsrc[i < n16 ? i : n16 - 1];
-            }
-#pragma unroll
-            for (uint32_t u = 0; u < 4; u++) asm volatile("" ::"v"(v[u]));
-#pragma unroll
-            for (uint32_t u = 0; u < 4; u++) {
-                const uint32_t i = i0 + u * MD_NW * 64;
-                if (i < n16) ((ghip_u32x4 *)hs)[i] = v[u];
-            }
-        }
+    const uint32_t tid = threadIdx.x;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t dim = bank.dim, inter = bank.inter;
+    uint16_t *xs = (uint16_t *)dl;
+
+    /* --- phase A: route (wave 0) while x goes to LDS ------------------- */
+    {
+        /* the first MD_NW * 64 pieces of x are loaded before the routing, so
+         * the routing wave's piece does not cost a round trip after it */
+        const uint32_t n16 = dim >> 3;
+        const ghip_u32x4 x0 = ((const ghip_u32x4 *)x)[tid < n16 ? tid : n16 - 1];
+        if (wv == 0)
+            md_route_ids(logits, idx, w, topk, (int)bank.n_experts, sh,
+                         blockIdx.x == 0 ? err : nullptr);
+        asm volatile("" ::"v"(x0));
+        if (tid < n16) ((ghip_u32x4 *)xs)[tid] = x0;
+        for (uint32_t i = tid + MD_NW * 64; i < n16; i += MD_NW * 64)
+            ((ghip_u32x4 *)xs)[i] = ((const ghip_u32x4 *)x)[i];
+        /* nothing of the routing (its error-flag atomic included) stays in
+         * flight into the streaming loops, whose vmcnt waits count only DMA */
         GHIP_VMCNT(0);
         __syncthreads();
-        md_phase_down(bank, sh, r0, base, hs, ring);
-        __syncthreads();
     }
-    md_combine(sh, r0, out);
-}
 
-/* ------------------------------------------------------------------------ */
+    /* --- phase B: gate/up + SwiGLU -> tagged h words ------------------- */
+    md_phase_gateup(bank, xs, dl + ((dim * 2u + 1023u) & ~1023u), sh, limit, hw, tag);
+
+    /* --- phase C: down + combine per 16 output rows -------------------- */
+    const uint32_t nsel = __builtin_amdgcn_readfirstlane(sh.nsel);
+    uint16_t *hs = (uint16_t *)dl;
+    uint8_t *ring = dl + (size_t)MD_NW * inter * 2u;
+    if (wv == 0 && logits) md_route_finish(sh, topk);
+    for (uint32_t rg = blockIdx.x; rg * MD_T < dim; rg += gridDim.x) {
+        const uint32_t r0 = rg * MD_T;
+        for (uint32_t base = 0; base < nsel; base += MD_NW) {
+            const uint32_t m = nsel - base < MD_NW ? nsel - base : MD_NW;
+            /* the weight ring's first stages stream while h is awaited */
+            md_down_prologue(bank, sh, r0, base, ring);
+            /* h of this pass's slots (once when all slots fit one pass) */
+            if (base > 0 || rg == blockIdx.x || nsel > MD_NW) {
+                if (!md_stage_h(hw, base, m, inter, tag, hs, sh)) {
+                    if (tid == 0) atomicOr(err, 4u);
+                    GHIP_VMCNT(0);                /* drain the ring before leaving */
+                    return;
+                }
+            }
+            GHIP_VMCNT(0);
+            __syncthreads();
+            md_phase_down(bank, sh, r0, base, hs, ring);
+            __syncthreads();
+        }
+        md_combine(sh, r0, out);
+    }
+}
 
 /* ------------------------------------------------------------------------ */
 /* router with the reference semantics (c/gmoe.h:191-208)                   */
@@ -718,7 +742,7 @@ extern "C" hipError_t ghip_launch_moe_decode(const GhipBank *bank,
                                              const int32_t *idx, const float *w,
                                              int topk, float limit,
                                              uint16_t *out,
-                                             const GhipMoeDecodeWs *ws,
+                                             GhipMoeDecodeWs *ws,
                                              const hipEvent_t *ev,
                                              hipStream_t st) {
     if (!bank || !bank->nan_flags || !ws || !x || !out) return hipErrorInvalidValue;
@@ -734,27 +758,26 @@ extern "C" hipError_t ghip_launch_moe_decode(const GhipBank *bank,
         return hipErrorInvalidValue;
     const size_t lds_gu = (((size_t)dim * 2 + 1023) & ~(size_t)1023) + GU_NW * GU_R * GU_STG;
     const size_t lds_dn = (size_t)MD_NW * inter * 2 + MD_NW * DN_R * DN_STG;
-    if (lds_gu > MD_LDS_MAX || lds_dn > MD_LDS_MAX || ws->n_cu == 0)
+    const size_t lds = lds_gu > lds_dn ? lds_gu : lds_dn;
+    if (lds > MD_LDS_MAX || ws->n_cu == 0 || !ws->hw || !ws->err || inter > ws->hw_inter)
         return hipErrorInvalidValue;
-    hipEvent_t e0 = ev ? ev[0] : nullptr, e1 = ev ? ev[1] : nullptr;
-    hipEvent_t e2 = ev ? ev[2] : nullptr, e3 = ev ? ev[3] : nullptr;
+    /* one workgroup per CU (the LDS use keeps it at one); the tag names
+     * this launch's h words: 1..65535, and when it wraps the words are
+     * cleared first (by a fill kernel, ordered on st), so a word left from
+     * 65535 launches ago cannot pass for this launch's */
     hipError_t e;
-    uint32_t groups = ((uint32_t)topk * (inter / MD_T) + GU_IPW - 1) / GU_IPW;
-    if (groups > ws->n_cu) groups = ws->n_cu;             /* persistent */
-    GHIP_LAUNCH(e0, e1, k_moe_gateup, dim3(groups), dim3(GU_NW * 64), lds_gu, st, *bank,
-                x, logits, idx, w, topk, limit, ws->h, ws->route, ws->err);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    GHIP_LAUNCH(e2, e3, k_moe_down, dim3(dim / MD_T), dim3(MD_NW * 64), lds_dn, st,
-                *bank, ws->h, ws->route, out);
+    if (++ws->tag > 0xffffu) {
+        if ((e = ghip_launch_fill_u32(ws->hw, (size_t)MD_MAXK * inter, 0u, st)) != hipSuccess)
+            return e;
+        ws->tag = 1;
+    }
+    GHIP_LAUNCH(ev ? ev[0] : nullptr, ev ? ev[1] : nullptr, k_moe_decode, dim3(ws->n_cu),
+                dim3(MD_NW * 64), lds, st, *bank, x, logits, idx, w, topk, limit, ws->hw,
+                ws->tag, ws->err, out);
     return hipGetLastError();
 }
 
 extern "C" hipError_t ghip_moe_decode_init(void) {
-    const void *ks[2] = {(const void *)k_moe_gateup, (const void *)k_moe_down};
-    for (int i = 0; i < 2; i++) {
-        hipError_t e = hipFuncSetAttribute(ks[i], hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           MD_LDS_MAX);
-        if (e != hipSuccess) return e;
-    }
-    return hipSuccess;
+    return hipFuncSetAttribute((const void *)k_moe_decode,
+                               hipFuncAttributeMaxDynamicSharedMemorySize, MD_LDS_MAX);
 }

@@ -212,14 +212,13 @@ def bench_moe_decode(lib, pkg, rt, steps, warmup, rotate=64):
     t0 = time.perf_counter()
     ms = timed(rt, st, step, warmup, steps)
     wall = time.perf_counter() - t0
-    kt = kernel_times(lib, rt, step, warmup + steps, steps, 4,
-                      {"k_moe_gateup": (0, 1), "k_moe_down": (2, 3)})
-    nbytes, flops, gu_bytes = moe_algorithmic_bytes(E, k, dim, inter)
+    kt = kernel_times(lib, rt, step, warmup + steps, steps, 2, {"k_moe_decode": (0, 1)})
+    nbytes, flops, _ = moe_algorithmic_bytes(E, k, dim, inter)
     gbs = nbytes / (ms * 1e-3) / 1e9
     lib.apus_ghip_store_close(store)
-    # the dominant launch: routing + gate/up (2/3 of the weight bytes)
-    kern = {"kernel": "k_moe_gateup", "kernel_ms": kt["k_moe_gateup"],
-            "kernel_bytes": gu_bytes, "kernel_flops": 2 * k * 2 * inter * dim,
+    # the step is one launch: routing, gate/up, hand-off, down + combine
+    kern = {"kernel": "k_moe_decode", "kernel_ms": kt["k_moe_decode"],
+            "kernel_bytes": nbytes, "kernel_flops": flops,
             "launch_ms": {n: round(v, 5) for n, v in kt.items()}}
     return {
         "ms_per_step": ms, "value": gbs, "wall_s": wall,
@@ -668,32 +667,30 @@ def bench_moe_decode_router(lib, pkg, rt, steps, warmup, rotate=64):
         decode(i)
 
     ms = timed(rt, st, both, warmup, steps)
-    # per-launch times: the router and the two decode launches, each with
-    # its own dispatch-packet events
+    # per-launch times: the router and the decode launch, each with its own
+    # events
     n = steps
-    evs = [[rt.Event() for _ in range(6)] for _ in range(n)]
-    arr2, arr4 = ctypes.c_void_p * 2, ctypes.c_void_p * 4
+    evs = [[rt.Event() for _ in range(4)] for _ in range(n)]
+    arr2 = ctypes.c_void_p * 2
     for i in range(n):
         lib.apus_ghip_set_trace_events(arr2(*[e.handle for e in evs[i][:2]]), 2)
         router(warmup + steps + i)
-        lib.apus_ghip_set_trace_events(arr4(*[e.handle for e in evs[i][2:]]), 4)
+        lib.apus_ghip_set_trace_events(arr2(*[e.handle for e in evs[i][2:]]), 2)
         decode(warmup + steps + i)
     lib.apus_ghip_set_trace_events(None, 0)
     rt.synchronize()
     t_router = sum(e[0].elapsed_ms(e[1]) for e in evs) / n
-    t_gu = sum(e[2].elapsed_ms(e[3]) for e in evs) / n
-    t_dn = sum(e[4].elapsed_ms(e[5]) for e in evs) / n
+    t_dec = sum(e[2].elapsed_ms(e[3]) for e in evs) / n
     lib.apus_ghip_store_close(store)
-    full, _, gu_bytes = moe_algorithmic_bytes(E, k, dim, inter)
+    full, _, _ = moe_algorithmic_bytes(E, k, dim, inter)
     nbytes = full - E * 4 + E * dim * 2 + E * 4         # gate_w + bias, no logits
     return {
         "ms_per_step": ms, "value": nbytes / (ms * 1e-3) / 1e9,
         "weight_bytes": k * 3 * inter * dim + E * dim * 2,
         "bytes": nbytes, "flops": 2 * k * 3 * inter * dim + 2 * E * dim,
-        "kernel": "k_moe_gateup", "kernel_ms": t_gu, "kernel_bytes": gu_bytes - E * 4,
-        "kernel_flops": 2 * k * 2 * inter * dim, "traffic_key": "k_moe_gateup@given_routing",
-        "launch_ms": {"k_router": round(t_router, 5), "k_moe_gateup": round(t_gu, 5),
-                      "k_moe_down": round(t_dn, 5)},
+        "kernel": "k_moe_decode", "kernel_ms": t_dec, "kernel_bytes": full - E * 4,
+        "kernel_flops": 2 * k * 3 * inter * dim, "traffic_key": "k_moe_decode@given_routing",
+        "launch_ms": {"k_router": round(t_router, 5), "k_moe_decode": round(t_dec, 5)},
         "config": {"workload": "moe_decode_router (BASELINE config 2 shapes, routed by "
                                "the reference router c/gmoe.h:191-208)",
                    "experts": E, "topk": k, "dim": dim, "inter": inter,

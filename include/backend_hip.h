@@ -219,10 +219,11 @@ int apus_ghip_moe_router_dev(const uint16_t *x, const uint16_t *gate_w,
                              int32_t *idx, float *w, void *stream);
 
 /* --- routed MoE decode (one token): SwiGLU experts + ordered combine,
- * c/gmoe.h:210-227 + 307-320 without the router and shared expert. Two
- * stream-ordered launches: routing + gate/up GEMVs with the SwiGLU epilogue
- * (activations to HBM), then down GEMVs with the ascending-expert
- * bf16-per-add combine.
+ * c/gmoe.h:210-227 + 307-320 without the router and shared expert. One
+ * cooperative launch (one workgroup per CU): routing, gate/up GEMVs with the
+ * SwiGLU epilogue (activations to HBM), a device-wide hand-off, then down
+ * GEMVs with the ascending-expert bf16-per-add combine. Calls that share a
+ * store must not overlap in time (one stream).
  * Routing either given (idx/w [topk]) or computed on the device from
  * logits [n_experts] f32: stable top-k (ties -> lower id), w = softmax over
  * the k selected logits. Host-pointer variant is synchronous. */
@@ -281,8 +282,8 @@ int apus_ghip_moe_prefill_dev_noalloc(ApusGhipStore *s, const uint16_t *x, size_
  * events: n caller-created hipEvent_t handles, NULL/0 turns it off. While
  * set, launches carry start/stop events in their dispatch packets
  * (hipExtLaunchKernelGGL), so an event pair spans exactly one kernel:
- * apus_ghip_moe_decode_dev (n >= 4) times the routing + gate/up launch
- * with events[0..1] and the down launch with events[2..3];
+ * apus_ghip_moe_decode_dev (n >= 2) records events[0] and events[1]
+ * around its one launch;
  * apus_ghip_fp8blk_linear_dev, apus_ghip_bf16_gemm_dev and
  * apus_ghip_moe_router_dev (n >= 2) start events[0] with their first launch
  * and stop events[1] with their last; apus_ghip_moe_prefill_dev

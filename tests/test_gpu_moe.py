@@ -261,3 +261,30 @@ def test_config2_golden(ghip, pkg):
         record("config2_golden_host_routing", st)
     finally:
         ghip.apus_ghip_store_close(s)
+
+
+def test_moe_decode_back_to_back_calls(small):
+    """Decode calls enqueued back to back on one stream, no host sync in
+    between: each launch's device-wide hand-off counts only its own
+    workgroups (the arrival counter is monotone across launches), so every
+    output equals the same call run alone, bitwise."""
+    ghip, s, slabs, (E, dim, inter) = small
+    rng = np.random.default_rng(21)
+    calls = []
+    for k in (4, 1, 8, 3, 8):
+        x = O.f32_to_bf16(rng.standard_normal(dim).astype(np.float32))
+        idx = rng.choice(E, k, replace=False).astype(np.int32)
+        w = rng.uniform(0.05, 0.5, k).astype(np.float32)
+        calls.append((x, idx, w))
+    alone = []
+    for x, idx, w in calls:
+        out = np.empty(dim, np.uint16)
+        assert ghip.apus_ghip_moe_decode(s, O.ptr(x), O.ptr(idx), O.ptr(w), len(idx),
+                                         O.ptr(out)) == 0
+        alone.append(out)
+    bufs = [(G.dev(x), G.dev(idx), G.dev(w), G.empty(dim * 2), len(idx)) for x, idx, w in calls]
+    for dx, di, dw, do, k in bufs:
+        assert ghip.apus_ghip_moe_decode_dev(s, G.vp(dx), None, G.vp(di), G.vp(dw), k,
+                                             G.vp(do), G.stream()) == 0
+    for (dx, di, dw, do, k), want in zip(bufs, alone):
+        assert np.array_equal(G.host(do, np.uint16, (dim,)), want), "k=%d back to back" % k
