@@ -147,11 +147,12 @@ hipError_t ghip_launch_moe_prefill(const GhipBank *bank, const uint16_t *x,
 
 /* Dense FP8-block GEMM on MFMA (the prefill tile body): Y [M, N] =
  * bf16(X [M, K] . dequant(W [N, K])^T). Shapes it takes: N % 256 == 0,
- * K % 128 == 0, K <= 16384, 16-byte aligned codes and X
+ * K % 128 == 0, K <= 16384, 16-byte aligned codes, X and Y
  * (ghip_fp8_gemm_fits). Persistent grid of at most n_cu workgroups; the
  * dynamic-LDS limit is raised by ghip_moe_prefill_init. ev: NULL or 2
  * events. */
-int ghip_fp8_gemm_fits(size_t M, size_t N, size_t K, const void *codes, const void *x);
+int ghip_fp8_gemm_fits(size_t M, size_t N, size_t K, const void *codes, const void *x,
+                       const void *y);
 hipError_t ghip_launch_fp8_gemm(const uint8_t *codes, const float *scales,
                                 const uint16_t *x, uint16_t *y, size_t M, size_t N,
                                 size_t K, const uint32_t *exact_dev, uint32_t n_cu,

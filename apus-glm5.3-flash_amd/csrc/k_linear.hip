@@ -434,7 +434,7 @@ extern "C" hipError_t ghip_launch_fp8_linear(const uint8_t *codes,
     }
     /* from GHIP_GEMM_MIN_M rows on, the weights are read once by the MFMA
      * GEMM instead of once per group of <= 4 rows */
-    if (M >= GHIP_GEMM_MIN_M && g_gs_ncu && ghip_fp8_gemm_fits(M, O, K, codes, x))
+    if (M >= GHIP_GEMM_MIN_M && g_gs_ncu && ghip_fp8_gemm_fits(M, O, K, codes, x, y))
         return ghip_launch_fp8_gemm(codes, scales, x, y, M, O, K, exact_dev, g_gs_ncu, ev,
                                     st);
     /* m-groups of up to 4 rows, each as large as the x staging allows */

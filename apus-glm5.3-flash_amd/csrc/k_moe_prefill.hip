@@ -217,14 +217,27 @@ __global__ __launch_bounds__(1024) void k_pf_scatter(
  * c/gmoe.h:217-225 with the numpy-stable sigmoid (c/gmhc.h:157-160) on the
  * hardware exp2 and reciprocal (a few f32 ulps, far below the bf16 step
  * that follows; a tolerance-class result like every GEMM output). */
-__device__ __forceinline__ uint32_t pf_swiglu(float g, float u, float limit) {
+__device__ __forceinline__ uint16_t pf_bf16_bits(float x) {
+    /* the hardware RNE narrow (v_cvt_pk_bf16_f32): the reference's bits for
+     * every finite value, subnormals included, and a quiet NaN for a NaN */
+    return __builtin_bit_cast(uint16_t, (__bf16)x);
+}
+
+__device__ __forceinline__ float pf_bf16_round(float x) {
+    return __uint_as_float((uint32_t)pf_bf16_bits(x) << 16);
+}
+
+/* SwiGLU of the fp32 gate / up accumulators: each rounded to bf16 first,
+ * then the clamps (compares, so a NaN stays NaN as in the reference) */
+__device__ __forceinline__ uint16_t pf_swiglu(float accg, float accu, float limit) {
+    float g = pf_bf16_round(accg), u = pf_bf16_round(accu);
     if (g > limit) g = limit;
     if (u > limit) u = limit;
     else if (u < -limit) u = -limit;
     const float e = __expf(-fabsf(g));
     const float r = __frcp_rn(1.0f + e);
     const float sg = g >= 0.0f ? r : e * r;
-    return ghip_bf16_bits(ghip_bf16_round(g * sg) * u);
+    return pf_bf16_bits(pf_bf16_round(g * sg) * u);
 }
 
 /* 8 codes (two dwords) -> one bf16x8 MFMA operand. */
@@ -511,27 +524,72 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
     stage(nst - 1, std::false_type{}, std::false_type{});
 
     /* epilogue: lane (n, h), register i of row block rb holds output row
-     * rb*32 + 8*(i/4) + 4*h + i%4, column n of each slot */
-    const uint32_t c0 = t.cb0 + 32 * cw + n, c1 = t.cb1 + 32 * cw + n;
+     * rowbase + rb*32 + 8*(i/4) + 4*h + i%4, column n of each slot */
+    const uint32_t rowbase = hr * NRBW * 32;
+    if constexpr (MODE == 2) {
+        const uint32_t c0 = t.cb0 + 32 * cw + n, c1 = t.cb1 + 32 * cw + n;
 #pragma unroll
-    for (int rb = 0; rb < (int)NRBW; rb++) {
+        for (int rb = 0; rb < (int)NRBW; rb++) {
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const uint32_t r = (hr * NRBW + rb) * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
-            if (r < t.rows) {
-                uint16_t *o = t.out + (size_t)(t.row0 + r) * t.N;
-                if (MODE == 0) {
-                    const float g = ghip_bf16_round(a0[rb][i]);
-                    const float u = ghip_bf16_round(a1[rb][i]);
-                    o[c0] = (uint16_t)pf_swiglu(g, u, t.limit);
-                } else if (MODE == 2) {
+            for (int i = 0; i < 16; i++) {
+                const uint32_t r = rowbase + rb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+                if (r < t.rows) {
                     float *of = t.outf + (size_t)(t.row0 + r) * t.N;
                     of[c0] = a0[rb][i];
                     of[c1] = a1[rb][i];
-                } else {
-                    o[c0] = (uint16_t)ghip_bf16_bits(a0[rb][i]);
-                    o[c1] = (uint16_t)ghip_bf16_bits(a1[rb][i]);
                 }
+            }
+        }
+    } else {
+        /* Staged through a wave-private LDS area so the stores are
+         * row-contiguous 16-byte vectors: every wave's reads of the ring
+         * are done first (the area overlaps the ring). MODE 0 stages the
+         * wave's 32 h columns (64 B per row), MODE 1 its two 32-column
+         * groups c0 | c1 (128 B per row). A row r sits at r ^ ((r >> 2) & 1)
+         * (MODE 0) or its two 64-byte halves swap when (r >> 2) & 1
+         * (MODE 1), so lanes h = 0 and 1 (rows r and r + 4) write to
+         * different banks. */
+        constexpr uint32_t RW = NRBW * 32, RB = MODE == 0 ? 64 : 128;
+        __builtin_amdgcn_s_waitcnt(0xc07f);            /* lgkmcnt(0) */
+        __builtin_amdgcn_s_barrier();
+        uint8_t *sw = lds + wv * (RW * RB);
+#pragma unroll
+        for (int rb = 0; rb < (int)NRBW; rb++) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const uint32_t r = rb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+                if (MODE == 0) {
+                    const uint32_t pr = r ^ ((r >> 2) & 1u);
+                    *(uint16_t *)(sw + pr * 64u + n * 2u) = pf_swiglu(a0[rb][i], a1[rb][i], t.limit);
+                } else {
+                    const uint32_t x = ((r >> 2) & 1u) * 64u;
+                    *(uint16_t *)(sw + r * 128u + ((n * 2u) ^ x)) = pf_bf16_bits(a0[rb][i]);
+                    *(uint16_t *)(sw + r * 128u + ((64u + n * 2u) ^ x)) = pf_bf16_bits(a1[rb][i]);
+                }
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);            /* the wave's own LDS writes */
+        __builtin_amdgcn_wave_barrier();
+        const uint32_t p = lane & 3u;
+        if (MODE == 0) {
+            /* lane: row lane/4 + 16j, 16 bytes at column 8p of the wave's 32 */
+            uint16_t *ob = t.out + (size_t)(t.row0 + rowbase) * t.N + t.cb0 + 32 * cw + 8 * p;
+#pragma unroll
+            for (int j = 0; j < (int)RW / 16; j++) {
+                const uint32_t rr = (lane >> 2) + 16u * j, prr = rr ^ ((rr >> 2) & 1u);
+                const ghip_u32x4 v = *(const ghip_u32x4 *)(sw + prr * 64u + p * 16u);
+                if (rowbase + rr < t.rows) *(ghip_u32x4 *)(ob + (size_t)rr * t.N) = v;
+            }
+        } else {
+            /* lane: row lane/8 + 8j, group (lane/4) & 1, 16 bytes at column 8p */
+            const uint32_t gs = (lane >> 2) & 1u;
+            uint16_t *ob = t.out + (size_t)(t.row0 + rowbase) * t.N + (gs ? t.cb1 : t.cb0)
+                         + 32 * cw + 8 * p;
+#pragma unroll
+            for (int j = 0; j < (int)RW / 8; j++) {
+                const uint32_t rr = (lane >> 3) + 8u * j, x = ((rr >> 2) & 1u) * 64u;
+                const ghip_u32x4 v = *(const ghip_u32x4 *)(sw + rr * 128u + ((gs * 64u + p * 16u) ^ x));
+                if (rowbase + rr < t.rows) *(ghip_u32x4 *)(ob + (size_t)rr * t.N) = v;
             }
         }
     }
@@ -913,10 +971,11 @@ extern "C" hipError_t ghip_launch_moe_prefill(const GhipBank *bank,
 }
 
 extern "C" int ghip_fp8_gemm_fits(size_t M, size_t N, size_t K, const void *codes,
-                                  const void *x) {
+                                  const void *x, const void *y) {
     return M > 0 && M <= 0x7fffffffu && N % 256 == 0 && N <= 0x7fffffffu && K % 128 == 0
         && K / 128 <= PF_SCT_MAX && K * 2 * (size_t)M <= 0xffffffffull
-        && ((uintptr_t)codes & 15) == 0 && ((uintptr_t)x & 15) == 0;
+        && ((uintptr_t)codes & 15) == 0 && ((uintptr_t)x & 15) == 0
+        && ((uintptr_t)y & 15) == 0;
 }
 
 /* split-K partials: one device buffer, grown on demand, kept for the
@@ -930,7 +989,7 @@ extern "C" hipError_t ghip_launch_fp8_gemm(const uint8_t *codes, const float *sc
                                            size_t N, size_t K, const uint32_t *exact_dev,
                                            uint32_t n_cu, const hipEvent_t *ev,
                                            hipStream_t st) {
-    if (!ghip_fp8_gemm_fits(M, N, K, codes, x) || n_cu == 0 || n_cu % 8)
+    if (!ghip_fp8_gemm_fits(M, N, K, codes, x, y) || n_cu == 0 || n_cu % 8)
         return hipErrorInvalidValue;
     const size_t nblk = N / 256, nkb = K / 128;
     /* Tile height bm and K splits S: among bm in {256, 128, 64, 32} (no
