@@ -5,6 +5,7 @@ this file. Also builds the test-only CPU checker under oracle/ (make).
 Usage: python build.py   (or __graft_entry__.build())
 """
 import os
+import re
 import subprocess
 import sys
 from concurrent.futures import ThreadPoolExecutor
@@ -28,7 +29,11 @@ CFLAGS = ["-std=c11", "-O2", "-Wall", "-Wextra", "-fPIC", "-ffp-contract=off",
 # not know the feature: harmless); fp contraction pinned off.
 HIPFLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
             "-ffp-contract=off", "-Xclang", "-target-feature", "-Xclang",
-            "-packed-fp32-ops", "-Wno-unused-command-line-argument"] + INC
+            "-packed-fp32-ops", "-Wno-unused-command-line-argument",
+            "-Rpass-analysis=kernel-resource-usage"] + INC
+
+_REMARK = re.compile(r"remark:\s+(Function Name|VGPRs Spill|ScratchSize \[bytes/lane\]"
+                     r"|SGPRs Spill):\s*(\S+)")
 
 
 def _run(cmd):
@@ -39,6 +44,42 @@ def _run(cmd):
     if p.returncode != 0:
         raise RuntimeError("build failed: %s\n%s" % (" ".join(cmd), out))
     return out
+
+
+def resource_usage(out):
+    """Per-kernel {name: {"vgpr_spill", "scratch", "sgpr_spill"}} from the
+    compiler's kernel-resource-usage remarks; the remark lines are dropped
+    from the returned text."""
+    usage, name, keep, ctx = {}, None, [], False
+    for l in out.splitlines():
+        m = _REMARK.search(l)
+        if not m:
+            if "kernel-resource-usage" in l:
+                ctx = True
+            elif not (ctx and re.match(r"\s*\d*\s*\|", l)):
+                ctx = False
+                keep.append(l)
+            continue
+        ctx = True
+        key, val = m.group(1), m.group(2)
+        if key == "Function Name":
+            name = val
+            usage[name] = {}
+        elif name is not None:
+            usage[name][{"VGPRs Spill": "vgpr_spill", "SGPRs Spill": "sgpr_spill"}
+                        .get(key, "scratch")] = int(val)
+    return usage, "\n".join(keep)
+
+
+def check_resources(usage):
+    """A kernel that spills VGPRs or uses scratch memory fails the build
+    (SGPR spills go to VGPR lanes, not memory, and are allowed)."""
+    bad = ["%s: %d VGPR spills, %d B/lane scratch"
+           % (k, u.get("vgpr_spill", 0), u.get("scratch", 0))
+           for k, u in sorted(usage.items())
+           if u.get("vgpr_spill", 0) or u.get("scratch", 0)]
+    if bad:
+        raise RuntimeError("kernels spill to scratch memory:\n  " + "\n  ".join(bad))
 
 
 def build(verbose=False):
@@ -53,10 +94,14 @@ def build(verbose=False):
         o = os.path.join(BUILD, s + ".o")
         jobs.append([HIPCC] + HIPFLAGS + ["-c", os.path.join(CSRC, s), "-o", o])
         objs.append(o)
+    usage = {}
     with ThreadPoolExecutor(max_workers=min(8, len(jobs))) as ex:
         for out in ex.map(_run, jobs):
+            u, out = resource_usage(out)
+            usage.update(u)
             if verbose and out.strip():
                 print(out)
+    check_resources(usage)
     tmp = LIB + ".tmp"
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objs
          + ["-lm"])
