@@ -1,15 +1,14 @@
 /*
  * k_moe.hip — K3: routed-MoE decode for one token (gfx950), and the router.
  *
- * The decode is ONE cooperative persistent launch (one workgroup per CU, all
- * co-resident) with three phases:
+ * The decode is ONE persistent launch (one workgroup per CU, all resident
+ * at once) with three phases:
  *   route    one wave per workgroup (every workgroup routes redundantly, so
  *            none waits for another): the harness routing (stable top-k of
  *            f32 logits, ties -> lower id) or given idx/w, a repeated id
  *            keeping its first slot (c/gmoe.h:309-312). Only the selected
  *            ids are needed to start streaming; the softmax weights and the
- *            ascending-id combine order are computed later, while the
- *            workgroup waits for the device-wide hand-off.
+ *            ascending-id combine order are computed later.
  *   gate/up  per (slot q, 16 rows) the g and u GEMVs over dim with the FP8
  *            dequant fused (bit-exact weights) and the SwiGLU epilogue of
  *            c/gmoe.h:217-225 -> h[q] in HBM.
@@ -18,18 +17,17 @@
  *            combine y = bf16(y + bf16(bf16(o)*w)) (c/gmoe.h:307-320) runs
  *            in-workgroup -- no float atomics, no cross-workgroup reduction,
  *            deterministic.
- * Hand-off of h between the phases: each workgroup, after its gate/up work,
- * makes its h stores visible device-wide (agent-scope release) and bumps a
- * monotone arrival counter; before reading h it issues the first stages of
- * its down weight ring, then waits (bounded) until the counter shows every
- * workgroup of this launch, and acquires. The down weights are therefore
- * already streaming when h becomes readable; there is no kernel boundary.
+ * Hand-off of h between the phases: every h value is stored as one 32-bit
+ * word carrying the value and this launch's tag, with a device-coherent
+ * store; a reader polls the words with device-coherent loads until each
+ * carries the tag (bounded). No fence, counter or kernel boundary is
+ * involved, and a reader needs nothing but the words it reads.
  *
- * Weight streaming: each wave pulls its 16-row chunks (128-wide k, one
+ * Weight streaming: gate/up waves pull their 16-row chunks (128-wide k, one
  * scale block) through a wave-private LDS ring with direct global->LDS
- * loads, so the bytes in flight are not bounded by registers; the GEMV inner
- * step (ghip_chunk_mfma) dequantizes in registers and reduces over k on
- * MFMA with the activation (x or h) from LDS as the A operand.
+ * loads; each down wave issues its first ring stages before it awaits h.
+ * The GEMV inner step dequantizes in registers and reduces over k on MFMA
+ * with the activation (x or h) from LDS as the A operand.
  */
 #include "ghip_device.h"
 #include "ghip_internal.h"
