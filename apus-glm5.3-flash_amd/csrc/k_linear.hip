@@ -299,10 +299,6 @@ __global__ __launch_bounds__(GS_NW * 64, 1) void k_fp8_gemv_stream(
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t n = lane & 15u, g = lane >> 4;
-    for (uint32_t i = tid; i < (uint32_t)M * (K >> 3); i += GS_NW * 64)
-        ((ghip_u32x4 *)xs)[i] = ((const ghip_u32x4 *)X)[i];
-    __syncthreads();
-    const bool exact = !BF && exact_flag != nullptr && *exact_flag != 0u;
     uint8_t *ring = gsl + (((size_t)M * K * 2u + 1023u) & ~(size_t)1023u) +
                     wv * (GS_R * 2048u);
     /* chunk = 128 bytes of each of 16 rows; row stride in bytes */
@@ -312,19 +308,57 @@ __global__ __launch_bounds__(GS_NW * 64, 1) void k_fp8_gemv_stream(
     const uint32_t c0 = part * nch / KS, c1 = (part + 1) * nch / KS, nc = c1 - c0;
     const uint32_t groups = (O + 15) / 16, passes = (groups + GPP - 1) / GPP;
     const uint16_t *xa = xs + (size_t)min(n, (uint32_t)M - 1u) * K + (BF ? 16u : 32u) * g;
+    /* pass ps's row group of this wave: its rows, the DMA offsets (a
+     * partial last group re-reads row O-1, outputs discarded) */
+    auto rows_of = [&](uint32_t ps) {
+        return W + (size_t)(ps * GPP + slot) * 16u * KB;
+    };
+    auto dma_of = [&](uint32_t ps) {
+        return ghip_cdma_offsets(lane, KB, min(15u, O - 1u - (ps * GPP + slot) * 16u));
+    };
+    auto prologue = [&](uint32_t ps) {
+        const uint8_t *rows = rows_of(ps);
+        const ghip_cdma d = dma_of(ps);
+#pragma unroll
+        for (uint32_t i = 0; i + 1 < GS_R; i++)
+            if (i < nc) ghip_cdma_issue(rows, c0 + i, d, ring + i * 2048u);
+    };
+    /* x into LDS without delaying the weight stream: x goes by direct DMA
+     * too (1 KB pieces dealt to the waves, lanes past x re-read its last
+     * vector into the 1 KB-rounded x region), ahead of the first pass's
+     * ring prologue; that prologue issues a fixed count of loads (group and
+     * chunk clamped to valid ones: a stage past the wave's chunks lands in a
+     * ring slot this pass never reads and only makes the ring waits below
+     * stricter), so waiting until no more than that count is in flight
+     * means this wave's x pieces have landed */
+    {
+        const uint32_t nvec = (uint32_t)M * (K >> 3), nxc = (nvec + 63u) >> 6;
+        for (uint32_t c = wv; c < nxc; c += GS_NW)
+            ghip_dma16(X + (size_t)min(c * 64u + lane, nvec - 1u) * 8u, gsl + c * 1024u);
+        const uint32_t grp0 = min(blockIdx.x * GPP + slot, groups - 1u);
+        const uint8_t *rows = W + (size_t)grp0 * 16u * KB;
+        const ghip_cdma d = ghip_cdma_offsets(lane, KB, min(15u, O - 1u - grp0 * 16u));
+#pragma unroll
+        for (uint32_t i = 0; i + 1 < GS_R; i++)
+            ghip_cdma_issue(rows, min(c0 + i, nch - 1u), d, ring + i * 2048u);
+        GHIP_VMCNT(2 * (GS_R - 1));
+    }
+    /* a bare barrier: __syncthreads() would also wait for the prologue
+     * (its workgroup-scope release waits for every load in flight) */
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    const bool exact = !BF && exact_flag != nullptr && *exact_flag != 0u;
     for (uint32_t ps = blockIdx.x; ps < passes; ps += gridDim.x) {
         const uint32_t grp = ps * GPP + slot;
         const bool live = grp < groups;
         if (live) {
             /* a wave with no chunks (K < KS * 128) contributes zeros */
             const uint32_t row0 = grp * 16;
-            const uint8_t *rows = W + (size_t)row0 * KB;
-            /* a partial last group re-reads row O-1 (outputs discarded) */
-            const ghip_cdma d = ghip_cdma_offsets(lane, KB, min(15u, O - 1u - row0));
+            const uint8_t *rows = rows_of(ps);
+            const ghip_cdma d = dma_of(ps);
             const float *srow = BF ? nullptr : S + (size_t)(row0 >> 7) * nkb;
-#pragma unroll
-            for (uint32_t i = 0; i + 1 < GS_R; i++)
-                if (i < nc) ghip_cdma_issue(rows, c0 + i, d, ring + i * 2048u);
+            if (ps != blockIdx.x) prologue(ps);
             ghip_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
             for (uint32_t t = 0; t < nc; t++) {
                 ghip_wait_stages<2, GS_R - 2>(nc - 1 - t);
