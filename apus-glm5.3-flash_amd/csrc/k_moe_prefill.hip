@@ -59,6 +59,8 @@ typedef float ghip_f32x16 __attribute__((ext_vector_type(16)));
 #define PF_RING (3 * PF_STAGE)                  /* 144 KB ring */
 #define PF_SCT_MAX 128           /* k blocks in the per-tile scale table (K <= 16384) */
 #define PF_LDS (PF_RING + PF_SCT_MAX * 8)       /* ring + scale table */
+#define PF_WB (256 * 128)                       /* 32 KB weight block: 256 rows x 128 k */
+#define PF_LDS_WB (3 * PF_A_STAGE + 2 * PF_WB)  /* the full-tile 8-wave body: 160 KB */
 #define PF_MAXK 16               /* max top-k per token */
 #define PF_MAXE 1024             /* max experts in a bank */
 
@@ -300,9 +302,17 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
      * keep more weight bytes in flight (3, 4, 6, 7 stages for 8, 4, 2, 1
      * row blocks) */
     constexpr uint32_t ASTG = NRB * 32 * PF_BK * 2;
-    constexpr uint32_t STG = ASTG + PF_W_STAGE;
-    constexpr uint32_t NS = PF_RING / STG < 8 ? PF_RING / STG : 8;
+    /* WB (the full 256-row tile with 8 waves, modes 0 and 1): the weights
+     * come in 128-wide k blocks (32 KB: 256 rows x one full 128-byte line
+     * each, so every load instruction reads 8 whole lines instead of 16
+     * half lines) through their own 2-block ring after the 3-stage A ring,
+     * filling all 160 KB; the scales come by scalar loads (no table) */
+    constexpr bool WB = NW == 8 && NRB == 8 && MODE < 2 && !EXACT;
+    constexpr uint32_t STG = WB ? ASTG : ASTG + PF_W_STAGE;
+    constexpr uint32_t NS = WB ? 3u : (PF_RING / STG < 8 ? PF_RING / STG : 8);
+    constexpr uint32_t NWW = WB ? (PF_WB / 1024) / NW : 0;  /* block loads per wave */
     static_assert(NS >= 2 && LPS * (NS - 1) <= 63, "ring depth vs vmcnt range");
+    static_assert(!WB || NS * ASTG + 2 * PF_WB == PF_LDS_WB, "WB layout");
     /* opaque thread id: keeps the lane-derived address math of this body
      * inside the persistent item loop instead of hoisted and held live
      * across items for every body */
@@ -321,8 +331,10 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
      * the tile's start until the whole prologue landed) */
     const uint32_t nsc = t.KS >> 7, sb = tid < nsc ? tid : nsc - 1;
     ghip_f32x2 sv;
-    sv[0] = t.sr0[sb];
-    sv[1] = t.sr1[sb];
+    if constexpr (!WB) {
+        sv[0] = t.sr0[sb];
+        sv[1] = t.sr1[sb];
+    }
 
     /* --- DMA sources: a wave-uniform base (SGPRs; stage j adds j*64
      * elements) plus a 32-bit per-lane offset, so each load is one
@@ -339,12 +351,28 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
         const uint32_t p = (lane & 7) ^ ((r >> 1) & 7);
         aofs[i] = src * K * 2u + 16u * p;
     }
-    if (tid < nsc) sct[tid] = sv;
-    for (uint32_t b = tid + NW * 64; b < nsc; b += NW * 64) {
-        ghip_f32x2 v;
-        v[0] = t.sr0[b];
-        v[1] = t.sr1[b];
-        sct[b] = v;
+    if constexpr (!WB) {
+        if (tid < nsc) sct[tid] = sv;
+        for (uint32_t b = tid + NW * 64; b < nsc; b += NW * 64) {
+            ghip_f32x2 v;
+            v[0] = t.sr0[b];
+            v[1] = t.sr1[b];
+            sct[b] = v;
+        }
+    }
+    /* WB weight block loads: instruction b of wave wv fills LDS rows 8q ..
+     * 8q + 7 of the block (q = wv + 8b; 128 bytes each), rows of slot hr
+     * (the same logical row order as the stage layout: row 64i + 32s + c is
+     * column 32i + c of slot s's block), piece p of row r at p ^ ((r >> 1)
+     * & 7); block m adds 128 m bytes */
+    /* (row 8q + l/8 with q = wv + 8b is 64b + r0, r0 = 8wv + l/8 < 64: column
+     * 32b + (r0 & 31), swizzle (r0 >> 1) & 7 -- load b adds 32b rows) */
+    const uint8_t *wsrcB = nullptr;
+    uint32_t wofsB = 0;
+    if constexpr (WB) {
+        wsrcB = (hr ? t.w1 : t.w0) + (size_t)(hr ? t.cb1 : t.cb0) * K;
+        const uint32_t r0 = 8u * wv + (lane >> 3);
+        wofsB = (r0 & 31u) * K + 16u * ((lane & 7u) ^ ((r0 >> 1) & 7u));
     }
     /* weight load i of wave wv, lane l: LDS weight row 64i + 16wv + l/4,
      * i.e. slot (wv >> 1) & 1 (uniform), column 32i + 16(wv & 1) + l/4 of
@@ -381,18 +409,52 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
         issue_part(std::integral_constant<int, 2>{}, j, b);
         issue_part(std::integral_constant<int, 3>{}, j, b);
     };
+    /* WB: half P (of 2) of stage j's A loads / of weight block m's loads */
+    auto issue_a = [&](auto part_c, uint32_t j) {
+        constexpr int P = decltype(part_c)::value;
+        uint8_t *st = lds + (j % NS) * ASTG;
+        const uint8_t *aj = abase + (size_t)j * PF_BK * 2;
+#pragma unroll
+        for (int i = 0; i < (int)NA; i++)
+            if (i % 2 == P) ghip_dma16(aj + aofs[i], st + alds[i]);
+    };
+    auto issue_w = [&](auto part_c, uint32_t m) {
+        constexpr int P = decltype(part_c)::value;
+        uint8_t *wb = lds + NS * ASTG + (m & 1u) * PF_WB;
+        const uint8_t *wm = wsrcB + (size_t)m * 128u;
+#pragma unroll
+        for (int b = 0; b < (int)NWW; b++)
+            if (b % 2 == P)
+                ghip_dma16(wm + (size_t)(32u * b) * K + wofsB, wb + (wv + NW * b) * 1024);
+    };
 
     /* --- operand read offsets inside a stage --------------------------- */
-    uint32_t aoff[4], boff0[2], boff1[2];
+    /* slot 1's rows follow slot 0's 32 rows later in both layouts (the
+     * swizzle depends on n only): one offset register per u, the slot-1
+     * read at a constant distance BD */
+    constexpr uint32_t BD = WB ? 32u * 128u : 32u * 64u;
+    uint32_t aoff[4], boff0[2];
 #pragma unroll
     for (int s = 0; s < 4; s++)
         aoff[s] = n * 128 + 16 * (((4 * h) | s) ^ ((n >> 1) & 7));
 #pragma unroll
     for (int u = 0; u < 2; u++) {
-        const uint32_t ph = ((2 * h + u) ^ ((n >> 2) & 3)) * 16;
-        boff0[u] = ASTG + (64 * cw + n) * 64 + ph;
-        boff1[u] = ASTG + (64 * cw + 32 + n) * 64 + ph;
+        if constexpr (WB) {
+            /* in the weight block, from its base; an odd stage reads the
+             * other 64 bytes of each line: offset ^ 64 (piece ^ 4) */
+            const uint32_t ph = ((2 * h + u) ^ ((n >> 1) & 7)) * 16;
+            boff0[u] = (64 * cw + n) * 128 + ph;
+        } else {
+            const uint32_t ph = ((2 * h + u) ^ ((n >> 2) & 3)) * 16;
+            boff0[u] = ASTG + (64 * cw + n) * 64 + ph;
+        }
     }
+    /* B codes of stage j: WB reads weight block j / 2, else the stage */
+    auto bsrc = [&](uint32_t j) -> const uint8_t * {
+        if constexpr (WB) return lds + NS * ASTG + ((j >> 1) & 1u) * PF_WB;
+        else return lds + (j % NS) * STG;
+    };
+    auto bpar = [&](uint32_t j) -> uint32_t { return WB ? (j & 1u) * 64u : 0u; };
 
     ghip_f32x16 a0[NRBW], a1[NRBW];
     /* this wave's first row block in the stage's A rows */
@@ -408,22 +470,40 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
      * tile's last stage, so none is left in flight when the tile ends: the
      * next item (possibly another body with another LDS layout) starts on
      * a quiet ring. */
+    ghip_f32x2 sc, scn;                          /* WB: scales of this / the next k block */
+    if constexpr (WB) {
+        /* weight block 0 first, then A stages 0 and 1 (nst >= 2): waiting
+         * for stage 0's A loads covers block 0 */
+        issue_w(std::integral_constant<int, 0>{}, 0u);
+        issue_w(std::integral_constant<int, 1>{}, 0u);
+        issue_a(std::integral_constant<int, 0>{}, 0u);
+        issue_a(std::integral_constant<int, 1>{}, 0u);
+        issue_a(std::integral_constant<int, 0>{}, 1u);
+        issue_a(std::integral_constant<int, 1>{}, 1u);
+        sc[0] = ghip_sload(t.sr0, 0);
+        sc[1] = ghip_sload(t.sr1, 0);
+        const uint32_t b1i = nst > 2 ? 1u : 0u;
+        scn[0] = ghip_sload(t.sr0, b1i);
+        scn[1] = ghip_sload(t.sr1, b1i);
+        GHIP_VMCNT(NA);
+    } else {
 #pragma unroll
-    for (uint32_t i = 0; i + 1 < NS; i++)
-        if (i < nst) issue(i, i);
-    ghip_wait_stages<LPS, NS - 2>(nst - 1);
+        for (uint32_t i = 0; i + 1 < NS; i++)
+            if (i < nst) issue(i, i);
+        ghip_wait_stages<LPS, NS - 2>(nst - 1);
+    }
     __builtin_amdgcn_s_waitcnt(0xc07f);          /* lgkmcnt(0): scale table */
     __builtin_amdgcn_s_barrier();
     ghip_u32x4 q0[2], q1[2];
-    ghip_f32x2 sc;
     ghip_bf16x8 av[NRBW], an[NRBW], b0, b1, nb0, nb1;
     {
         const uint8_t *st = lds;
-        sc = sct[0];
+        const uint8_t *sb0 = bsrc(0);
+        if constexpr (!WB) sc = sct[0];
 #pragma unroll
         for (int u = 0; u < 2; u++) {
-            q0[u] = *(const ghip_u32x4 *)(st + boff0[u]);
-            q1[u] = *(const ghip_u32x4 *)(st + boff1[u]);
+            q0[u] = *(const ghip_u32x4 *)(sb0 + boff0[u]);
+            q1[u] = *(const ghip_u32x4 *)(sb0 + boff0[u] + BD);
         }
 #pragma unroll
         for (int rb = 0; rb < (int)NRBW; rb++)
@@ -437,17 +517,28 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
      * j + NS - 1 exists and is loaded during this one. Branch-free inside,
      * so each step is one scheduling region in which the next operands' LDS
      * reads and dequant interleave with the MFMAs. */
-    auto stage = [&](uint32_t j, auto next_c, auto refill_c) {
+    auto stage = [&](uint32_t j, auto next_c, auto refill_c, auto par_c) {
         constexpr bool NEXT = decltype(next_c)::value;
         constexpr bool REFILL = decltype(refill_c)::value;
+        constexpr int PAR = decltype(par_c)::value;       /* WB: j % 2 */
         const uint8_t *st = lds + (j % NS) * STG;
         const uint32_t ld = j + NS - 1;
 #pragma unroll
         for (int s = 0; s < 4; s++) {
-            if (REFILL && s == 0) issue_part(std::integral_constant<int, 0>{}, ld, ld);
-            if (REFILL && s == 1) issue_part(std::integral_constant<int, 1>{}, ld, ld);
-            if (REFILL && s == 2) issue_part(std::integral_constant<int, 2>{}, ld, ld);
-            if (REFILL && s == 3) issue_part(std::integral_constant<int, 3>{}, ld, ld);
+            if constexpr (WB) {
+                /* an even stage issues weight block j/2 + 1 (steps 0, 1)
+                 * ahead of stage j + 2's A rows (steps 2, 3), so waiting for
+                 * those A rows covers the block too */
+                if (REFILL && PAR == 0 && s == 0) issue_w(std::integral_constant<int, 0>{}, (j >> 1) + 1u);
+                if (REFILL && PAR == 0 && s == 1) issue_w(std::integral_constant<int, 1>{}, (j >> 1) + 1u);
+                if (REFILL && s == 2) issue_a(std::integral_constant<int, 0>{}, j + 2u);
+                if (REFILL && s == 3) issue_a(std::integral_constant<int, 1>{}, j + 2u);
+            } else {
+                if (REFILL && s == 0) issue_part(std::integral_constant<int, 0>{}, ld, ld);
+                if (REFILL && s == 1) issue_part(std::integral_constant<int, 1>{}, ld, ld);
+                if (REFILL && s == 2) issue_part(std::integral_constant<int, 2>{}, ld, ld);
+                if (REFILL && s == 3) issue_part(std::integral_constant<int, 3>{}, ld, ld);
+            }
             if (s < 3) {
                 /* step s+1 of this stage: A rows from LDS, B codes already
                  * in registers */
@@ -464,17 +555,36 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
                  * ring) after which buffer j % NS is free for stage j+NS.
                  * Stages up to min(j + NS - 1, nst - 1) are issued by now,
                  * in order: min(NS - 2, nst - 2 - j) of them after j+1 */
-                if (REFILL) GHIP_VMCNT(LPS * (NS - 2));
-                else ghip_wait_stages<LPS, NS - 2>(nst - 2 - j);
+                if constexpr (WB) {
+                    if (!REFILL) GHIP_VMCNT(0);
+                    else if (PAR == 0) GHIP_VMCNT(NA + NWW);
+                    else GHIP_VMCNT(NA);
+                } else {
+                    if (REFILL) GHIP_VMCNT(LPS * (NS - 2));
+                    else ghip_wait_stages<LPS, NS - 2>(nst - 2 - j);
+                }
                 __builtin_amdgcn_s_waitcnt(0xc07f);
                 __builtin_amdgcn_s_barrier();
                 __builtin_amdgcn_sched_barrier(0);
                 const uint8_t *sn = lds + ((j + 1) % NS) * STG;
-                sc = sct[(j + 1) >> 1];
+                const uint8_t *sbn = bsrc(j + 1);
+                const uint32_t bx = bpar(j + 1);
+                if constexpr (WB) {
+                    if (PAR == 1) {                       /* stage j + 1 opens k block (j+1)/2 */
+                        sc = scn;
+                        const uint32_t mb = ((j + 1) >> 1) + 1u;
+                        if (mb < (nst >> 1)) {
+                            scn[0] = ghip_sload(t.sr0, mb);
+                            scn[1] = ghip_sload(t.sr1, mb);
+                        }
+                    }
+                } else {
+                    sc = sct[(j + 1) >> 1];
+                }
 #pragma unroll
                 for (int u = 0; u < 2; u++) {
-                    q0[u] = *(const ghip_u32x4 *)(sn + boff0[u]);
-                    q1[u] = *(const ghip_u32x4 *)(sn + boff1[u]);
+                    q0[u] = *(const ghip_u32x4 *)(sbn + (boff0[u] ^ bx));
+                    q1[u] = *(const ghip_u32x4 *)(sbn + (boff0[u] ^ bx) + BD);
                 }
 #pragma unroll
                 for (int rb = 0; rb < (int)NRBW; rb++)
@@ -518,10 +628,23 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
             b1 = nb1;
         }
     };
-    uint32_t j = 0;
-    for (; j + NS - 1 < nst; j++) stage(j, std::true_type{}, std::true_type{});
-    for (; j + 1 < nst; j++) stage(j, std::true_type{}, std::false_type{});
-    stage(nst - 1, std::false_type{}, std::false_type{});
+    using P0 = std::integral_constant<int, 0>;
+    using P1 = std::integral_constant<int, 1>;
+    if constexpr (WB) {
+        /* stage pairs (nst is even: K % 128 == 0) */
+        uint32_t j = 0;
+        for (; j + 2 < nst; j += 2) {
+            stage(j, std::true_type{}, std::true_type{}, P0{});
+            stage(j + 1, std::true_type{}, std::true_type{}, P1{});
+        }
+        stage(nst - 2, std::true_type{}, std::false_type{}, P0{});
+        stage(nst - 1, std::false_type{}, std::false_type{}, P1{});
+    } else {
+        uint32_t j = 0;
+        for (; j + NS - 1 < nst; j++) stage(j, std::true_type{}, std::true_type{}, P0{});
+        for (; j + 1 < nst; j++) stage(j, std::true_type{}, std::false_type{}, P0{});
+        stage(nst - 1, std::false_type{}, std::false_type{}, P0{});
+    }
 
     /* epilogue: lane (n, h), register i of row block rb holds output row
      * rowbase + rb*32 + 8*(i/4) + 4*h + i%4, column n of each slot */
@@ -938,7 +1061,7 @@ extern "C" hipError_t ghip_launch_moe_prefill(const GhipBank *bank,
     GHIP_LAUNCH(nullptr, e1, k_pf_scatter, dim3(nch), dim3(1024), 16 * E * 4, st,
                 ws->eid, (uint32_t)P, E, ws->cnt, ws->perm, ws->pos);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    const size_t lds = PF_LDS;
+    const size_t lds = PF_LDS, lds8 = PF_LDS_WB;
     (void)mt;
     const uint32_t g0 = ws->n_cu, g1 = ws->n_cu;
     /* two waves per SIMD when the tiles are mostly full (on average at
@@ -947,7 +1070,7 @@ extern "C" hipError_t ghip_launch_moe_prefill(const GhipBank *bank,
      * per SIMD, which wastes no MFMAs on a half-empty row split */
     const bool full = P >= (size_t)E * (PF_BM / 2);
     if (full)
-        GHIP_LAUNCH(e2, e3, (k_pf_gemm<0, 8>), dim3(g0), dim3(512), lds, st, *bank,
+        GHIP_LAUNCH(e2, e3, (k_pf_gemm<0, 8>), dim3(g0), dim3(512), lds8, st, *bank,
                     x, ws->perm, (const uint4 *)ws->tiles, ws->hdr, inter / 128,
                     (uint32_t)topk, limit, ws->h);
     else
@@ -956,7 +1079,7 @@ extern "C" hipError_t ghip_launch_moe_prefill(const GhipBank *bank,
                     (uint32_t)topk, limit, ws->h);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (full)
-        GHIP_LAUNCH(e4, e5, (k_pf_gemm<1, 8>), dim3(g1), dim3(512), lds, st, *bank,
+        GHIP_LAUNCH(e4, e5, (k_pf_gemm<1, 8>), dim3(g1), dim3(512), lds8, st, *bank,
                     ws->h, ws->perm, (const uint4 *)ws->tiles, ws->hdr, dim / 256,
                     (uint32_t)topk, limit, ws->o);
     else
@@ -1136,13 +1259,13 @@ extern "C" hipError_t ghip_pf_scratch_ws(int device, size_t pairs, uint32_t n_ex
 }
 
 extern "C" hipError_t ghip_moe_prefill_init(void) {
-    const int lds = PF_LDS;
     const void *ks[5] = {(const void *)k_pf_gemm<0, 8>, (const void *)k_pf_gemm<0, 4>,
                          (const void *)k_pf_gemm<1, 8>, (const void *)k_pf_gemm<1, 4>,
                          (const void *)k_fp8_gemm};
+    const int lds[5] = {PF_LDS_WB, PF_LDS, PF_LDS_WB, PF_LDS, PF_LDS};
     for (int i = 0; i < 5; i++) {
         hipError_t e = hipFuncSetAttribute(ks[i], hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           lds);
+                                           lds[i]);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
