@@ -237,7 +237,13 @@ __device__ __forceinline__ uint16_t pf_swiglu(float accg, float accu, float limi
     if (u > limit) u = limit;
     else if (u < -limit) u = -limit;
     const float e = __expf(-fabsf(g));
-    const float r = __frcp_rn(1.0f + e);
+    /* 1 / (1 + e) for 1 + e in (1, 2]: the hardware reciprocal (1 ulp) and
+     * one Newton step with fused multiply-adds, which lands on the
+     * correctly rounded value (the IEEE division sequence costs ~10
+     * instructions per element of the epilogue) */
+    const float d = 1.0f + e;
+    const float r0 = __builtin_amdgcn_rcpf(d);
+    const float r = __builtin_fmaf(__builtin_fmaf(-d, r0, 1.0f), r0, r0);
     const float sg = g >= 0.0f ? r : e * r;
     return pf_bf16_bits(pf_bf16_round(g * sg) * u);
 }
