@@ -25,7 +25,8 @@
  *
  * Weight streaming: gate/up waves pull their 16-row chunks (128-wide k, one
  * scale block) through a wave-private LDS ring with direct global->LDS
- * loads; each down wave issues its first ring stages before it awaits h.
+ * loads; each down wave issues its first ring stages, then awaits its own
+ * slot's h (no workgroup barrier) and streams its rows as soon as it is in.
  * The GEMV inner step dequantizes in registers and reduces over k on MFMA
  * with the activation (x or h) from LDS as the A operand.
  */
@@ -182,7 +183,7 @@ struct MdShared {
     float lg[MD_MAXK];           /* logits path: slot q's logit */
     int32_t te[MD_MAXK];
     float tw[MD_MAXK];
-    uint32_t nsel, go;
+    uint32_t nsel;
     float red[GU_IPW][2][2][16];
     float oq[MD_MAXK][16];
 };
@@ -416,26 +417,25 @@ __device__ __forceinline__ void md_combine(const MdShared &sh, uint32_t r0,
     }
 }
 
-/* h of slots [base, base + m) into LDS (hs [m][inter] bf16) from the tagged
- * words hw (value in bits 0..15, the writing launch's tag in 16..31). Every
- * thread loads its words with device-coherent loads and re-polls the ones
- * that do not carry this launch's tag yet (their gate/up item is still
- * running on another CU), all waves at most MD_SPIN_MAX rounds. Returns
- * false (after a workgroup barrier, the same in every thread) when a word
- * is still missing then. */
-__device__ __forceinline__ bool md_stage_h(const uint32_t *hw, uint32_t base, uint32_t m,
-                                           uint32_t inter, uint32_t tag, uint16_t *hs,
-                                           MdShared &sh) {
-    constexpr uint32_t NT = MD_NW * 64, PER = 8;
-    const uint32_t tid = threadIdx.x, n = m * inter;
-    const uint32_t *src = hw + (size_t)base * inter;
-    bool ok = true;
-    for (uint32_t i0 = 0; i0 < n; i0 += NT * PER) {
+/* h of slot q into LDS (hs [inter] bf16) by the calling wave alone, from
+ * the tagged words hw (value in bits 0..15, the writing launch's tag in
+ * 16..31): the lanes load their words with device-coherent loads and
+ * re-poll the ones that do not carry this launch's tag yet (their gate/up
+ * item is still running on another CU), at most MD_SPIN_MAX rounds.
+ * Returns false (the same in every lane) when a word is still missing
+ * then. No workgroup barrier: each wave goes on to its own slot's rows as
+ * soon as that slot's h is in. */
+__device__ __forceinline__ bool md_stage_h_wave(const uint32_t *hw, uint32_t q, uint32_t inter,
+                                                uint32_t tag, uint16_t *hs) {
+    constexpr uint32_t PER = 16;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t *src = hw + (size_t)q * inter;
+    for (uint32_t i0 = 0; i0 < inter; i0 += 64u * PER) {
         uint32_t v[PER];
 #pragma unroll
         for (uint32_t u = 0; u < PER; u++) {
-            const uint32_t i = i0 + u * NT + tid;
-            v[u] = __hip_atomic_load(src + (i < n ? i : n - 1), __ATOMIC_RELAXED,
+            const uint32_t i = i0 + u * 64u + lane;
+            v[u] = __hip_atomic_load(src + (i < inter ? i : inter - 1u), __ATOMIC_RELAXED,
                                      __HIP_MEMORY_SCOPE_AGENT);
         }
         /* the wave polls until all its words carry the tag (uniform exit) */
@@ -443,34 +443,26 @@ __device__ __forceinline__ bool md_stage_h(const uint32_t *hw, uint32_t base, ui
             uint32_t miss = 0;
 #pragma unroll
             for (uint32_t u = 0; u < PER; u++) {
-                const uint32_t i = i0 + u * NT + tid;
-                miss |= (i < n && (v[u] >> 16) != tag) ? 1u << u : 0u;
+                const uint32_t i = i0 + u * 64u + lane;
+                miss |= (i < inter && (v[u] >> 16) != tag) ? 1u << u : 0u;
             }
             if (!__builtin_amdgcn_readfirstlane((uint32_t)(__ballot(miss != 0u) != 0ull)))
                 break;
-            if (it >= MD_SPIN_MAX) {
-                ok = false;
-                break;
-            }
+            if (it >= MD_SPIN_MAX) return false;
             __builtin_amdgcn_s_sleep(4);
 #pragma unroll
             for (uint32_t u = 0; u < PER; u++)
                 if ((miss >> u) & 1u)
-                    v[u] = __hip_atomic_load(src + i0 + u * NT + tid, __ATOMIC_RELAXED,
+                    v[u] = __hip_atomic_load(src + i0 + u * 64u + lane, __ATOMIC_RELAXED,
                                              __HIP_MEMORY_SCOPE_AGENT);
         }
 #pragma unroll
         for (uint32_t u = 0; u < PER; u++) {
-            const uint32_t i = i0 + u * NT + tid;
-            if (i < n) hs[i] = (uint16_t)v[u];
+            const uint32_t i = i0 + u * 64u + lane;
+            if (i < inter) hs[i] = (uint16_t)v[u];
         }
-        if (!ok) break;
     }
-    if (tid == 0) sh.go = 1u;
-    __syncthreads();
-    if (!ok) sh.go = 0u;
-    __syncthreads();
-    return __builtin_amdgcn_readfirstlane(sh.go) != 0u;
+    return true;
 }
 
 /* ------------------------------------------------------------------------ */
@@ -525,23 +517,24 @@ __global__ __launch_bounds__(MD_NW * 64, 1) void k_moe_decode(
     for (uint32_t rg = blockIdx.x; rg * MD_T < dim; rg += gridDim.x) {
         const uint32_t r0 = rg * MD_T;
         for (uint32_t base = 0; base < nsel; base += MD_NW) {
-            const uint32_t m = nsel - base < MD_NW ? nsel - base : MD_NW;
             /* the weight ring's first stages stream while h is awaited */
             md_down_prologue(bank, sh, r0, base, ring);
-            /* h of this pass's slots (once when all slots fit one pass) */
-            if (base > 0 || rg == blockIdx.x || nsel > MD_NW) {
-                if (!md_stage_h(hw, base, m, inter, tag, hs, sh)) {
-                    if (tid == 0) atomicOr(err, 4u);
-                    GHIP_VMCNT(0);                /* drain the ring before leaving */
-                    return;
-                }
+            /* wave w: h of slot base + w (once when all slots fit one
+             * pass), then at once its down rows; a wave whose wait runs
+             * out flags the error and computes nothing */
+            bool ok = true;
+            if (base + wv < nsel && (base > 0 || rg == blockIdx.x || nsel > MD_NW))
+                ok = md_stage_h_wave(hw, base + wv, inter, tag, hs + (size_t)wv * inter);
+            if (ok) {
+                md_phase_down(bank, sh, r0, base, hs, ring);
+            } else {
+                if ((tid & 63u) == 0) atomicOr(err, 4u);
+                GHIP_VMCNT(0);                    /* drain the ring */
             }
-            GHIP_VMCNT(0);
-            __syncthreads();
-            md_phase_down(bank, sh, r0, base, hs, ring);
             __syncthreads();
         }
         md_combine(sh, r0, out);
+        __syncthreads();                          /* sh.oq is reused by the next rows */
     }
 }
 

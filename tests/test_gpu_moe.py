@@ -198,6 +198,38 @@ def test_moe_decode_vs_oracle(small, k):
         assert np.array_equal(out, out2), "run-to-run determinism"
 
 
+@pytest.mark.parametrize("dim,inter,k", [(256, 128, 12), (4352, 128, 4), (4352, 256, 11)])
+def test_moe_decode_multipass(ghip, dim, inter, k):
+    """The decode's second passes: more than 8 slots (the down phase takes
+    the slots 8 at a time per workgroup) and more 16-row output groups than
+    workgroups (a workgroup takes a second row group, reusing its staged
+    h), against the oracle and run to run."""
+    E = 16
+    rng = np.random.default_rng(dim + k)
+    slabs = random_slabs(E, dim, inter, rng, nan_codes_in=(5,))
+    s = open_store(ghip, E, dim, inter)
+    try:
+        for e, sl in enumerate(slabs):
+            assert ghip.apus_ghip_store_put(s, e, O.ptr(sl), sl.nbytes) == 0
+        for trial in range(2):
+            x = O.f32_to_bf16(rng.standard_normal(dim).astype(np.float32))
+            idx = rng.permutation(E)[:k].astype(np.int32)
+            w = rng.uniform(0.01, 1.0, k).astype(np.float32)
+            out = np.empty(dim, np.uint16)
+            assert ghip.apus_ghip_moe_decode(s, O.ptr(x), O.ptr(idx), O.ptr(w), k,
+                                             O.ptr(out)) == 0, ghip.apus_ghip_last_error()
+            want, eo = O.moe_forward(slabs, dim, inter, x, idx[None], w[None],
+                                     want_expert_out=True)
+            assert_close_combined(out, want[0], moe_floor(eo, w[None], idx[None])[0],
+                                  "dim=%d k=%d trial %d" % (dim, k, trial))
+            out2 = np.empty(dim, np.uint16)
+            assert ghip.apus_ghip_moe_decode(s, O.ptr(x), O.ptr(idx), O.ptr(w), k,
+                                             O.ptr(out2)) == 0
+            assert np.array_equal(out, out2), "run-to-run determinism"
+    finally:
+        ghip.apus_ghip_store_close(s)
+
+
 def test_moe_decode_duplicate_ids_first_slot(small):
     ghip, s, slabs, (E, dim, inter) = small
     rng = np.random.default_rng(99)
@@ -265,9 +297,9 @@ def test_config2_golden(ghip, pkg):
 
 def test_moe_decode_back_to_back_calls(small):
     """Decode calls enqueued back to back on one stream, no host sync in
-    between: each launch's device-wide hand-off counts only its own
-    workgroups (the arrival counter is monotone across launches), so every
-    output equals the same call run alone, bitwise."""
+    between: every h word a launch writes carries that launch's tag, so a
+    launch never takes an earlier launch's h for its own, and every output
+    equals the same call run alone, bitwise."""
     ghip, s, slabs, (E, dim, inter) = small
     rng = np.random.default_rng(21)
     calls = []
