@@ -289,7 +289,7 @@ struct PfTile {
  * (b) is followed by MFMA work that hides the latency of the next stage's
  * first LDS reads. Scales come from the per-tile table in LDS (sct: one
  * {slot 0, slot 1} pair per 128-wide k block), not from memory. */
-template <int MODE, int NRB, bool EXACT, int NW>
+template <int MODE, int NRB, bool EXACT, int NW, int NRBC = 0, int H0 = 0>
 __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
                                         ghip_f32x2 *sct) {
     /* NW = 4 waves (one per SIMD) or 8 (two per SIMD). Wave wv computes
@@ -299,7 +299,15 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
      * a 1-block tile loads its A rows twice, so every wave issues the same
      * count: identical bytes to the same LDS place). */
     static_assert(NW == 4 || NW == 8, "4 or 8 waves");
-    constexpr uint32_t NRBW = NW == 8 ? (NRB >= 2 ? NRB / 2 : 1) : NRB;
+    /* NRBC, H0 (8 waves, 8-block layout only): this wave computes NRBC row
+     * blocks and the first row half holds H0 -- a tile of 7 blocks runs its
+     * second half on 3 (no MFMAs on the empty fourth block), with loads,
+     * LDS layout and barriers unchanged */
+    constexpr uint32_t NRBL = NW == 8 ? (NRB >= 2 ? NRB / 2 : 1) : NRB;
+    constexpr uint32_t NRBW = NRBC > 0 ? (uint32_t)NRBC : NRBL;   /* computed here */
+    constexpr uint32_t HB0 = H0 > 0 ? (uint32_t)H0 : NRBL;        /* first half */
+    static_assert(NRBC == 0 || (NW == 8 && NRB == 8 && NRBW <= HB0 && HB0 <= 4),
+                  "short row halves: 8-wave, 8-block layout");
     constexpr uint32_t QA = NW == 8 && NRB < 2 ? 8 : 4 * NRB;
     constexpr uint32_t NA = QA / NW;              /* A loads per wave per stage */
     constexpr uint32_t NWL = 16 / NW;             /* weight loads per wave per stage */
@@ -464,7 +472,7 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
 
     ghip_f32x16 a0[NRBW], a1[NRBW];
     /* this wave's first row block in the stage's A rows */
-    const uint32_t arow0 = NW == 8 && NRB >= 2 ? hr * NRBW * 32u * 128u : 0u;
+    const uint32_t arow0 = NW == 8 && NRB >= 2 ? hr * HB0 * 32u * 128u : 0u;
 #pragma unroll
     for (int rb = 0; rb < (int)NRBW; rb++)
 #pragma unroll
@@ -654,7 +662,7 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
 
     /* epilogue: lane (n, h), register i of row block rb holds output row
      * rowbase + rb*32 + 8*(i/4) + 4*h + i%4, column n of each slot */
-    const uint32_t rowbase = hr * NRBW * 32;
+    const uint32_t rowbase = hr * HB0 * 32;
     if constexpr (MODE == 2) {
         const uint32_t c0 = t.cb0 + 32 * cw + n, c1 = t.cb1 + 32 * cw + n;
 #pragma unroll
@@ -678,10 +686,11 @@ __device__ __forceinline__ void pf_tile(const PfTile &t, uint8_t *lds,
          * (MODE 0) or its two 64-byte halves swap when (r >> 2) & 1
          * (MODE 1), so lanes h = 0 and 1 (rows r and r + 4) write to
          * different banks. */
+        /* RW: rows this wave computed; areas are HB0 * 32 rows apart */
         constexpr uint32_t RW = NRBW * 32, RB = MODE == 0 ? 64 : 128;
         __builtin_amdgcn_s_waitcnt(0xc07f);            /* lgkmcnt(0) */
         __builtin_amdgcn_s_barrier();
-        uint8_t *sw = lds + wv * (RW * RB);
+        uint8_t *sw = lds + wv * (HB0 * 32u * RB);
 #pragma unroll
         for (int rb = 0; rb < (int)NRBW; rb++) {
 #pragma unroll
@@ -832,6 +841,15 @@ __global__ __launch_bounds__(NW * 64, 1) void k_pf_gemm(
         ghip_f32x2 *sct = (ghip_f32x2 *)(pf_lds + PF_RING);
         const uint32_t nrb = (t.rows + 31) >> 5;
         if (td.w) pf_tile<MODE, PF_RB, true, NW>(t, pf_lds, sct);
+        else if (NW == 8 && nrb == 7) {
+            /* 7 blocks: the second row half computes 3 (same loads) */
+            if constexpr (NW == 8) {
+                if (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) >> 2)
+                    pf_tile<MODE, 8, false, NW, 3, 4>(t, pf_lds, sct);
+                else
+                    pf_tile<MODE, 8, false, NW, 4, 4>(t, pf_lds, sct);
+            }
+        }
         else if (nrb > 4) pf_tile<MODE, 8, false, NW>(t, pf_lds, sct);
         else if (nrb > 2) pf_tile<MODE, 4, false, NW>(t, pf_lds, sct);
         else if (nrb > 1) pf_tile<MODE, 2, false, NW>(t, pf_lds, sct);
