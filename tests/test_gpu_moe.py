@@ -295,6 +295,49 @@ def test_config2_golden(ghip, pkg):
         ghip.apus_ghip_store_close(s)
 
 
+def test_moe_decode_tag_wrap(ghip):
+    """The hand-off tag is 16 bits: launch 65536 on a workspace clears the h
+    words (a fill kernel ordered on the stream) and restarts at tag 1. Calls
+    on both sides of the wrap, enqueued back to back after 65,527 others,
+    give the outputs the same inputs gave on the fresh workspace, bitwise."""
+    E, dim, inter = 16, 256, 128
+    rng = np.random.default_rng(65536)
+    slabs = random_slabs(E, dim, inter, rng)
+    s = open_store(ghip, E, dim, inter)
+    try:
+        for e, sl in enumerate(slabs):
+            assert ghip.apus_ghip_store_put(s, e, O.ptr(sl), sl.nbytes) == 0
+        calls = []
+        for k in (8, 3, 8, 5, 8, 1):
+            x = O.f32_to_bf16(rng.standard_normal(dim).astype(np.float32))
+            idx = rng.choice(E, k, replace=False).astype(np.int32)
+            w = rng.uniform(0.05, 0.5, k).astype(np.float32)
+            calls.append((x, idx, w))
+        fresh = []
+        for x, idx, w in calls:                   # launches 1..6 (tags 1..6)
+            out = np.empty(dim, np.uint16)
+            assert ghip.apus_ghip_moe_decode(s, O.ptr(x), O.ptr(idx), O.ptr(w), len(idx),
+                                             O.ptr(out)) == 0, ghip.apus_ghip_last_error()
+            fresh.append(out)
+        x0, i0, w0 = calls[0]
+        dx, di, dw, do = G.dev(x0), G.dev(i0), G.dev(w0), G.empty(dim * 2)
+        st = G.stream()
+        for _ in range(65533 - 6):                # launches 7..65533
+            assert ghip.apus_ghip_moe_decode_dev(s, G.vp(dx), None, G.vp(di), G.vp(dw),
+                                                 len(i0), G.vp(do), st) == 0
+        bufs = [(G.dev(x), G.dev(idx), G.dev(w), G.empty(dim * 2), len(idx))
+                for x, idx, w in calls]
+        for bx, bi, bw, bo, k in bufs:            # launches 65534..65539 (wrap at 65536)
+            assert ghip.apus_ghip_moe_decode_dev(s, G.vp(bx), None, G.vp(bi), G.vp(bw), k,
+                                                 G.vp(bo), st) == 0
+        for n, ((bx, bi, bw, bo, k), want) in enumerate(zip(bufs, fresh)):
+            assert np.array_equal(G.host(bo, np.uint16, (dim,)), want), \
+                "launch %d (k=%d) across the tag wrap" % (65534 + n, k)
+        assert np.array_equal(G.host(do, np.uint16, (dim,)), fresh[0])
+    finally:
+        ghip.apus_ghip_store_close(s)
+
+
 def test_moe_decode_back_to_back_calls(small):
     """Decode calls enqueued back to back on one stream, no host sync in
     between: every h word a launch writes carries that launch's tag, so a
