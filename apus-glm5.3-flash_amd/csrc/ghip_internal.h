@@ -73,7 +73,7 @@ typedef struct {
  * ordered combine) as one cooperative launch on st (ws->n_cu workgroups);
  * ev: NULL or 2 events recorded around it. Either logits (device f32
  * [n_experts]; top-k + softmax on the device) or idx/w (device [topk]) must
- * be given. out: device [dim] bf16. Advances ws->arrived. Launches that
+ * be given. out: device [dim] bf16. Advances ws->tag. Launches that
  * share a workspace must not overlap in time. */
 hipError_t ghip_launch_moe_decode(const GhipBank *bank, const uint16_t *x,
                                   const float *logits, const int32_t *idx,

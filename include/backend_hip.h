@@ -220,10 +220,12 @@ int apus_ghip_moe_router_dev(const uint16_t *x, const uint16_t *gate_w,
 
 /* --- routed MoE decode (one token): SwiGLU experts + ordered combine,
  * c/gmoe.h:210-227 + 307-320 without the router and shared expert. One
- * cooperative launch (one workgroup per CU): routing, gate/up GEMVs with the
- * SwiGLU epilogue (activations to HBM), a device-wide hand-off, then down
- * GEMVs with the ascending-expert bf16-per-add combine. Calls that share a
- * store must not overlap in time (one stream).
+ * persistent launch (one workgroup per CU, all resident at once): routing,
+ * gate/up GEMVs with the SwiGLU epilogue (activations to HBM as words
+ * tagged with the launch), then down GEMVs, each wave starting as soon as
+ * its expert's activations carry the tag, and the ascending-expert
+ * bf16-per-add combine. Calls that share a store must not overlap in time
+ * (one stream).
  * Routing either given (idx/w [topk]) or computed on the device from
  * logits [n_experts] f32: stable top-k (ties -> lower id), w = softmax over
  * the k selected logits. Host-pointer variant is synchronous. */
