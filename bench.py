@@ -1330,7 +1330,7 @@ def main():
         args.warmup = d_warm
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(the sharding design is described in DESIGN.md); run --gpus 1",
+              "(it runs on one GPU's share of the work); run --gpus 1",
               file=sys.stderr)
         sys.exit(2)
     if args.workload == "library_gemm":

@@ -5,9 +5,10 @@
  * bench.py's cpu_baseline leg; never linked into or called by the product
  * library (apus-glm5.3-flash_amd/).
  *
- * Every function cites the reference file:line it restates. Pinning (what
- * each function is checked against) is listed in oracle/README.md and in the
- * CPU test suite (tests/test_oracle_*.py).
+ * Every function cites the reference file:line it restates. What each
+ * function is checked against (the reference's known-answer tests and
+ * golden vectors, closed forms, the reference's own C kernels built under
+ * oracle/_ref) is exercised by the CPU test suite (tests/test_oracle_*.py).
  */
 #ifndef APUS_ORACLE_H
 #define APUS_ORACLE_H
