@@ -91,6 +91,33 @@ def test_prefill_vs_oracle(bank, T, k, host):
     assert_close_combined(out, want, floor_of(eo, w, idx), "T=%d k=%d" % (T, k))
 
 
+def test_prefill_full_tile_bodies_every_row(bank):
+    """A full-tile routing (two-waves-per-SIMD bodies) with chosen row counts
+    per expert, every output row checked: 7-block tiles at both ends (193
+    and 224 rows: the second row half runs on 3 blocks), 5- and 6-block
+    tiles (the 8-block body), exact 256-row tiles, 257 rows (a full tile
+    plus a 1-row tile), short tiles of 1 to 4 blocks, and the NaN-code
+    expert (exact decode) at 210 rows."""
+    ghip, s, slabs, (E, dim, inter) = bank
+    rows = {0: 224, 1: 193, 2: 200, 3: 160, 4: 210, 5: 256, 6: 257, 7: 129, 8: 100,
+            9: 64, 10: 33, 11: 1}
+    T, k = max(rows.values()), len(rows)
+    rng = np.random.default_rng(193)
+    idx = np.empty((T, k), np.int32)
+    for t in range(T):
+        mine = [e for e in rows if t < rows[e]]
+        mine = list(rng.permutation(mine))
+        idx[t] = mine + [mine[0]] * (k - len(mine))    # repeats are dropped
+    assert T * k >= E * 128                               # the full-tile bodies
+    w = rng.uniform(0.02, 0.6, (T, k)).astype(np.float32)
+    x = O.f32_to_bf16((rng.standard_normal((T, dim)) *
+                       rng.uniform(0.5, 4.0, (T, 1))).astype(np.float32))
+    out = prefill(ghip, s, x, idx, w, host=False)
+    want, eo = O.moe_forward(slabs, dim, inter, x, idx, w, want_expert_out=True,
+                             threads=8)
+    assert_close_combined(out, want, floor_of(eo, w, idx), "full-tile bodies")
+
+
 def test_prefill_repeated_ids_and_determinism(bank):
     ghip, s, slabs, (E, dim, inter) = bank
     rng = np.random.default_rng(5)
