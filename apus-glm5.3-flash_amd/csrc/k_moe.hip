@@ -752,6 +752,11 @@ extern "C" hipError_t ghip_launch_moe_decode(const GhipBank *bank,
     const size_t lds = lds_gu > lds_dn ? lds_gu : lds_dn;
     if (lds > MD_LDS_MAX || ws->n_cu == 0 || !ws->hw || !ws->err || inter > ws->hw_inter)
         return hipErrorInvalidValue;
+    /* the tag is host state advanced per call, so a launch recorded into a
+     * graph would replay with a stale tag: refuse to be captured */
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
+        return hipErrorStreamCaptureUnsupported;
     /* one workgroup per CU (the LDS use keeps it at one); the tag names
      * this launch's h words: 1..65535, and when it wraps the words are
      * cleared first (by a fill kernel, ordered on st), so a word left from

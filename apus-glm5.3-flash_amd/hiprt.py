@@ -45,6 +45,12 @@ def hip():
             "hipDeviceGetAttribute": [ctypes.POINTER(ctypes.c_int), ctypes.c_int,
                                       ctypes.c_int],
             "hipMemGetInfo": [ctypes.POINTER(sz), ctypes.POINTER(sz)],
+            "hipStreamBeginCapture": [vp, ctypes.c_int],
+            "hipStreamEndCapture": [vp, ctypes.POINTER(vp)],
+            "hipGraphInstantiate": [ctypes.POINTER(vp), vp, vp, vp, sz],
+            "hipGraphLaunch": [vp, vp],
+            "hipGraphExecDestroy": [vp],
+            "hipGraphDestroy": [vp],
         }
         for name, args in sigs.items():
             fn = getattr(lib, name)
@@ -161,3 +167,39 @@ class Event:
                                         ctypes.c_void_p(end.handle)),
               "hipEventElapsedTime")
         return ms.value
+
+
+class Graph:
+    """Work enqueued on `stream` between begin() and end(), captured into a
+    HIP graph (global capture mode) and instantiated; launch() replays it
+    on the stream."""
+
+    def __init__(self, stream):
+        self.stream = stream
+        self.graph = None
+        self.exec = None
+
+    def begin(self):
+        check(hip().hipStreamBeginCapture(self.stream.vp, 0), "hipStreamBeginCapture")
+
+    def end(self):
+        g = ctypes.c_void_p()
+        check(hip().hipStreamEndCapture(self.stream.vp, ctypes.byref(g)),
+              "hipStreamEndCapture")
+        self.graph = g.value
+        e = ctypes.c_void_p()
+        check(hip().hipGraphInstantiate(ctypes.byref(e), ctypes.c_void_p(self.graph), None,
+                                        None, 0), "hipGraphInstantiate")
+        self.exec = e.value
+
+    def launch(self):
+        check(hip().hipGraphLaunch(ctypes.c_void_p(self.exec), self.stream.vp),
+              "hipGraphLaunch")
+
+    def close(self):
+        if self.exec:
+            hip().hipGraphExecDestroy(ctypes.c_void_p(self.exec))
+            self.exec = None
+        if self.graph:
+            hip().hipGraphDestroy(ctypes.c_void_p(self.graph))
+            self.graph = None

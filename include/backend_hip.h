@@ -225,7 +225,10 @@ int apus_ghip_moe_router_dev(const uint16_t *x, const uint16_t *gate_w,
  * tagged with the launch), then down GEMVs, each wave starting as soon as
  * its expert's activations carry the tag, and the ascending-expert
  * bf16-per-add combine. Calls that share a store must not overlap in time
- * (one stream).
+ * (one stream). Each call advances a host-side tag that names its
+ * activations, so the device variant cannot be captured into a graph (a
+ * replay would reuse the recorded tag): it returns 1 on a capturing
+ * stream and launches nothing.
  * Routing either given (idx/w [topk]) or computed on the device from
  * logits [n_experts] f32: stable top-k (ties -> lower id), w = softmax over
  * the k selected logits. Host-pointer variant is synchronous. */

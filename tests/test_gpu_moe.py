@@ -338,6 +338,37 @@ def test_moe_decode_tag_wrap(ghip):
         ghip.apus_ghip_store_close(s)
 
 
+def test_moe_decode_refuses_graph_capture(small):
+    """The decode's hand-off tag is host state advanced per call, so a
+    launch recorded into a HIP graph would replay with a stale tag: the
+    device entry refuses a capturing stream (returns 1, launches nothing),
+    the capture ends cleanly, and calls afterwards are unaffected."""
+    ghip, s, slabs, (E, dim, inter) = small
+    rt = G.rt()
+    rng = np.random.default_rng(404)
+    x = O.f32_to_bf16(rng.standard_normal(dim).astype(np.float32))
+    idx = rng.choice(E, 4, replace=False).astype(np.int32)
+    w = rng.uniform(0.05, 0.5, 4).astype(np.float32)
+    want = np.empty(dim, np.uint16)
+    assert ghip.apus_ghip_moe_decode(s, O.ptr(x), O.ptr(idx), O.ptr(w), 4, O.ptr(want)) == 0
+    dx, di, dw, do = G.dev(x), G.dev(idx), G.dev(w), G.empty(dim * 2)
+    st = rt.Stream()
+    g = rt.Graph(st)
+    g.begin()
+    try:
+        rc = ghip.apus_ghip_moe_decode_dev(s, G.vp(dx), None, G.vp(di), G.vp(dw), 4,
+                                           G.vp(do), st.vp)
+    finally:
+        g.end()
+        g.close()
+    assert rc == 1
+    assert b"captur" in ghip.apus_ghip_last_error().lower()
+    assert ghip.apus_ghip_moe_decode_dev(s, G.vp(dx), None, G.vp(di), G.vp(dw), 4,
+                                         G.vp(do), st.vp) == 0
+    st.synchronize()
+    assert np.array_equal(G.host(do, np.uint16, (dim,)), want)
+
+
 def test_moe_decode_back_to_back_calls(small):
     """Decode calls enqueued back to back on one stream, no host sync in
     between: every h word a launch writes carries that launch's tag, so a
