@@ -72,3 +72,55 @@ def test_noalloc_prefill_rejects_oversize(ghip):
         assert b"fixed" in ghip.apus_ghip_last_error()
     finally:
         ghip.apus_ghip_store_close(s)
+
+
+def test_noalloc_prefill_graph_replay(ghip):
+    """The allocation-free entry point inside a HIP graph: two calls (a
+    sparse and a full-tile routing) captured on a stream, the graph replayed
+    four times with eager calls on the same fixed workspace in between, and
+    every replay's outputs equal to the eager ones, bitwise (the per-call
+    state -- header, queue counters, tile list -- is rebuilt by kernels in
+    the graph, with no memset nodes)."""
+    E, dim, inter = 12, 256, 256
+    rt = G.rt()
+    rng = np.random.default_rng(0x6A)
+    slabs = random_slabs(E, dim, inter, rng, nan_codes_in=(4,))
+    s = open_store(ghip, E, dim, inter)
+    g = None
+    try:
+        for e, sl in enumerate(slabs):
+            assert ghip.apus_ghip_store_put(s, e, O.ptr(sl), sl.nbytes) == 0
+        cases = []
+        for T, k, hot in ((40, 4, 2), (300, 6, 4)):        # sparse, then full tiles
+            x = O.f32_to_bf16(rng.standard_normal((T, dim)).astype(np.float32))
+            idx, w = skewed_routing(rng, T, E, k, hot=hot)
+            cases.append((x, idx, w))
+        want = [run(ghip, ghip.apus_ghip_moe_prefill_dev_noalloc, s, *c) for c in cases]
+        bufs = [(G.dev(x), G.dev(idx), G.dev(w), G.empty(len(x) * dim * 2), idx.shape)
+                for x, idx, w in cases]
+        st = rt.Stream()
+        g = rt.Graph(st)
+        g.begin()
+        rcs = []
+        try:
+            for dx, di, dw, do, (T, k) in bufs:
+                rcs.append(ghip.apus_ghip_moe_prefill_dev_noalloc(
+                    s, G.vp(dx), T, G.vp(di), G.vp(dw), k, G.vp(do), st.vp))
+        finally:
+            g.end()
+        assert rcs == [0, 0], ghip.apus_ghip_last_error()
+        for rep in range(4):
+            for *_, do, _ in bufs:
+                do.zero()
+            g.launch()
+            st.synchronize()
+            for n, ((_, _, _, do, (T, k)), ref) in enumerate(zip(bufs, want)):
+                assert np.array_equal(G.host(do, np.uint16, (T, dim)), ref), \
+                    "replay %d, call %d (T=%d)" % (rep, n, T)
+            c = cases[rep % 2]                           # eager work between replays
+            assert np.array_equal(run(ghip, ghip.apus_ghip_moe_prefill_dev_noalloc, s, *c),
+                                  want[rep % 2])
+    finally:
+        if g is not None:
+            g.close()
+        ghip.apus_ghip_store_close(s)
