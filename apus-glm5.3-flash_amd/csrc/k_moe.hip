@@ -167,9 +167,9 @@ __device__ __forceinline__ int md_select(const float *__restrict__ logits, int t
 
 #define GU_NW 8                  /* waves per workgroup (two per SIMD) */
 #define GU_IPW 4                 /* items per workgroup pass (2 waves each) */
-#define GU_R 4                   /* ring stages per wave (gate + up chunk) */
+#define GU_R 2                   /* ring stages per wave (gate + up chunk) */
 #define GU_STG 4096              /* bytes per stage */
-#define DN_R 6                   /* down ring stages per wave (one chunk each) */
+#define DN_R 3                   /* down ring stages per wave (one chunk each) */
 #define DN_STG 2048
 
 /* Per-workgroup shared state (static LDS). Slots: the kept routing picks
