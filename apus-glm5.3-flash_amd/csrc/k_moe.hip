@@ -300,10 +300,14 @@ __device__ __forceinline__ void md_phase_gateup(const GhipBank &bank, const uint
 #pragma unroll
             for (uint32_t i = 0; i + 1 < GU_R; i++)
                 if (i < nc) issue(i);
-            /* the expert's NaN-code flag is read after the ring's first
-             * stages are on their way, so its round trip overlaps theirs */
+            /* the expert's NaN-code flag and the first chunk's scales are
+             * read after the ring's first stages are on their way, so their
+             * round trips (the scales' line is cold) overlap those stages'
+             * instead of following them */
             __builtin_amdgcn_sched_barrier(0);
             const bool exact = ghip_sload_u32(bank.nan_flags, e) != 0u;
+            const float scg0 = ghip_sload(sg, c0), scu0 = ghip_sload(su, c0);
+            __builtin_amdgcn_sched_barrier(0);
             ghip_f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
             for (uint32_t t = 0; t < nc; t++) {
                 /* own DMA of stage t landed; stage t-1's buffer is free
@@ -314,7 +318,8 @@ __device__ __forceinline__ void md_phase_gateup(const GhipBank &bank, const uint
                 const ghip_chunk cg = ghip_cdma_read(buf, n, g);
                 const ghip_chunk cu = ghip_cdma_read(buf + 2048, n, g);
                 const uint32_t c = c0 + t;
-                const float scg = ghip_sload(sg, c), scu = ghip_sload(su, c);
+                const float scg = t ? ghip_sload(sg, c) : scg0;
+                const float scu = t ? ghip_sload(su, c) : scu0;
                 const uint16_t *xa = xs + c * 128u + 32u * g;
                 if (exact) {
                     ghip_chunk_mfma<true>(cg, scg, xa, ag);
@@ -350,26 +355,42 @@ __device__ __forceinline__ void md_phase_gateup(const GhipBank &bank, const uint
  * A operand and leaves the expert output in sh.oq; md_combine then runs the
  * ordered combine in-workgroup. md_down_prologue issues the first DN_R - 1
  * stages (so they stream while the workgroup waits for h). */
-__device__ __forceinline__ void md_down_prologue(const GhipBank &bank, const MdShared &sh,
-                                                 uint32_t r0, uint32_t base,
-                                                 uint8_t *ring_base) {
+/* what md_down_prologue loaded for md_phase_down: the expert's NaN-code
+ * flag and the first chunk's scale, as vector loads issued before the wait
+ * for h, so their cold round trips overlap it (the h polling waits for them
+ * with its own loads; scalar loads would be waited at once, their SGPRs
+ * being spilled to VGPR lanes) */
+struct MdDownHead {
+    uint32_t flag;
+    uint32_t sc0;
+};
+
+__device__ __forceinline__ MdDownHead md_down_prologue(const GhipBank &bank, const MdShared &sh,
+                                                       uint32_t r0, uint32_t base,
+                                                       uint8_t *ring_base) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t nsel = __builtin_amdgcn_readfirstlane(sh.nsel);
-    if (base + wv >= nsel) return;
-    const uint32_t inter = bank.inter, nch = inter >> 7;
+    if (base + wv >= nsel) return MdDownHead{0u, 0u};
+    const uint32_t inter = bank.inter, nch = inter >> 7, nkb = inter >> 7;
     const uint32_t e = (uint32_t)__builtin_amdgcn_readfirstlane(sh.sel[base + wv]);
-    const uint8_t *rows = bank.base + (size_t)e * bank.stride + bank.off_dw + (size_t)r0 * inter;
+    const uint8_t *slab = bank.base + (size_t)e * bank.stride;
+    const uint8_t *rows = slab + bank.off_dw + (size_t)r0 * inter;
     const ghip_cdma d = ghip_cdma_offsets(lane, inter);
     uint8_t *ring = ring_base + wv * (DN_R * DN_STG);
 #pragma unroll
     for (uint32_t i = 0; i + 1 < DN_R; i++)
         if (i < nch) ghip_cdma_issue(rows, i, d, ring + i * DN_STG);
+    __builtin_amdgcn_sched_barrier(0);
+    const float *srow = (const float *)(slab + bank.off_ds) + (size_t)(r0 >> 7) * nkb;
+    return MdDownHead{
+        __hip_atomic_load(bank.nan_flags + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP),
+        __hip_atomic_load((const uint32_t *)srow, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)};
 }
 
 __device__ __forceinline__ void md_phase_down(const GhipBank &bank, MdShared &sh,
                                               uint32_t r0, uint32_t base, const uint16_t *hs,
-                                              uint8_t *ring_base) {
+                                              uint8_t *ring_base, const MdDownHead &hd) {
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t n = lane & 15u, g = lane >> 4;
@@ -380,7 +401,8 @@ __device__ __forceinline__ void md_phase_down(const GhipBank &bank, MdShared &sh
         const uint8_t *slab = bank.base + (size_t)e * bank.stride;
         const uint8_t *rows = slab + bank.off_dw + (size_t)r0 * inter;
         const float *srow = (const float *)(slab + bank.off_ds) + (size_t)(r0 >> 7) * nkb;
-        const bool exact = ghip_sload_u32(bank.nan_flags, e) != 0u;
+        const bool exact = __builtin_amdgcn_readfirstlane(hd.flag) != 0u;
+        const float sc0 = __uint_as_float(__builtin_amdgcn_readfirstlane(hd.sc0));
         const ghip_cdma d = ghip_cdma_offsets(lane, inter);
         uint8_t *ring = ring_base + wv * (DN_R * DN_STG);
         ghip_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -389,7 +411,7 @@ __device__ __forceinline__ void md_phase_down(const GhipBank &bank, MdShared &sh
             if (t + DN_R - 1 < nch)
                 ghip_cdma_issue(rows, t + DN_R - 1, d, ring + ((t + DN_R - 1) % DN_R) * DN_STG);
             const ghip_chunk cw = ghip_cdma_read(ring + (t % DN_R) * DN_STG, n, g);
-            const float sc = ghip_sload(srow, t);
+            const float sc = t ? ghip_sload(srow, t) : sc0;
             const uint16_t *ha = hs + (size_t)wv * inter + t * 128u + 32u * g;
             if (exact) ghip_chunk_mfma<true>(cw, sc, ha, acc);
             else ghip_chunk_mfma<false>(cw, sc, ha, acc);
@@ -518,7 +540,7 @@ __global__ __launch_bounds__(MD_NW * 64, 1) void k_moe_decode(
         const uint32_t r0 = rg * MD_T;
         for (uint32_t base = 0; base < nsel; base += MD_NW) {
             /* the weight ring's first stages stream while h is awaited */
-            md_down_prologue(bank, sh, r0, base, ring);
+            const MdDownHead hd = md_down_prologue(bank, sh, r0, base, ring);
             /* wave w: h of slot base + w (once when all slots fit one
              * pass), then at once its down rows; a wave whose wait runs
              * out flags the error and computes nothing */
@@ -526,7 +548,7 @@ __global__ __launch_bounds__(MD_NW * 64, 1) void k_moe_decode(
             if (base + wv < nsel && (base > 0 || rg == blockIdx.x || nsel > MD_NW))
                 ok = md_stage_h_wave(hw, base + wv, inter, tag, hs + (size_t)wv * inter);
             if (ok) {
-                md_phase_down(bank, sh, r0, base, hs, ring);
+                md_phase_down(bank, sh, r0, base, hs, ring, hd);
             } else {
                 if ((tid & 63u) == 0) atomicOr(err, 4u);
                 GHIP_VMCNT(0);                    /* drain the ring */
