@@ -59,38 +59,38 @@ __device__ __forceinline__ float rt_val(uint32_t k) {
     return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
-/* k = max (or min) of k and k moved by a DPP pattern; lanes without a
- * source keep k */
-template <int CTRL, int ROWMASK, bool MAX>
+/* k = max of k and k moved by a DPP pattern; lanes without a source keep
+ * k (the moved value is 0 there, the identity of an unsigned max, so the
+ * move folds into one v_max_u32_dpp) */
+template <int CTRL, int ROWMASK>
 __device__ __forceinline__ uint32_t rt_dpp(uint32_t k) {
-    const uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp((int)k, (int)k, CTRL, ROWMASK,
-                                                             0xf, false);
-    return MAX ? (o > k ? o : k) : (o < k ? o : k);
+    const uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)k, CTRL, ROWMASK, 0xf, true);
+    return o > k ? o : k;
 }
 
-/* Wave max (or min) on DPP (VALU lane moves, no LDS round trips): row
- * shifts leave each row's result in its lane 15, two row broadcasts carry
- * it to lane 63, read back as a wave-uniform value. */
-template <bool MAX>
-__device__ __forceinline__ uint32_t rt_wave_red(uint32_t k) {
-    k = rt_dpp<0x111, 0xf, MAX>(k);      /* row_shr:1 */
-    k = rt_dpp<0x112, 0xf, MAX>(k);      /* row_shr:2 */
-    k = rt_dpp<0x114, 0xf, MAX>(k);      /* row_shr:4 */
-    k = rt_dpp<0x118, 0xf, MAX>(k);      /* row_shr:8 */
-    k = rt_dpp<0x142, 0xa, MAX>(k);      /* row_bcast:15 */
-    k = rt_dpp<0x143, 0xc, MAX>(k);      /* row_bcast:31 */
+/* Wave max on DPP (VALU lane moves, no LDS round trips): row shifts leave
+ * each row's result in its lane 15, two row broadcasts carry it to lane
+ * 63, read back as a wave-uniform value. */
+__device__ __forceinline__ uint32_t rt_wave_max(uint32_t k) {
+    k = rt_dpp<0x111, 0xf>(k);           /* row_shr:1 */
+    k = rt_dpp<0x112, 0xf>(k);           /* row_shr:2 */
+    k = rt_dpp<0x114, 0xf>(k);           /* row_shr:4 */
+    k = rt_dpp<0x118, 0xf>(k);           /* row_shr:8 */
+    k = rt_dpp<0x142, 0xa>(k);           /* row_bcast:15 */
+    k = rt_dpp<0x143, 0xc>(k);           /* row_bcast:31 */
     return (uint32_t)__builtin_amdgcn_readlane((int)k, 63);
 }
 
 /* Stable top-k by one wave (c/gmoe.h:175-189: larger first, ties to the
- * lower index): slot s of lane l holds the key of index l + 64 s (0 =
- * empty). Each lane first sorts its R keys in descending order (a bubble
- * network that swaps only on a strictly larger key, so equal keys keep
- * the lower index first). Each of the k rounds then takes one 32-bit DPP
- * wave max of the lanes' heads; the winning lane drops its head. When
- * more than one lane holds the max, a second wave reduction picks the
- * lowest index among them. Lane j < k returns pick j's index and its key
- * in mykey. */
+ * lower index): slot s of lane l holds the key of index R l + s (0 =
+ * empty), so each lane holds a run of consecutive indices and a lower lane
+ * lower ones. Each lane first sorts its R keys in descending order (a
+ * bubble network that swaps only on a strictly larger key, so equal keys
+ * keep the lower index first). Each of the k rounds then takes one 32-bit
+ * DPP wave max of the lanes' heads; of the lanes whose head equals it the
+ * lowest one holds the lowest index with that key (its head is its lowest
+ * such index, and lower lanes hold lower indices), and it drops its head.
+ * Lane j < k returns pick j's index and its key in mykey. */
 template <int R>
 __device__ __forceinline__ int rt_select(uint32_t (&key)[R], int topk, uint32_t &mykey) {
     const uint32_t lane = threadIdx.x & 63u;
@@ -111,16 +111,10 @@ __device__ __forceinline__ int rt_select(uint32_t (&key)[R], int topk, uint32_t 
     int myid = -1;
     mykey = 0u;
     for (int j = 0; j < topk; j++) {
-        const uint32_t wm = rt_wave_red<true>(key[0]);
-        const uint64_t bal = __ballot(key[0] == wm);
-        uint32_t widx;
-        if (__popcll(bal) == 1) {
-            const int wl = (int)__builtin_ctzll(bal);
-            widx = (uint32_t)wl + 64u * (uint32_t)__builtin_amdgcn_readlane((int)ss[0], wl);
-        } else {
-            widx = rt_wave_red<false>(key[0] == wm ? lane + 64u * ss[0] : 0xffffffffu);
-        }
-        if (lane == (widx & 63u)) {
+        const uint32_t wm = rt_wave_max(key[0]);
+        const uint32_t wl = (uint32_t)__builtin_ctzll(__ballot(key[0] == wm));
+        const uint32_t widx = wl * (uint32_t)R + (uint32_t)__builtin_amdgcn_readlane((int)ss[0], wl);
+        if (lane == wl) {
 #pragma unroll
             for (int s = 0; s + 1 < R; s++) {
                 key[s] = key[s + 1];
@@ -149,7 +143,7 @@ __device__ __forceinline__ int md_select(const float *__restrict__ logits, int t
     float v[R];
 #pragma unroll
     for (int s = 0; s < R; s++) {
-        const int i = lane + 64 * s;
+        const int i = lane * R + s;
         v[s] = logits[i < E ? i : E - 1];
     }
     /* an unconditional use pins each load here (the compiler would
@@ -158,7 +152,7 @@ __device__ __forceinline__ int md_select(const float *__restrict__ logits, int t
     for (int s = 0; s < R; s++) asm volatile("" ::"v"(v[s]));
     uint32_t key[R];
 #pragma unroll
-    for (int s = 0; s < R; s++) key[s] = lane + 64 * s < E ? rt_key(v[s]) : 0u;
+    for (int s = 0; s < R; s++) key[s] = lane * R + s < E ? rt_key(v[s]) : 0u;
     uint32_t mk;
     const int myid = rt_select<R>(key, topk, mk);
     mylog = rt_val(mk);
@@ -620,7 +614,7 @@ __device__ __forceinline__ void rt_sigmoid_select(Logit lg, const float *__restr
     float lv[R], bv[R];
 #pragma unroll
     for (int s = 0; s < R; s++) {
-        const uint32_t i = (uint32_t)lane + 64u * s, ic = i < E ? i : E - 1u;
+        const uint32_t i = (uint32_t)lane * R + s, ic = i < E ? i : E - 1u;
         lv[s] = lg(ic);
         bv[s] = bias[ic];
     }
@@ -629,7 +623,7 @@ __device__ __forceinline__ void rt_sigmoid_select(Logit lg, const float *__restr
     uint32_t key[R];
 #pragma unroll
     for (int s = 0; s < R; s++) {
-        const uint32_t i = (uint32_t)lane + 64u * s;
+        const uint32_t i = (uint32_t)lane * R + s;
         key[s] = 0u;
         if (i < E) {
             const float v = ghip_sigmoid_np(lv[s]);
