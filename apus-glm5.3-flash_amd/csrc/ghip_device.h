@@ -140,6 +140,30 @@ __device__ __forceinline__ void ghip_chunk_mfma(const ghip_chunk &c, float sc,
     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[3], b3, acc, 0, 0, 0);
 }
 
+/* the same with this lane's four activation operands already in registers
+ * (read from LDS together with the chunk's codes, so one LDS wait covers
+ * both) */
+template <bool EXACT>
+__device__ __forceinline__ void ghip_chunk_mfma_a(const ghip_chunk &c, float sc,
+                                                  const ghip_bf16x8 (&a)[4],
+                                                  ghip_f32x4 &acc) {
+    ghip_bf16x8 b0, b1, b2, b3;
+    ghip_deq16<EXACT>(c.lo, sc, b0, b1);
+    ghip_deq16<EXACT>(c.hi, sc, b2, b3);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b0, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1], b1, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[2], b2, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[3], b3, acc, 0, 0, 0);
+}
+
+__device__ __forceinline__ void ghip_read_a4(const uint16_t *xa, ghip_bf16x8 (&a)[4]) {
+    const ghip_bf16x8 *p = (const ghip_bf16x8 *)xa;
+    a[0] = p[0];
+    a[1] = p[1];
+    a[2] = p[2];
+    a[3] = p[3];
+}
+
 /* ---- activation staging without serializing the weight stream ----------
  * vmcnt retires loads in issue order, so an activation load issued AFTER
  * the weight loads makes its LDS write wait for every weight byte. Stage in

@@ -309,18 +309,22 @@ __device__ __forceinline__ void md_phase_gateup(const GhipBank &bank, const uint
                 ghip_wait_stages<4, GU_R - 2>(nc - 1 - t);
                 if (t + GU_R - 1 < nc) issue(t + GU_R - 1);
                 const uint8_t *buf = ring + (t % GU_R) * GU_STG;
+                const uint32_t c = c0 + t;
+                /* codes, activations and scales requested before any is
+                 * used: one LDS wait covers them */
                 const ghip_chunk cg = ghip_cdma_read(buf, n, g);
                 const ghip_chunk cu = ghip_cdma_read(buf + 2048, n, g);
-                const uint32_t c = c0 + t;
+                ghip_bf16x8 xa[4];
+                ghip_read_a4(xs + c * 128u + 32u * g, xa);
                 const float scg = t ? ghip_sload(sg, c) : scg0;
                 const float scu = t ? ghip_sload(su, c) : scu0;
-                const uint16_t *xa = xs + c * 128u + 32u * g;
+                __builtin_amdgcn_sched_barrier(0);
                 if (exact) {
-                    ghip_chunk_mfma<true>(cg, scg, xa, ag);
-                    ghip_chunk_mfma<true>(cu, scu, xa, au);
+                    ghip_chunk_mfma_a<true>(cg, scg, xa, ag);
+                    ghip_chunk_mfma_a<true>(cu, scu, xa, au);
                 } else {
-                    ghip_chunk_mfma<false>(cg, scg, xa, ag);
-                    ghip_chunk_mfma<false>(cu, scu, xa, au);
+                    ghip_chunk_mfma_a<false>(cg, scg, xa, ag);
+                    ghip_chunk_mfma_a<false>(cu, scu, xa, au);
                 }
             }
             if (g == 0) {
@@ -405,10 +409,12 @@ __device__ __forceinline__ void md_phase_down(const GhipBank &bank, MdShared &sh
             if (t + DN_R - 1 < nch)
                 ghip_cdma_issue(rows, t + DN_R - 1, d, ring + ((t + DN_R - 1) % DN_R) * DN_STG);
             const ghip_chunk cw = ghip_cdma_read(ring + (t % DN_R) * DN_STG, n, g);
+            ghip_bf16x8 ha[4];
+            ghip_read_a4(hs + (size_t)wv * inter + t * 128u + 32u * g, ha);
             const float sc = t ? ghip_sload(srow, t) : sc0;
-            const uint16_t *ha = hs + (size_t)wv * inter + t * 128u + 32u * g;
-            if (exact) ghip_chunk_mfma<true>(cw, sc, ha, acc);
-            else ghip_chunk_mfma<false>(cw, sc, ha, acc);
+            __builtin_amdgcn_sched_barrier(0);
+            if (exact) ghip_chunk_mfma_a<true>(cw, sc, ha, acc);
+            else ghip_chunk_mfma_a<false>(cw, sc, ha, acc);
         }
         if (g == 0) sh.oq[base + wv][n] = acc[0];
     }
