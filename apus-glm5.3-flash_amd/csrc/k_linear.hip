@@ -369,18 +369,23 @@ __global__ __launch_bounds__(GS_NW * 64, 1) void k_fp8_gemv_stream(
                 if (t + GS_R - 1 < nc)
                     ghip_cdma_issue(rows, c0 + t + GS_R - 1, d,
                                     ring + ((t + GS_R - 1) % GS_R) * 2048u);
-                const ghip_chunk cw = ghip_cdma_read(ring + (t % GS_R) * 2048u, n, g);
                 const uint32_t c = c0 + t;
-                if (BF) {
+                const ghip_chunk cw = ghip_cdma_read(ring + (t % GS_R) * 2048u, n, g);
+                if constexpr (BF) {
                     const ghip_bf16x8 *a = (const ghip_bf16x8 *)(xa + c * 64u);
                     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
                         a[0], __builtin_bit_cast(ghip_bf16x8, cw.lo), acc, 0, 0, 0);
                     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
                         a[1], __builtin_bit_cast(ghip_bf16x8, cw.hi), acc, 0, 0, 0);
                 } else {
+                    /* codes, activations and scale requested before any is
+                     * used: one LDS wait covers them */
+                    ghip_bf16x8 a4[4];
+                    ghip_read_a4(xa + c * 128u, a4);
                     const float sc = ghip_sload(srow, c);
-                    if (exact) ghip_chunk_mfma<true>(cw, sc, xa + c * 128u, acc);
-                    else ghip_chunk_mfma<false>(cw, sc, xa + c * 128u, acc);
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (exact) ghip_chunk_mfma_a<true>(cw, sc, a4, acc);
+                    else ghip_chunk_mfma_a<false>(cw, sc, a4, acc);
                 }
             }
             if (g == 0) {
