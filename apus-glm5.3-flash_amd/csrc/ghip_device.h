@@ -321,6 +321,26 @@ __device__ __forceinline__ void ghip_cdma_issue(const uint8_t *rows, uint32_t c,
     ghip_dma16(rows + (size_t)c * 128u + d.off1, buf + 1024);
 }
 
+/* ---- streaming chunks through registers ---------------------------------
+ * The same whole-line pattern as the DMA (ghip_cdma_offsets: load i, lane
+ * l -> row 8i + l/8, swizzled piece l % 8), as two 16-byte register loads
+ * per lane; ghip_rl_store then writes them where the DMA would (lane l's
+ * bytes at 16 l of each 1 KB half), so ghip_cdma_read reads either. Plain
+ * register loads stream faster than global_load_lds on this part at the
+ * same bytes in flight, and the compiler tracks their waits exactly. */
+__device__ __forceinline__ void ghip_rl_load(const uint8_t *rows, const ghip_cdma &d,
+                                             uint32_t c, ghip_u32x4 &v0, ghip_u32x4 &v1) {
+    const uint8_t *p = rows + (size_t)c * 128u;
+    v0 = __builtin_nontemporal_load((const ghip_u32x4 *)(p + d.off0));
+    v1 = __builtin_nontemporal_load((const ghip_u32x4 *)(p + d.off1));
+}
+
+__device__ __forceinline__ void ghip_rl_store(uint8_t *buf, uint32_t lane, const ghip_u32x4 &v0,
+                                              const ghip_u32x4 &v1) {
+    *(ghip_u32x4 *)(buf + lane * 16u) = v0;
+    *(ghip_u32x4 *)(buf + 1024u + lane * 16u) = v1;
+}
+
 /* this lane's 32 codes of a chunk in LDS (row n, pieces 2g, 2g+1) */
 __device__ __forceinline__ ghip_chunk ghip_cdma_read(const uint8_t *buf, uint32_t n,
                                                     uint32_t g) {

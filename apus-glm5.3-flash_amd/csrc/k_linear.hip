@@ -24,6 +24,7 @@
  * output is deterministic run to run.
  */
 #include "ghip_device.h"
+#include <type_traits>
 #include "ghip_internal.h"
 
 #define GEMV_NW 8          /* waves per workgroup (k split) */
@@ -271,21 +272,24 @@ extern "C" hipError_t ghip_launch_nan_scan(const uint8_t *codes, size_t n,
 /* ------------------------------------------------------------------------ */
 
 #define GS_NW 8                  /* waves per workgroup */
-/* ring stages per wave (one chunk each). Two chunks in flight per wave
- * (32 KB per CU) stream faster than deeper rings: measured on configs 0
- * and 1, 3 stages beat 4, 5, 6 and 8 (more bytes in flight per CU made the
- * whole launch slower) and 2. */
-#define GS_R 3
+/* LDS chunk slots per wave: a chunk is written from registers and read
+ * back in the MFMA layout while the next two are in flight (two chunks in
+ * flight per wave, 32 KB per CU: with the earlier DMA ring, more bytes in
+ * flight per CU made the launch slower) */
+#define GS_R 2
 #define GS_LDS (144u * 1024u)    /* dynamic LDS limit of the streaming GEMV */
 
 /* Y[m, rows] for M <= 4 token rows. A row group (16 weight rows) is split
  * over KS waves along K (KS in {2, 8}); a workgroup pass covers 8 / KS row
  * groups, passes run over the groups persistently (grid <= CUs). Each wave
  * streams its chunks (16 rows x 128 bytes: 128 FP8 codes with one scale
- * block, or 64 BF16 weights when BF) through a wave-private GS_R-stage LDS
- * ring filled by direct DMA, dequantizes in registers (FP8) and reduces on
- * MFMA with the token rows of x (staged once per workgroup) as the A
- * operand: A row i = lane % 16 is token min(i, M-1), rows past M feed
+ * block, or 64 BF16 weights when BF) through registers: two 16-byte loads
+ * per lane in a whole-line pattern (load i: rows 8i + lane / 8, piece lane
+ * % 8), two chunks in flight, each chunk written to a wave-private 2-slot
+ * LDS area (lane l's bytes at 16 l, piece p of row r at p ^ ((r >> 1) & 7))
+ * and read back in the MFMA layout, dequantized in registers (FP8) and
+ * reduced on MFMA with the token rows of x (staged once per workgroup) as
+ * the A operand: A row i = lane % 16 is token min(i, M-1), rows past M feed
  * output rows that are discarded. The KS partial sums of a group are added
  * in LDS in a fixed order (deterministic). BF: the BF16 GEMV of the
  * bf16_gemm hook (c/bf16.h:712-767), no scales; lane 16g + n holds row n,
@@ -312,42 +316,40 @@ __global__ __launch_bounds__(GS_NW * 64, 1) void k_fp8_gemv_stream(
     const uint32_t c0 = part * nch / KS, c1 = (part + 1) * nch / KS, nc = c1 - c0;
     const uint32_t groups = (O + 15) / 16, passes = (groups + GPP - 1) / GPP;
     const uint16_t *xa = xs + (size_t)min(n, (uint32_t)M - 1u) * K + (BF ? 16u : 32u) * g;
-    /* pass ps's row group of this wave: its rows, the DMA offsets (a
+    /* pass ps's row group of this wave: its rows and load offsets (a
      * partial last group re-reads row O-1, outputs discarded) */
     auto rows_of = [&](uint32_t ps) {
         return W + (size_t)(ps * GPP + slot) * 16u * KB;
     };
-    auto dma_of = [&](uint32_t ps) {
+    auto offs_of = [&](uint32_t ps) {
         return ghip_cdma_offsets(lane, KB, min(15u, O - 1u - (ps * GPP + slot) * 16u));
     };
-    auto prologue = [&](uint32_t ps) {
-        const uint8_t *rows = rows_of(ps);
-        const ghip_cdma d = dma_of(ps);
-#pragma unroll
-        for (uint32_t i = 0; i + 1 < GS_R; i++)
-            if (i < nc) ghip_cdma_issue(rows, c0 + i, d, ring + i * 2048u);
+    /* the two chunks in flight: chunk t's two 16-byte pieces in (ra0, ra1)
+     * when t is even, (rb0, rb1) when odd */
+    ghip_u32x4 ra0, ra1, rb0, rb1;
+    /* the first two chunks of a pass, always both loaded (chunk indices
+     * clamped): a fixed count of loads in flight, in a fixed order */
+    auto first2 = [&](const uint8_t *rows, const ghip_cdma &d) {
+        ghip_rl_load(rows, d, min(c0, nch - 1u), ra0, ra1);
+        __builtin_amdgcn_sched_barrier(0);
+        ghip_rl_load(rows, d, min(c0 + 1u, nch - 1u), rb0, rb1);
+        __builtin_amdgcn_sched_barrier(0);
     };
     /* x into LDS without delaying the weight stream: x goes by direct DMA
-     * too (1 KB pieces dealt to the waves, lanes past x re-read its last
-     * vector into the 1 KB-rounded x region), ahead of the first pass's
-     * ring prologue; that prologue issues a fixed count of loads (group and
-     * chunk clamped to valid ones: a stage past the wave's chunks lands in a
-     * ring slot this pass never reads and only makes the ring waits below
-     * stricter), so waiting until no more than that count is in flight
-     * means this wave's x pieces have landed */
+     * (1 KB pieces dealt to the waves, lanes past x re-read its last vector
+     * into the 1 KB-rounded x region) ahead of the first pass's four chunk
+     * loads, so waiting until no more than those four are in flight means
+     * this wave's x pieces have landed */
     {
         const uint32_t nvec = (uint32_t)M * (K >> 3), nxc = (nvec + 63u) >> 6;
         for (uint32_t c = wv; c < nxc; c += GS_NW)
             ghip_dma16(X + (size_t)min(c * 64u + lane, nvec - 1u) * 8u, gsl + c * 1024u);
         const uint32_t grp0 = min(blockIdx.x * GPP + slot, groups - 1u);
-        const uint8_t *rows = W + (size_t)grp0 * 16u * KB;
-        const ghip_cdma d = ghip_cdma_offsets(lane, KB, min(15u, O - 1u - grp0 * 16u));
-#pragma unroll
-        for (uint32_t i = 0; i + 1 < GS_R; i++)
-            ghip_cdma_issue(rows, min(c0 + i, nch - 1u), d, ring + i * 2048u);
-        GHIP_VMCNT(2 * (GS_R - 1));
+        first2(W + (size_t)grp0 * 16u * KB,
+               ghip_cdma_offsets(lane, KB, min(15u, O - 1u - grp0 * 16u)));
+        GHIP_VMCNT(4);
     }
-    /* a bare barrier: __syncthreads() would also wait for the prologue
+    /* a bare barrier: __syncthreads() would also wait for the chunk loads
      * (its workgroup-scope release waits for every load in flight) */
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
@@ -360,17 +362,23 @@ __global__ __launch_bounds__(GS_NW * 64, 1) void k_fp8_gemv_stream(
             /* a wave with no chunks (K < KS * 128) contributes zeros */
             const uint32_t row0 = grp * 16;
             const uint8_t *rows = rows_of(ps);
-            const ghip_cdma d = dma_of(ps);
+            const ghip_cdma d = offs_of(ps);
             const float *srow = BF ? nullptr : S + (size_t)(row0 >> 7) * nkb;
-            if (ps != blockIdx.x) prologue(ps);
+            if (ps != blockIdx.x) first2(rows, d);
             ghip_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-            for (uint32_t t = 0; t < nc; t++) {
-                ghip_wait_stages<2, GS_R - 2>(nc - 1 - t);
-                if (t + GS_R - 1 < nc)
-                    ghip_cdma_issue(rows, c0 + t + GS_R - 1, d,
-                                    ring + ((t + GS_R - 1) % GS_R) * 2048u);
+            /* chunk t: its registers into LDS slot t % 2, the registers
+             * refilled with chunk t + 2 (REFILL), the chunk read back in
+             * the MFMA layout with this lane's activations and the scale */
+            auto step = [&](auto refill_c, uint32_t t, ghip_u32x4 &v0, ghip_u32x4 &v1,
+                            uint8_t *buf) {
+                ghip_rl_store(buf, lane, v0, v1);
+                if constexpr (decltype(refill_c)::value) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    ghip_rl_load(rows, d, c0 + t + 2u, v0, v1);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
                 const uint32_t c = c0 + t;
-                const ghip_chunk cw = ghip_cdma_read(ring + (t % GS_R) * 2048u, n, g);
+                const ghip_chunk cw = ghip_cdma_read(buf, n, g);
                 if constexpr (BF) {
                     const ghip_bf16x8 *a = (const ghip_bf16x8 *)(xa + c * 64u);
                     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
@@ -378,20 +386,37 @@ __global__ __launch_bounds__(GS_NW * 64, 1) void k_fp8_gemv_stream(
                     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
                         a[1], __builtin_bit_cast(ghip_bf16x8, cw.hi), acc, 0, 0, 0);
                 } else {
-                    /* codes, activations and scale requested before any is
-                     * used: one LDS wait covers them */
                     ghip_bf16x8 a4[4];
                     ghip_read_a4(xa + c * 128u, a4);
                     const float sc = ghip_sload(srow, c);
-                    __builtin_amdgcn_sched_barrier(0);
                     if (exact) ghip_chunk_mfma_a<true>(cw, sc, a4, acc);
                     else ghip_chunk_mfma_a<false>(cw, sc, a4, acc);
                 }
+            };
+            using RF = std::true_type;
+            using NR = std::false_type;
+            uint32_t t = 0;
+            for (; t + 3u < nc; t += 2) {
+                step(RF{}, t, ra0, ra1, ring);
+                step(RF{}, t + 1u, rb0, rb1, ring + 2048u);
+            }
+            if (nc - t == 3u) {
+                step(RF{}, t, ra0, ra1, ring);
+                step(NR{}, t + 1u, rb0, rb1, ring + 2048u);
+                step(NR{}, t + 2u, ra0, ra1, ring);
+            } else if (nc - t == 2u) {
+                step(NR{}, t, ra0, ra1, ring);
+                step(NR{}, t + 1u, rb0, rb1, ring + 2048u);
+            } else if (nc - t == 1u) {
+                step(NR{}, t, ra0, ra1, ring);
             }
             if (g == 0) {
 #pragma unroll
                 for (int i = 0; i < M; i++) red[slot][part][i][n] = acc[i];
             }
+        } else {
+            /* the pass's two prefetched chunks are not used */
+            GHIP_VMCNT(0);
         }
         __syncthreads();
         if (tid < GPP * M * 16u) {

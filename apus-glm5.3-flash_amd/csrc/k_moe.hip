@@ -31,6 +31,7 @@
  * with the activation (x or h) from LDS as the A operand.
  */
 #include "ghip_device.h"
+#include <type_traits>
 #include "ghip_internal.h"
 
 #define MD_NW 8                  /* waves per workgroup */
@@ -286,29 +287,38 @@ __device__ __forceinline__ void md_phase_gateup(const GhipBank &bank, const uint
             const uint8_t *wu = slab + bank.off_uw + (size_t)r0 * dim;
             const float *sg = (const float *)(slab + bank.off_gs) + (size_t)(r0 >> 7) * nkb;
             const float *su = (const float *)(slab + bank.off_us) + (size_t)(r0 >> 7) * nkb;
-            auto issue = [&](uint32_t t) {
-                uint8_t *buf = ring + (t % GU_R) * GU_STG;
-                ghip_cdma_issue(wg, c0 + t, d, buf);
-                ghip_cdma_issue(wu, c0 + t, d, buf + 2048);
+            /* stage t (gate chunk + up chunk) through registers: two sets,
+             * stage t in set t % 2, written to LDS slot t % 2 and refilled
+             * with stage t + 2; the first two stages always loaded (indices
+             * clamped), in a fixed order */
+            ghip_u32x4 ga0, ga1, ua0, ua1, gb0, gb1, ub0, ub1;
+            auto ld = [&](uint32_t t, ghip_u32x4 &g0, ghip_u32x4 &g1, ghip_u32x4 &u0,
+                          ghip_u32x4 &u1) {
+                ghip_rl_load(wg, d, c0 + t, g0, g1);
+                ghip_rl_load(wu, d, c0 + t, u0, u1);
             };
-#pragma unroll
-            for (uint32_t i = 0; i + 1 < GU_R; i++)
-                if (i < nc) issue(i);
+            ld(0u, ga0, ga1, ua0, ua1);
+            __builtin_amdgcn_sched_barrier(0);
+            ld(nc > 1u ? 1u : 0u, gb0, gb1, ub0, ub1);
             /* the expert's NaN-code flag and the first chunk's scales are
-             * read after the ring's first stages are on their way, so their
-             * round trips (the scales' line is cold) overlap those stages'
-             * instead of following them */
+             * read after the first stages are on their way, so their round
+             * trips (the scales' line is cold) overlap those stages' instead
+             * of following them */
             __builtin_amdgcn_sched_barrier(0);
             const bool exact = ghip_sload_u32(bank.nan_flags, e) != 0u;
             const float scg0 = ghip_sload(sg, c0), scu0 = ghip_sload(su, c0);
             __builtin_amdgcn_sched_barrier(0);
             ghip_f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
-            for (uint32_t t = 0; t < nc; t++) {
-                /* own DMA of stage t landed; stage t-1's buffer is free
-                 * (its reads fed stage t-1's MFMAs) */
-                ghip_wait_stages<4, GU_R - 2>(nc - 1 - t);
-                if (t + GU_R - 1 < nc) issue(t + GU_R - 1);
-                const uint8_t *buf = ring + (t % GU_R) * GU_STG;
+            auto step = [&](auto refill_c, uint32_t t, ghip_u32x4 &g0, ghip_u32x4 &g1,
+                            ghip_u32x4 &u0, ghip_u32x4 &u1) {
+                uint8_t *buf = ring + (t & 1u) * GU_STG;
+                ghip_rl_store(buf, lane, g0, g1);
+                ghip_rl_store(buf + 2048, lane, u0, u1);
+                if constexpr (decltype(refill_c)::value) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    ld(t + 2u, g0, g1, u0, u1);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
                 const uint32_t c = c0 + t;
                 /* codes, activations and scales requested before any is
                  * used: one LDS wait covers them */
@@ -326,6 +336,23 @@ __device__ __forceinline__ void md_phase_gateup(const GhipBank &bank, const uint
                     ghip_chunk_mfma_a<false>(cg, scg, xa, ag);
                     ghip_chunk_mfma_a<false>(cu, scu, xa, au);
                 }
+            };
+            using RF = std::true_type;
+            using NR = std::false_type;
+            uint32_t t = 0;
+            for (; t + 3u < nc; t += 2) {
+                step(RF{}, t, ga0, ga1, ua0, ua1);
+                step(RF{}, t + 1u, gb0, gb1, ub0, ub1);
+            }
+            if (nc - t == 3u) {
+                step(RF{}, t, ga0, ga1, ua0, ua1);
+                step(NR{}, t + 1u, gb0, gb1, ub0, ub1);
+                step(NR{}, t + 2u, ga0, ga1, ua0, ua1);
+            } else if (nc - t == 2u) {
+                step(NR{}, t, ga0, ga1, ua0, ua1);
+                step(NR{}, t + 1u, gb0, gb1, ub0, ub1);
+            } else if (nc - t == 1u) {
+                step(NR{}, t, ga0, ga1, ua0, ua1);
             }
             if (g == 0) {
                 sh.red[slot][half][0][n] = ag[0];
@@ -361,6 +388,7 @@ __device__ __forceinline__ void md_phase_gateup(const GhipBank &bank, const uint
 struct MdDownHead {
     uint32_t flag;
     uint32_t sc0;
+    ghip_u32x4 a0, a1, b0, b1;    /* the first two chunks (registers) */
 };
 
 __device__ __forceinline__ MdDownHead md_down_prologue(const GhipBank &bank, const MdShared &sh,
@@ -369,26 +397,28 @@ __device__ __forceinline__ MdDownHead md_down_prologue(const GhipBank &bank, con
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t nsel = __builtin_amdgcn_readfirstlane(sh.nsel);
-    if (base + wv >= nsel) return MdDownHead{0u, 0u};
+    MdDownHead hd{};
+    if (base + wv >= nsel) return hd;
     const uint32_t inter = bank.inter, nch = inter >> 7, nkb = inter >> 7;
     const uint32_t e = (uint32_t)__builtin_amdgcn_readfirstlane(sh.sel[base + wv]);
     const uint8_t *slab = bank.base + (size_t)e * bank.stride;
     const uint8_t *rows = slab + bank.off_dw + (size_t)r0 * inter;
     const ghip_cdma d = ghip_cdma_offsets(lane, inter);
-    uint8_t *ring = ring_base + wv * (DN_R * DN_STG);
-#pragma unroll
-    for (uint32_t i = 0; i + 1 < DN_R; i++)
-        if (i < nch) ghip_cdma_issue(rows, i, d, ring + i * DN_STG);
+    (void)ring_base;
+    ghip_rl_load(rows, d, 0u, hd.a0, hd.a1);
+    __builtin_amdgcn_sched_barrier(0);
+    ghip_rl_load(rows, d, nch > 1u ? 1u : 0u, hd.b0, hd.b1);
     __builtin_amdgcn_sched_barrier(0);
     const float *srow = (const float *)(slab + bank.off_ds) + (size_t)(r0 >> 7) * nkb;
-    return MdDownHead{
-        __hip_atomic_load(bank.nan_flags + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP),
-        __hip_atomic_load((const uint32_t *)srow, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)};
+    hd.flag = __hip_atomic_load(bank.nan_flags + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    hd.sc0 = __hip_atomic_load((const uint32_t *)srow, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_WORKGROUP);
+    return hd;
 }
 
 __device__ __forceinline__ void md_phase_down(const GhipBank &bank, MdShared &sh,
                                               uint32_t r0, uint32_t base, const uint16_t *hs,
-                                              uint8_t *ring_base, const MdDownHead &hd) {
+                                              uint8_t *ring_base, MdDownHead &hd) {
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t n = lane & 15u, g = lane >> 4;
@@ -404,17 +434,40 @@ __device__ __forceinline__ void md_phase_down(const GhipBank &bank, MdShared &sh
         const ghip_cdma d = ghip_cdma_offsets(lane, inter);
         uint8_t *ring = ring_base + wv * (DN_R * DN_STG);
         ghip_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        for (uint32_t t = 0; t < nch; t++) {
-            ghip_wait_stages<2, DN_R - 2>(nch - 1 - t);
-            if (t + DN_R - 1 < nch)
-                ghip_cdma_issue(rows, t + DN_R - 1, d, ring + ((t + DN_R - 1) % DN_R) * DN_STG);
-            const ghip_chunk cw = ghip_cdma_read(ring + (t % DN_R) * DN_STG, n, g);
+        /* chunk t: registers (set t % 2, the first two loaded by the
+         * prologue) into LDS slot t % 2, refilled with chunk t + 2 */
+        auto step = [&](auto refill_c, uint32_t t, ghip_u32x4 &v0, ghip_u32x4 &v1) {
+            uint8_t *buf = ring + (t & 1u) * DN_STG;
+            ghip_rl_store(buf, lane, v0, v1);
+            if constexpr (decltype(refill_c)::value) {
+                __builtin_amdgcn_sched_barrier(0);
+                ghip_rl_load(rows, d, t + 2u, v0, v1);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            const ghip_chunk cw = ghip_cdma_read(buf, n, g);
             ghip_bf16x8 ha[4];
             ghip_read_a4(hs + (size_t)wv * inter + t * 128u + 32u * g, ha);
             const float sc = t ? ghip_sload(srow, t) : sc0;
             __builtin_amdgcn_sched_barrier(0);
             if (exact) ghip_chunk_mfma_a<true>(cw, sc, ha, acc);
             else ghip_chunk_mfma_a<false>(cw, sc, ha, acc);
+        };
+        using RF = std::true_type;
+        using NR = std::false_type;
+        uint32_t t = 0;
+        for (; t + 3u < nch; t += 2) {
+            step(RF{}, t, hd.a0, hd.a1);
+            step(RF{}, t + 1u, hd.b0, hd.b1);
+        }
+        if (nch - t == 3u) {
+            step(RF{}, t, hd.a0, hd.a1);
+            step(NR{}, t + 1u, hd.b0, hd.b1);
+            step(NR{}, t + 2u, hd.a0, hd.a1);
+        } else if (nch - t == 2u) {
+            step(NR{}, t, hd.a0, hd.a1);
+            step(NR{}, t + 1u, hd.b0, hd.b1);
+        } else if (nch - t == 1u) {
+            step(NR{}, t, hd.a0, hd.a1);
         }
         if (g == 0) sh.oq[base + wv][n] = acc[0];
     }
@@ -540,7 +593,7 @@ __global__ __launch_bounds__(MD_NW * 64, 1) void k_moe_decode(
         const uint32_t r0 = rg * MD_T;
         for (uint32_t base = 0; base < nsel; base += MD_NW) {
             /* the weight ring's first stages stream while h is awaited */
-            const MdDownHead hd = md_down_prologue(bank, sh, r0, base, ring);
+            MdDownHead hd = md_down_prologue(bank, sh, r0, base, ring);
             /* wave w: h of slot base + w (once when all slots fit one
              * pass), then at once its down rows; a wave whose wait runs
              * out flags the error and computes nothing */
