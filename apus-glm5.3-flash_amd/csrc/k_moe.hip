@@ -287,38 +287,33 @@ __device__ __forceinline__ void md_phase_gateup(const GhipBank &bank, const uint
             const uint8_t *wu = slab + bank.off_uw + (size_t)r0 * dim;
             const float *sg = (const float *)(slab + bank.off_gs) + (size_t)(r0 >> 7) * nkb;
             const float *su = (const float *)(slab + bank.off_us) + (size_t)(r0 >> 7) * nkb;
-            /* stage t (gate chunk + up chunk) through registers: two sets,
-             * stage t in set t % 2, written to LDS slot t % 2 and refilled
-             * with stage t + 2; the first two stages always loaded (indices
-             * clamped), in a fixed order */
-            ghip_u32x4 ga0, ga1, ua0, ua1, gb0, gb1, ub0, ub1;
+            /* stage t (gate chunk + up chunk) through registers: written to
+             * LDS slot t % 2, then the registers take stage t + 1 while
+             * stage t is computed (one stage in flight per wave: deeper
+             * made the step slower, as with the LDS-DMA ring) */
+            ghip_u32x4 ga0, ga1, ua0, ua1;
             auto ld = [&](uint32_t t, ghip_u32x4 &g0, ghip_u32x4 &g1, ghip_u32x4 &u0,
                           ghip_u32x4 &u1) {
                 ghip_rl_load(wg, d, c0 + t, g0, g1);
                 ghip_rl_load(wu, d, c0 + t, u0, u1);
             };
             ld(0u, ga0, ga1, ua0, ua1);
-            __builtin_amdgcn_sched_barrier(0);
-            ld(nc > 1u ? 1u : 0u, gb0, gb1, ub0, ub1);
             /* the expert's NaN-code flag and the first chunk's scales are
-             * read after the first stages are on their way, so their round
-             * trips (the scales' line is cold) overlap those stages' instead
-             * of following them */
+             * read after the first stage is on its way, so their round
+             * trips (the scales' line is cold) overlap the stage's instead
+             * of following it */
             __builtin_amdgcn_sched_barrier(0);
             const bool exact = ghip_sload_u32(bank.nan_flags, e) != 0u;
             const float scg0 = ghip_sload(sg, c0), scu0 = ghip_sload(su, c0);
             __builtin_amdgcn_sched_barrier(0);
             ghip_f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
-            auto step = [&](auto refill_c, uint32_t t, ghip_u32x4 &g0, ghip_u32x4 &g1,
-                            ghip_u32x4 &u0, ghip_u32x4 &u1) {
+            for (uint32_t t = 0; t < nc; t++) {
                 uint8_t *buf = ring + (t & 1u) * GU_STG;
-                ghip_rl_store(buf, lane, g0, g1);
-                ghip_rl_store(buf + 2048, lane, u0, u1);
-                if constexpr (decltype(refill_c)::value) {
-                    __builtin_amdgcn_sched_barrier(0);
-                    ld(t + 2u, g0, g1, u0, u1);
-                    __builtin_amdgcn_sched_barrier(0);
-                }
+                ghip_rl_store(buf, lane, ga0, ga1);
+                ghip_rl_store(buf + 2048, lane, ua0, ua1);
+                __builtin_amdgcn_sched_barrier(0);
+                if (t + 1u < nc) ld(t + 1u, ga0, ga1, ua0, ua1);
+                __builtin_amdgcn_sched_barrier(0);
                 const uint32_t c = c0 + t;
                 /* codes, activations and scales requested before any is
                  * used: one LDS wait covers them */
@@ -336,23 +331,6 @@ __device__ __forceinline__ void md_phase_gateup(const GhipBank &bank, const uint
                     ghip_chunk_mfma_a<false>(cg, scg, xa, ag);
                     ghip_chunk_mfma_a<false>(cu, scu, xa, au);
                 }
-            };
-            using RF = std::true_type;
-            using NR = std::false_type;
-            uint32_t t = 0;
-            for (; t + 3u < nc; t += 2) {
-                step(RF{}, t, ga0, ga1, ua0, ua1);
-                step(RF{}, t + 1u, gb0, gb1, ub0, ub1);
-            }
-            if (nc - t == 3u) {
-                step(RF{}, t, ga0, ga1, ua0, ua1);
-                step(NR{}, t + 1u, gb0, gb1, ub0, ub1);
-                step(NR{}, t + 2u, ga0, ga1, ua0, ua1);
-            } else if (nc - t == 2u) {
-                step(NR{}, t, ga0, ga1, ua0, ua1);
-                step(NR{}, t + 1u, gb0, gb1, ub0, ub1);
-            } else if (nc - t == 1u) {
-                step(NR{}, t, ga0, ga1, ua0, ua1);
             }
             if (g == 0) {
                 sh.red[slot][half][0][n] = ag[0];
@@ -388,7 +366,7 @@ __device__ __forceinline__ void md_phase_gateup(const GhipBank &bank, const uint
 struct MdDownHead {
     uint32_t flag;
     uint32_t sc0;
-    ghip_u32x4 a0, a1, b0, b1;    /* the first two chunks (registers) */
+    ghip_u32x4 a0, a1, b0, b1, c0, c1;    /* the first three chunks (registers) */
 };
 
 __device__ __forceinline__ MdDownHead md_down_prologue(const GhipBank &bank, const MdShared &sh,
@@ -408,6 +386,8 @@ __device__ __forceinline__ MdDownHead md_down_prologue(const GhipBank &bank, con
     ghip_rl_load(rows, d, 0u, hd.a0, hd.a1);
     __builtin_amdgcn_sched_barrier(0);
     ghip_rl_load(rows, d, nch > 1u ? 1u : 0u, hd.b0, hd.b1);
+    __builtin_amdgcn_sched_barrier(0);
+    ghip_rl_load(rows, d, nch > 2u ? 2u : 0u, hd.c0, hd.c1);
     __builtin_amdgcn_sched_barrier(0);
     const float *srow = (const float *)(slab + bank.off_ds) + (size_t)(r0 >> 7) * nkb;
     hd.flag = __hip_atomic_load(bank.nan_flags + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -434,14 +414,16 @@ __device__ __forceinline__ void md_phase_down(const GhipBank &bank, MdShared &sh
         const ghip_cdma d = ghip_cdma_offsets(lane, inter);
         uint8_t *ring = ring_base + wv * (DN_R * DN_STG);
         ghip_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        /* chunk t: registers (set t % 2, the first two loaded by the
-         * prologue) into LDS slot t % 2, refilled with chunk t + 2 */
-        auto step = [&](auto refill_c, uint32_t t, ghip_u32x4 &v0, ghip_u32x4 &v1) {
-            uint8_t *buf = ring + (t & 1u) * DN_STG;
+        /* chunk t: registers (set t % 3, the first three loaded by the
+         * prologue) into LDS slot t % 3, refilled with chunk t + 3 (three
+         * chunks in flight: the down rows stream after the hand-off, where
+         * deeper helps) */
+        auto step = [&](auto refill_c, uint32_t t, uint32_t j, ghip_u32x4 &v0, ghip_u32x4 &v1) {
+            uint8_t *buf = ring + j * DN_STG;
             ghip_rl_store(buf, lane, v0, v1);
             if constexpr (decltype(refill_c)::value) {
                 __builtin_amdgcn_sched_barrier(0);
-                ghip_rl_load(rows, d, t + 2u, v0, v1);
+                ghip_rl_load(rows, d, t + 3u, v0, v1);
                 __builtin_amdgcn_sched_barrier(0);
             }
             const ghip_chunk cw = ghip_cdma_read(buf, n, g);
@@ -455,19 +437,27 @@ __device__ __forceinline__ void md_phase_down(const GhipBank &bank, MdShared &sh
         using RF = std::true_type;
         using NR = std::false_type;
         uint32_t t = 0;
-        for (; t + 3u < nch; t += 2) {
-            step(RF{}, t, hd.a0, hd.a1);
-            step(RF{}, t + 1u, hd.b0, hd.b1);
+        for (; t + 5u < nch; t += 3) {
+            step(RF{}, t, 0u, hd.a0, hd.a1);
+            step(RF{}, t + 1u, 1u, hd.b0, hd.b1);
+            step(RF{}, t + 2u, 2u, hd.c0, hd.c1);
         }
-        if (nch - t == 3u) {
-            step(RF{}, t, hd.a0, hd.a1);
-            step(NR{}, t + 1u, hd.b0, hd.b1);
-            step(NR{}, t + 2u, hd.a0, hd.a1);
-        } else if (nch - t == 2u) {
-            step(NR{}, t, hd.a0, hd.a1);
-            step(NR{}, t + 1u, hd.b0, hd.b1);
-        } else if (nch - t == 1u) {
-            step(NR{}, t, hd.a0, hd.a1);
+        const uint32_t rem = nch - t;
+        if (rem == 5u) {
+            step(RF{}, t, 0u, hd.a0, hd.a1);
+            step(RF{}, t + 1u, 1u, hd.b0, hd.b1);
+            step(NR{}, t + 2u, 2u, hd.c0, hd.c1);
+            step(NR{}, t + 3u, 0u, hd.a0, hd.a1);
+            step(NR{}, t + 4u, 1u, hd.b0, hd.b1);
+        } else if (rem == 4u) {
+            step(RF{}, t, 0u, hd.a0, hd.a1);
+            step(NR{}, t + 1u, 1u, hd.b0, hd.b1);
+            step(NR{}, t + 2u, 2u, hd.c0, hd.c1);
+            step(NR{}, t + 3u, 0u, hd.a0, hd.a1);
+        } else {
+            if (rem > 0u) step(NR{}, t, 0u, hd.a0, hd.a1);
+            if (rem > 1u) step(NR{}, t + 1u, 1u, hd.b0, hd.b1);
+            if (rem > 2u) step(NR{}, t + 2u, 2u, hd.c0, hd.c1);
         }
         if (g == 0) sh.oq[base + wv][n] = acc[0];
     }
