@@ -273,10 +273,10 @@ extern "C" hipError_t ghip_launch_nan_scan(const uint8_t *codes, size_t n,
 
 #define GS_NW 8                  /* waves per workgroup */
 /* LDS chunk slots per wave: a chunk is written from registers and read
- * back in the MFMA layout while the next two are in flight (two chunks in
- * flight per wave, 32 KB per CU: with the earlier DMA ring, more bytes in
- * flight per CU made the launch slower) */
-#define GS_R 2
+ * back in the MFMA layout while the next ones are in flight: two for FP8
+ * weights (measured: one 13.8 us, two 12.3, three 12.6 on config 1), three
+ * for BF16 (the LM head: two 226 us, three 208) */
+#define GS_R 3
 #define GS_LDS (144u * 1024u)    /* dynamic LDS limit of the streaming GEMV */
 
 /* Y[m, rows] for M <= 4 token rows. A row group (16 weight rows) is split
@@ -324,30 +324,35 @@ __global__ __launch_bounds__(GS_NW * 64, 1) void k_fp8_gemv_stream(
     auto offs_of = [&](uint32_t ps) {
         return ghip_cdma_offsets(lane, KB, min(15u, O - 1u - (ps * GPP + slot) * 16u));
     };
-    /* the two chunks in flight: chunk t's two 16-byte pieces in (ra0, ra1)
-     * when t is even, (rb0, rb1) when odd */
-    ghip_u32x4 ra0, ra1, rb0, rb1;
-    /* the first two chunks of a pass, always both loaded (chunk indices
+    /* NA chunks in flight: chunk t's two 16-byte pieces in register set
+     * t % NA ((ra0, ra1), (rb0, rb1), (rc0, rc1)) and LDS slot t % NA */
+    constexpr uint32_t NA = BF ? 3u : 2u;
+    ghip_u32x4 ra0, ra1, rb0, rb1, rc0, rc1;
+    /* the first NA chunks of a pass, always all loaded (chunk indices
      * clamped): a fixed count of loads in flight, in a fixed order */
-    auto first2 = [&](const uint8_t *rows, const ghip_cdma &d) {
+    auto prefetch = [&](const uint8_t *rows, const ghip_cdma &d) {
         ghip_rl_load(rows, d, min(c0, nch - 1u), ra0, ra1);
         __builtin_amdgcn_sched_barrier(0);
         ghip_rl_load(rows, d, min(c0 + 1u, nch - 1u), rb0, rb1);
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (NA == 3u) {
+            ghip_rl_load(rows, d, min(c0 + 2u, nch - 1u), rc0, rc1);
+            __builtin_amdgcn_sched_barrier(0);
+        }
     };
     /* x into LDS without delaying the weight stream: x goes by direct DMA
      * (1 KB pieces dealt to the waves, lanes past x re-read its last vector
-     * into the 1 KB-rounded x region) ahead of the first pass's four chunk
-     * loads, so waiting until no more than those four are in flight means
-     * this wave's x pieces have landed */
+     * into the 1 KB-rounded x region) ahead of the first pass's 2 NA chunk
+     * loads, so waiting until no more than those are in flight means this
+     * wave's x pieces have landed */
     {
         const uint32_t nvec = (uint32_t)M * (K >> 3), nxc = (nvec + 63u) >> 6;
         for (uint32_t c = wv; c < nxc; c += GS_NW)
             ghip_dma16(X + (size_t)min(c * 64u + lane, nvec - 1u) * 8u, gsl + c * 1024u);
         const uint32_t grp0 = min(blockIdx.x * GPP + slot, groups - 1u);
-        first2(W + (size_t)grp0 * 16u * KB,
+        prefetch(W + (size_t)grp0 * 16u * KB,
                ghip_cdma_offsets(lane, KB, min(15u, O - 1u - grp0 * 16u)));
-        GHIP_VMCNT(4);
+        GHIP_VMCNT(2 * NA);
     }
     /* a bare barrier: __syncthreads() would also wait for the chunk loads
      * (its workgroup-scope release waits for every load in flight) */
@@ -364,17 +369,17 @@ __global__ __launch_bounds__(GS_NW * 64, 1) void k_fp8_gemv_stream(
             const uint8_t *rows = rows_of(ps);
             const ghip_cdma d = offs_of(ps);
             const float *srow = BF ? nullptr : S + (size_t)(row0 >> 7) * nkb;
-            if (ps != blockIdx.x) first2(rows, d);
+            if (ps != blockIdx.x) prefetch(rows, d);
             ghip_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-            /* chunk t: its registers into LDS slot t % 2, the registers
-             * refilled with chunk t + 2 (REFILL), the chunk read back in
+            /* chunk t: its registers into LDS slot t % NA, the registers
+             * refilled with chunk t + NA (REFILL), the chunk read back in
              * the MFMA layout with this lane's activations and the scale */
             auto step = [&](auto refill_c, uint32_t t, ghip_u32x4 &v0, ghip_u32x4 &v1,
                             uint8_t *buf) {
                 ghip_rl_store(buf, lane, v0, v1);
                 if constexpr (decltype(refill_c)::value) {
                     __builtin_amdgcn_sched_barrier(0);
-                    ghip_rl_load(rows, d, c0 + t + 2u, v0, v1);
+                    ghip_rl_load(rows, d, c0 + t + NA, v0, v1);
                     __builtin_amdgcn_sched_barrier(0);
                 }
                 const uint32_t c = c0 + t;
@@ -396,26 +401,51 @@ __global__ __launch_bounds__(GS_NW * 64, 1) void k_fp8_gemv_stream(
             using RF = std::true_type;
             using NR = std::false_type;
             uint32_t t = 0;
-            for (; t + 3u < nc; t += 2) {
-                step(RF{}, t, ra0, ra1, ring);
-                step(RF{}, t + 1u, rb0, rb1, ring + 2048u);
-            }
-            if (nc - t == 3u) {
-                step(RF{}, t, ra0, ra1, ring);
-                step(NR{}, t + 1u, rb0, rb1, ring + 2048u);
-                step(NR{}, t + 2u, ra0, ra1, ring);
-            } else if (nc - t == 2u) {
-                step(NR{}, t, ra0, ra1, ring);
-                step(NR{}, t + 1u, rb0, rb1, ring + 2048u);
-            } else if (nc - t == 1u) {
-                step(NR{}, t, ra0, ra1, ring);
+            if constexpr (NA == 2u) {
+                for (; t + 3u < nc; t += 2) {
+                    step(RF{}, t, ra0, ra1, ring);
+                    step(RF{}, t + 1u, rb0, rb1, ring + 2048u);
+                }
+                if (nc - t == 3u) {
+                    step(RF{}, t, ra0, ra1, ring);
+                    step(NR{}, t + 1u, rb0, rb1, ring + 2048u);
+                    step(NR{}, t + 2u, ra0, ra1, ring);
+                } else if (nc - t == 2u) {
+                    step(NR{}, t, ra0, ra1, ring);
+                    step(NR{}, t + 1u, rb0, rb1, ring + 2048u);
+                } else if (nc - t == 1u) {
+                    step(NR{}, t, ra0, ra1, ring);
+                }
+            } else {
+                for (; t + 5u < nc; t += 3) {
+                    step(RF{}, t, ra0, ra1, ring);
+                    step(RF{}, t + 1u, rb0, rb1, ring + 2048u);
+                    step(RF{}, t + 2u, rc0, rc1, ring + 4096u);
+                }
+                const uint32_t rem = nc - t;
+                if (rem == 5u) {
+                    step(RF{}, t, ra0, ra1, ring);
+                    step(RF{}, t + 1u, rb0, rb1, ring + 2048u);
+                    step(NR{}, t + 2u, rc0, rc1, ring + 4096u);
+                    step(NR{}, t + 3u, ra0, ra1, ring);
+                    step(NR{}, t + 4u, rb0, rb1, ring + 2048u);
+                } else if (rem == 4u) {
+                    step(RF{}, t, ra0, ra1, ring);
+                    step(NR{}, t + 1u, rb0, rb1, ring + 2048u);
+                    step(NR{}, t + 2u, rc0, rc1, ring + 4096u);
+                    step(NR{}, t + 3u, ra0, ra1, ring);
+                } else {
+                    if (rem > 0u) step(NR{}, t, ra0, ra1, ring);
+                    if (rem > 1u) step(NR{}, t + 1u, rb0, rb1, ring + 2048u);
+                    if (rem > 2u) step(NR{}, t + 2u, rc0, rc1, ring + 4096u);
+                }
             }
             if (g == 0) {
 #pragma unroll
                 for (int i = 0; i < M; i++) red[slot][part][i][n] = acc[i];
             }
         } else {
-            /* the pass's two prefetched chunks are not used */
+            /* the pass's prefetched chunks are not used */
             GHIP_VMCNT(0);
         }
         __syncthreads();
