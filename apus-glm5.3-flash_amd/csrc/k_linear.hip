@@ -268,7 +268,7 @@ extern "C" hipError_t ghip_launch_nan_scan(const uint8_t *codes, size_t n,
 }
 
 /* ------------------------------------------------------------------------ */
-/* K2 streaming: persistent FP8 GEMV through per-wave DMA rings             */
+/* K2 streaming: persistent FP8 / BF16 GEMV, register-load chunk streams   */
 /* ------------------------------------------------------------------------ */
 
 #define GS_NW 8                  /* waves per workgroup */

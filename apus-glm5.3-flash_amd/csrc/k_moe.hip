@@ -23,12 +23,13 @@
  * carries the tag (bounded). No fence, counter or kernel boundary is
  * involved, and a reader needs nothing but the words it reads.
  *
- * Weight streaming: gate/up waves pull their 16-row chunks (128-wide k, one
- * scale block) through a wave-private LDS ring with direct global->LDS
- * loads; each down wave issues its first ring stages, then awaits its own
- * slot's h (no workgroup barrier) and streams its rows as soon as it is in.
- * The GEMV inner step dequantizes in registers and reduces over k on MFMA
- * with the activation (x or h) from LDS as the A operand.
+ * Weight streaming: waves pull their 16-row chunks (128-wide k, one scale
+ * block) through registers (whole-line 16-byte loads), write each to a
+ * wave-private LDS slot and read it back in the MFMA layout; each down wave
+ * loads its first chunks, then awaits its own slot's h (no workgroup
+ * barrier) and streams its rows as soon as it is in. The GEMV inner step
+ * dequantizes in registers and reduces over k on MFMA with the activation
+ * (x or h) from LDS as the A operand.
  */
 #include "ghip_device.h"
 #include <type_traits>
@@ -162,9 +163,9 @@ __device__ __forceinline__ int md_select(const float *__restrict__ logits, int t
 
 #define GU_NW 8                  /* waves per workgroup (two per SIMD) */
 #define GU_IPW 4                 /* items per workgroup pass (2 waves each) */
-#define GU_R 2                   /* ring stages per wave (gate + up chunk) */
+#define GU_R 2                   /* LDS slots per wave (gate + up chunk each) */
 #define GU_STG 4096              /* bytes per stage */
-#define DN_R 3                   /* down ring stages per wave (one chunk each) */
+#define DN_R 3                   /* down LDS slots per wave (one chunk each) */
 #define DN_STG 2048
 
 /* Per-workgroup shared state (static LDS). Slots: the kept routing picks
@@ -252,10 +253,9 @@ __device__ __forceinline__ void md_route_finish(MdShared &sh, int topk) {
 
 /* Phase B: items = (slot q, 16 rows): gate and up GEMVs over dim and the
  * SwiGLU; workgroup b takes item groups b, b + G, ... of GU_IPW items; wave
- * w streams item (w / 2)'s half (w % 2) of K through a wave-private
- * GU_R-stage LDS ring filled by direct DMA (no registers hold loads in
- * flight, no barriers inside the stream); the halves are summed in LDS in a
- * fixed order (deterministic). The 16 h values of an item go to hw[q] in
+ * w streams item (w / 2)'s half (w % 2) of K through registers and a
+ * wave-private pair of LDS slots (no barriers inside the stream); the
+ * halves are summed in LDS in a fixed order (deterministic). The 16 h values of an item go to hw[q] in
  * HBM as tagged words (lanes 0..15 of the item's even wave). */
 __device__ __forceinline__ void md_phase_gateup(const GhipBank &bank, const uint16_t *xs,
                                                 uint8_t *ring_base, MdShared &sh,
@@ -353,16 +353,16 @@ __device__ __forceinline__ void md_phase_gateup(const GhipBank &bank, const uint
 }
 
 /* Phase C, down + ordered combine for the 16 output rows at r0: wave q
- * streams slot base + q's 16 rows of Wd over inter through its own
- * DN_R-stage DMA ring with h of that slot (in LDS at hs + q * inter) as the
+ * streams slot base + q's 16 rows of Wd over inter through registers and
+ * its DN_R LDS slots with h of that slot (in LDS at hs + q * inter) as the
  * A operand and leaves the expert output in sh.oq; md_combine then runs the
- * ordered combine in-workgroup. md_down_prologue issues the first DN_R - 1
- * stages (so they stream while the workgroup waits for h). */
-/* what md_down_prologue loaded for md_phase_down: the expert's NaN-code
- * flag and the first chunk's scale, as vector loads issued before the wait
- * for h, so their cold round trips overlap it (the h polling waits for them
- * with its own loads; scalar loads would be waited at once, their SGPRs
- * being spilled to VGPR lanes) */
+ * ordered combine in-workgroup. md_down_prologue loads the first DN_R
+ * chunks (so they stream while the wave waits for h). */
+/* what md_down_prologue loaded for md_phase_down: the first DN_R chunks,
+ * and the expert's NaN-code flag and the first chunk's scale as vector
+ * loads issued before the wait for h, so their cold round trips overlap it
+ * (the h polling waits for them with its own loads; scalar loads would be
+ * waited at once, their SGPRs being spilled to VGPR lanes) */
 struct MdDownHead {
     uint32_t flag;
     uint32_t sc0;
@@ -370,8 +370,7 @@ struct MdDownHead {
 };
 
 __device__ __forceinline__ MdDownHead md_down_prologue(const GhipBank &bank, const MdShared &sh,
-                                                       uint32_t r0, uint32_t base,
-                                                       uint8_t *ring_base) {
+                                                       uint32_t r0, uint32_t base) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t nsel = __builtin_amdgcn_readfirstlane(sh.nsel);
@@ -382,7 +381,6 @@ __device__ __forceinline__ MdDownHead md_down_prologue(const GhipBank &bank, con
     const uint8_t *slab = bank.base + (size_t)e * bank.stride;
     const uint8_t *rows = slab + bank.off_dw + (size_t)r0 * inter;
     const ghip_cdma d = ghip_cdma_offsets(lane, inter);
-    (void)ring_base;
     ghip_rl_load(rows, d, 0u, hd.a0, hd.a1);
     __builtin_amdgcn_sched_barrier(0);
     ghip_rl_load(rows, d, nch > 1u ? 1u : 0u, hd.b0, hd.b1);
@@ -566,7 +564,7 @@ __global__ __launch_bounds__(MD_NW * 64, 1) void k_moe_decode(
         for (uint32_t i = tid + MD_NW * 64; i < n16; i += MD_NW * 64)
             ((ghip_u32x4 *)xs)[i] = ((const ghip_u32x4 *)x)[i];
         /* nothing of the routing (its error-flag atomic included) stays in
-         * flight into the streaming loops, whose vmcnt waits count only DMA */
+         * flight into the streaming loops */
         GHIP_VMCNT(0);
         __syncthreads();
     }
@@ -582,8 +580,8 @@ __global__ __launch_bounds__(MD_NW * 64, 1) void k_moe_decode(
     for (uint32_t rg = blockIdx.x; rg * MD_T < dim; rg += gridDim.x) {
         const uint32_t r0 = rg * MD_T;
         for (uint32_t base = 0; base < nsel; base += MD_NW) {
-            /* the weight ring's first stages stream while h is awaited */
-            MdDownHead hd = md_down_prologue(bank, sh, r0, base, ring);
+            /* the down rows' first chunks stream while h is awaited */
+            MdDownHead hd = md_down_prologue(bank, sh, r0, base);
             /* wave w: h of slot base + w (once when all slots fit one
              * pass), then at once its down rows; a wave whose wait runs
              * out flags the error and computes nothing */
@@ -594,7 +592,7 @@ __global__ __launch_bounds__(MD_NW * 64, 1) void k_moe_decode(
                 md_phase_down(bank, sh, r0, base, hs, ring, hd);
             } else {
                 if ((tid & 63u) == 0) atomicOr(err, 4u);
-                GHIP_VMCNT(0);                    /* drain the ring */
+                GHIP_VMCNT(0);                    /* drain the chunk loads */
             }
             __syncthreads();
         }
