@@ -360,9 +360,8 @@ __device__ __forceinline__ float ghip_sigmoid_np(float x) {
 /* SwiGLU on bf16-valued g and u (c/gmoe.h:217-225): gate clamped above,
  * up clamped both sides, h = bf16(bf16(g * sigmoid(g)) * u). */
 __device__ __forceinline__ uint32_t ghip_swiglu(float g, float u, float limit) {
-    if (g > limit) g = limit;
-    if (u > limit) u = limit;
-    else if (u < -limit) u = -limit;
+    g = g > limit ? limit : g;                   /* selects: no exec branches */
+    u = u > limit ? limit : (u < -limit ? -limit : u);
     float hv = ghip_bf16_round(g * ghip_sigmoid_np(g));
     return ghip_bf16_bits(hv * u);
 }

@@ -233,9 +233,10 @@ __device__ __forceinline__ float pf_bf16_round(float x) {
  * then the clamps (compares, so a NaN stays NaN as in the reference) */
 __device__ __forceinline__ uint16_t pf_swiglu(float accg, float accu, float limit) {
     float g = pf_bf16_round(accg), u = pf_bf16_round(accu);
-    if (g > limit) g = limit;
-    if (u > limit) u = limit;
-    else if (u < -limit) u = -limit;
+    /* selects, not branches: an if/else chain compiles to exec-mask
+     * branches around every element of the epilogue */
+    g = g > limit ? limit : g;
+    u = u > limit ? limit : (u < -limit ? -limit : u);
     const float e = __expf(-fabsf(g));
     /* 1 / (1 + e) for 1 + e in (1, 2]: the hardware reciprocal (1 ulp) and
      * one Newton step with fused multiply-adds, which lands on the
