@@ -22,7 +22,7 @@ import pytest
 import oracle as O
 from test_gpu_moe import open_store, random_slabs, moe_floor
 from test_gpu_prefill import prefill, floor_of, skewed_routing
-from tolerance import assert_close_combined
+from tolerance import assert_close_combined, record
 
 pytestmark = pytest.mark.gpu
 
@@ -100,9 +100,10 @@ def test_decode_clamps(store, slabs):
             outs[lim] = out
         want, eo = O.moe_forward(slabs, DIM, INTER, x, idx[None], w[None], limit=limit,
                                  want_expert_out=True)
-        assert_close_combined(outs[limit], want[0],
-                              np.maximum(moe_floor(eo, w[None], idx[None])[0], inner[0]),
-                              "decode limit=%g trial %d" % (limit, trial))
+        st = assert_close_combined(outs[limit], want[0],
+                                   np.maximum(moe_floor(eo, w[None], idx[None])[0], inner[0]),
+                                   "decode limit=%g trial %d" % (limit, trial))
+        record("swiglu_limit%g_decode_trial%d" % (limit, trial), st, clamp_fracs=[round(float(v), 4) for v in frac])
         assert not np.array_equal(outs[limit], outs[10.0])
 
 
@@ -118,6 +119,7 @@ def test_prefill_clamps(store, slabs, T, k):
             for lim, s in stores.items()}
     want, eo = O.moe_forward(slabs, DIM, INTER, x, idx, w, limit=limit,
                              want_expert_out=True, threads=8)
-    assert_close_combined(outs[limit], want, np.maximum(floor_of(eo, w, idx), inner),
-                          "prefill limit=%g T=%d k=%d" % (limit, T, k))
+    st = assert_close_combined(outs[limit], want, np.maximum(floor_of(eo, w, idx), inner),
+                               "prefill limit=%g T=%d k=%d" % (limit, T, k))
+    record("swiglu_limit%g_prefill_T%d_k%d" % (limit, T, k), st, clamp_fracs=[round(float(v), 4) for v in frac])
     assert not np.array_equal(outs[limit], outs[10.0])
