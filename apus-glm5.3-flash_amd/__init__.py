@@ -78,6 +78,8 @@ SIGNATURES = {
                                           c_int, c_vp, c_vp]),
     "apus_ghip_moe_prefill_dev_noalloc": (c_int, [c_vp, c_vp, c_size, c_vp, c_vp,
                                                   c_int, c_vp, c_vp]),
+    "apus_ghip_store_status": (c_int, [c_vp, c_vp, c_int,
+                                       ctypes.POINTER(ctypes.c_uint32)]),
     "apus_ghip_set_trace_events": (None, [ctypes.POINTER(c_vp), c_int]),
     "apus_ghip_stream_hold": (c_int, [c_vp, ctypes.c_uint32]),
     # include/apus_synth.h

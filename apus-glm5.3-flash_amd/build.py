@@ -71,9 +71,27 @@ def resource_usage(out):
     return usage, "\n".join(keep)
 
 
-def check_resources(usage):
+# kernels whose remarks must be present: if the compiler stops emitting the
+# resource-usage remarks, or words them differently, the gate would see
+# nothing and pass, so their absence fails the build instead
+REQUIRED_KERNELS = ("k_moe_decode", "k_pf_gemm", "k_fp8_gemv_stream", "k_fp8_gemm")
+
+
+def check_resources(usage, required=REQUIRED_KERNELS):
     """A kernel that spills VGPRs or uses scratch memory fails the build
-    (SGPR spills go to VGPR lanes, not memory, and are allowed)."""
+    (SGPR spills go to VGPR lanes, not memory, and are allowed), and so does
+    a required kernel with no parsed remarks (or no remarks at all)."""
+    if not usage:
+        raise RuntimeError("no kernel-resource-usage remarks parsed from the "
+                           "compiler output: the spill/scratch gate cannot run")
+    missing = [k for k in required if not any(k in name for name in usage)]
+    if missing:
+        raise RuntimeError("no resource-usage remarks for kernels: " + ", ".join(missing))
+    incomplete = sorted(n for n, u in usage.items()
+                        if "vgpr_spill" not in u or "scratch" not in u)
+    if incomplete:
+        raise RuntimeError("resource-usage remarks without spill/scratch figures: "
+                           + ", ".join(incomplete))
     bad = ["%s: %d VGPR spills, %d B/lane scratch"
            % (k, u.get("vgpr_spill", 0), u.get("scratch", 0))
            for k, u in sorted(usage.items())

@@ -945,6 +945,28 @@ static void store_bank(const ApusGhipStore *s, GhipBank *bk) {
     bk->dim = (uint32_t)s->dim;
     bk->inter = (uint32_t)s->inter;
     bk->nan_flags = s->nan_flags;
+    bk->err = s->ws.err;
+}
+
+int apus_ghip_store_status(ApusGhipStore *s, void *stream, int clear,
+                           uint32_t *code) {
+    if (!s || !code) {
+        ghip_seterr("store_status: no store or no code pointer");
+        return 1;
+    }
+    HIPCHK(hipStreamSynchronize((hipStream_t)stream));
+    uint32_t v = 0;
+    HIPCHK(hipMemcpy(&v, s->ws.err, 4, hipMemcpyDeviceToHost));
+    if (clear && v) HIPCHK(hipMemset(s->ws.err, 0, 4));
+    *code = v;
+    return 0;
+}
+
+/* The host-pointer MoE entries report only their own launch's failure: the
+ * sticky word is cleared on their stream before they launch. */
+static int store_status_clear(ApusGhipStore *s) {
+    HIPCHK(hipMemsetAsync(s->ws.err, 0, 4, G.stream));
+    return 0;
 }
 
 /* ------------------------------------------------------------------------ */
@@ -1052,17 +1074,17 @@ int apus_ghip_moe_decode(ApusGhipStore *s, const uint16_t *x,
     if (h2d(s->d_x, x, s->dim * 2) || h2d(s->d_idx, idx, (size_t)topk * 4)
         || h2d(s->d_w, w, (size_t)topk * 4))
         return 1;
+    if (store_status_clear(s)) return 1;
     if (apus_ghip_moe_decode_dev(s, s->d_x, NULL, s->d_idx, s->d_w, topk,
                                  s->d_out, G.stream))
         return 1;
     if (sync_out(out, s->d_out, s->dim * 2)) return 1;
     uint32_t err = 0;
-    HIPCHK(hipMemcpy(&err, s->ws.err, 4, hipMemcpyDeviceToHost));
+    if (apus_ghip_store_status(s, G.stream, 1, &err)) return 1;
     if (err) {
         ghip_seterr(err & 4u ? "moe_decode: the gate/up -> down hand-off wait ran out "
                                "(code %u)"
                              : "moe_decode: invalid expert id in routing (code %u)", err);
-        hipMemset(s->ws.err, 0, 4);
         return 1;
     }
     return 0;
@@ -1225,14 +1247,16 @@ int apus_ghip_moe_prefill(ApusGhipStore *s, const uint16_t *x, size_t T,
     if (h2d(G.pf_x, x, T * s->dim * 2) || h2d(G.pf_idx, idx, P * 4)
         || h2d(G.pf_w, w, P * 4))
         return 1;
+    if (store_status_clear(s)) return 1;
     if (apus_ghip_moe_prefill_dev(s, (const uint16_t *)G.pf_x, T,
                                   (const int32_t *)G.pf_idx, (const float *)G.pf_w,
                                   topk, (uint16_t *)G.pf_out, G.stream))
         return 1;
     if (sync_out(out, G.pf_out, T * s->dim * 2)) return 1;
-    uint32_t hdr[PF_HDR_WORDS];
+    uint32_t hdr[PF_HDR_WORDS], err = 0;
     HIPCHK(hipMemcpy(hdr, G.pf.hdr, sizeof hdr, hipMemcpyDeviceToHost));
-    if (hdr[PF_HDR_ERR]) {
+    if (apus_ghip_store_status(s, G.stream, 1, &err)) return 1;
+    if (hdr[PF_HDR_ERR] || err) {
         ghip_seterr("moe_prefill: invalid expert id in routing");
         return 1;
     }

@@ -67,6 +67,9 @@ typedef struct {
     size_t off_gw, off_gs, off_uw, off_us, off_dw, off_ds;
     uint32_t n_experts, dim, inter;
     const uint32_t *nan_flags;   /* device [n_experts] u32 (required by decode) or NULL */
+    uint32_t *err;               /* device u32, the store's sticky error word (2 = an
+                                    invalid expert id was dropped, 4 = a decode hand-off
+                                    wait ran out) or NULL */
 } GhipBank;
 
 /* K3: routed MoE decode for one token (routing, gate/up + SwiGLU, down +

@@ -535,10 +535,13 @@ __device__ __forceinline__ bool md_stage_h_wave(const uint32_t *hw, uint32_t q, 
 /* One launch of gridDim.x workgroups (one per CU), 8 waves each. hw: the
  * tagged h words ([max topk][inter] u32), tag: this launch's tag (1..65535;
  * the host clears hw whenever the tag wraps, so no stale word carries a
- * live tag). Every workgroup must be resident at once (one per CU, as the
- * LDS use makes it): a workgroup whose wait for h runs out (MD_SPIN_MAX
- * polls, a concurrently running kernel holding CUs can cause it) flags
- * err |= 4 and skips its down rows instead of hanging. */
+ * live tag). The hand-off needs every workgroup resident at once: the grid
+ * is one workgroup per CU, which an otherwise idle device always holds.
+ * When other work holds CUs, a workgroup may wait for a slot while the
+ * resident ones wait for its h: a wait for h that runs out (MD_SPIN_MAX
+ * polls) flags err |= 4 and that wave skips its down rows (in every later
+ * row group too) instead of hanging, so the launch always ends, and its
+ * output is invalid whenever the word holds 4 afterwards. */
 __global__ __launch_bounds__(MD_NW * 64, 1) void k_moe_decode(
     GhipBank bank, const uint16_t *__restrict__ x, const float *__restrict__ logits,
     const int32_t *__restrict__ idx, const float *__restrict__ w, int topk, float limit,
@@ -577,6 +580,10 @@ __global__ __launch_bounds__(MD_NW * 64, 1) void k_moe_decode(
     uint16_t *hs = (uint16_t *)dl;
     uint8_t *ring = dl + (size_t)MD_NW * inter * 2u;
     if (wv == 0 && logits) md_route_finish(sh, topk);
+    /* whether this wave's staged h is this launch's (false once a wait ran
+     * out: the wave then computes no down rows at all, in this row group
+     * or in a later one that reuses the staged h) */
+    bool hs_ok = true;
     for (uint32_t rg = blockIdx.x; rg * MD_T < dim; rg += gridDim.x) {
         const uint32_t r0 = rg * MD_T;
         for (uint32_t base = 0; base < nsel; base += MD_NW) {
@@ -585,9 +592,9 @@ __global__ __launch_bounds__(MD_NW * 64, 1) void k_moe_decode(
             /* wave w: h of slot base + w (once when all slots fit one
              * pass), then at once its down rows; a wave whose wait runs
              * out flags the error and computes nothing */
-            bool ok = true;
             if (base + wv < nsel && (base > 0 || rg == blockIdx.x || nsel > MD_NW))
-                ok = md_stage_h_wave(hw, base + wv, inter, tag, hs + (size_t)wv * inter);
+                hs_ok = md_stage_h_wave(hw, base + wv, inter, tag, hs + (size_t)wv * inter);
+            const bool ok = hs_ok;
             if (ok) {
                 md_phase_down(bank, sh, r0, base, hs, ring, hd);
             } else {

@@ -69,12 +69,13 @@ typedef float ghip_f32x16 __attribute__((ext_vector_type(16)));
 /* ------------------------------------------------------------------------ */
 
 /* One workgroup per PF_CHUNK pairs (pair p = t * topk + j). eid[p] = the
- * expert of p, or -1 when the id is out of range (flags hdr[PF_HDR_ERR]) or
- * repeats an earlier slot of the same token. cnt[chunk][e] = count. */
+ * expert of p, or -1 when the id is out of range (flags hdr[PF_HDR_ERR] and,
+ * when given, bit 2 of the store's sticky error word serr) or repeats an
+ * earlier slot of the same token. cnt[chunk][e] = count. */
 __global__ __launch_bounds__(1024) void k_pf_count(
     const int32_t *__restrict__ idx, uint32_t P, uint32_t topk, uint32_t E,
     uint32_t *__restrict__ cnt, int32_t *__restrict__ eid,
-    uint32_t *__restrict__ hdr) {
+    uint32_t *__restrict__ hdr, uint32_t *__restrict__ serr) {
     extern __shared__ uint32_t hist[];
     for (uint32_t i = threadIdx.x; i < E; i += 1024) hist[i] = 0;
     __syncthreads();
@@ -85,6 +86,7 @@ __global__ __launch_bounds__(1024) void k_pf_count(
         bool ok = e >= 0 && (uint32_t)e < E;
         if (!ok) {
             atomicOr(&hdr[PF_HDR_ERR], 1u);
+            if (serr) atomicOr(serr, 2u);
         } else {
             for (uint32_t jj = 0; jj < j; jj++)
                 if (idx[(size_t)t * topk + jj] == e) { ok = false; break; }
@@ -217,8 +219,11 @@ __global__ __launch_bounds__(1024) void k_pf_scatter(
 
 /* SwiGLU of the prefill epilogue: the clamp order and bf16 roundings of
  * c/gmoe.h:217-225 with the numpy-stable sigmoid (c/gmhc.h:157-160) on the
- * hardware exp2 and reciprocal (a few f32 ulps, far below the bf16 step
- * that follows; a tolerance-class result like every GEMM output). */
+ * hardware exp2 and reciprocal. Their f32 results may differ from libm's
+ * expf and an IEEE division by an ulp, but the bf16 value bf16(g * s(g))
+ * that follows does not: it is a function of the bf16 gate alone, and on
+ * all 65,536 gate values it equals the reference's (an exhaustive device
+ * test at the model's clamp limit). */
 __device__ __forceinline__ uint16_t pf_bf16_bits(float x) {
     /* the hardware RNE narrow (v_cvt_pk_bf16_f32): the reference's bits for
      * every finite value, subnormals included, and a quiet NaN for a NaN */
@@ -237,7 +242,16 @@ __device__ __forceinline__ uint16_t pf_swiglu(float accg, float accu, float limi
      * branches around every element of the epilogue */
     g = g > limit ? limit : g;
     u = u > limit ? limit : (u < -limit ? -limit : u);
-    const float e = __expf(-fabsf(g));
+    /* e = exp(-|g|) on the hardware exp2 (v_exp_f32), which flushes results
+     * below 2^-126 to zero: there (|g| > ~87.3, e subnormal as in libm's
+     * expf) the argument is raised by 64 (exactly: both have exponent >= 6)
+     * and the result scaled back by 2^-64, one rounding onto the subnormal
+     * grid. Over all 65,536 bf16 gate values the resulting h equals the
+     * one computed with the host's libm expf (checked exhaustively on the
+     * device against the oracle). */
+    const float y = -fabsf(g) * 1.44269504088896341f;
+    const bool tiny = y < -126.0f;
+    const float e = __builtin_amdgcn_exp2f(tiny ? y + 64.0f : y) * (tiny ? 0x1p-64f : 1.0f);
     /* 1 / (1 + e) for 1 + e in (1, 2]: the hardware reciprocal (1 ulp) and
      * one Newton step with fused multiply-adds, which lands on the
      * correctly rounded value (the IEEE division sequence costs ~10
@@ -1078,7 +1092,7 @@ extern "C" hipError_t ghip_launch_moe_prefill(const GhipBank *bank,
     hipError_t e;
     if ((e = ghip_launch_fill_u32(ws->hdr, PF_HDR_WORDS, 0u, st)) != hipSuccess) return e;
     GHIP_LAUNCH(e0, nullptr, k_pf_count, dim3(nch), dim3(1024), E * 4, st, idx,
-                (uint32_t)P, (uint32_t)topk, E, ws->cnt, ws->eid, ws->hdr);
+                (uint32_t)P, (uint32_t)topk, E, ws->cnt, ws->eid, ws->hdr, bank->err);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(k_pf_scan, dim3(1), dim3(1024), 0, st, ws->cnt, nch, E,
                        bank->nan_flags, (uint4 *)ws->tiles, ws->hdr);

@@ -134,7 +134,11 @@ int apus_ghip_fp8blk_dequant(const uint8_t *codes, const float *scales,
  * the exact-decode flag word and the split-K partial buffer of the GEMM
  * path (M >= 16). Calls must therefore not overlap in time: issue them on
  * one stream, and do not run them concurrently with the host-pointer
- * entry points (which use the backend's own stream). */
+ * entry points (which use the backend's own stream).
+ * Alignment: the GEMM path (M >= 16; weights read once) needs 16-byte
+ * aligned codes, x and y, N % 256 == 0 and K % 128 == 0; otherwise the
+ * rows go to the streaming GEMV in groups of <= 4, which re-reads the
+ * weights ceil(M / 4) times (same results within the tolerance, slower). */
 int apus_ghip_fp8blk_dequant_dev(const uint8_t *codes, const float *scales,
                                  uint16_t *out, size_t O, size_t K,
                                  int exact, void *stream);
@@ -263,6 +267,23 @@ int apus_ghip_moe_prefill(ApusGhipStore *s, const uint16_t *x, size_t T,
 int apus_ghip_moe_prefill_dev(ApusGhipStore *s, const uint16_t *x, size_t T,
                               const int32_t *idx, const float *w, int topk,
                               uint16_t *out, void *stream);
+
+/* Device-side failures of the asynchronous MoE entries. No counterpart in
+ * the reference: its backend ops are synchronous and return the failure
+ * themselves (c/backend_gmetal.h:111-119), which the host-pointer entries
+ * here still do. A *_dev call returns 0 once its launch is queued; what
+ * goes wrong on the device afterwards is ORed into the store's sticky
+ * error word: 2 = an expert id outside 0..n_experts-1 was dropped (decode
+ * or prefill; that pair is missing from the sum), 4 = a decode's gate/up
+ * -> down hand-off wait ran out (another kernel held CUs the launch
+ * needed; the output of that decode is invalid). Waits for `stream` (a
+ * hipStream_t, NULL = the null stream), stores the word in *code and,
+ * with clear != 0, resets it. The host-pointer decode and prefill reset
+ * the word before their own launch, so read a *_dev call's status before
+ * the next host-pointer MoE call on the store. Synchronous; not for
+ * streams under graph capture. 0 = the word was read. */
+int apus_ghip_store_status(ApusGhipStore *s, void *stream, int clear,
+                           uint32_t *code);
 
 /* Allocation-free variant of apus_ghip_moe_prefill_dev. No counterpart in
  * the reference: it is for callers that cannot allocate device memory

@@ -45,8 +45,23 @@ def test_resource_remarks_parsed_and_context_dropped():
 def test_spilling_kernel_fails_the_gate():
     b = _build_mod()
     ok, _ = b.resource_usage(_remarks("_Z1av", 0, 32, 0))
-    b.check_resources(ok)                      # SGPR spills alone pass
+    b.check_resources(ok, required=())         # SGPR spills alone pass
     for scratch, vgpr in ((0, 1), (4, 0)):
         bad, _ = b.resource_usage(_remarks("_Z1bv", scratch, 0, vgpr))
         with pytest.raises(RuntimeError, match="_Z1bv"):
-            b.check_resources(bad)
+            b.check_resources(bad, required=())
+
+
+def test_gate_fails_without_remarks():
+    """No parsed remarks, a required kernel without remarks, or a remark
+    block without its spill and scratch figures fail the build: a gate that
+    saw nothing must not pass."""
+    b = _build_mod()
+    with pytest.raises(RuntimeError, match="no kernel-resource-usage"):
+        b.check_resources({})
+    ok, _ = b.resource_usage(_remarks("_Z12k_moe_decodev", 0, 0, 0))
+    b.check_resources(ok, required=("k_moe_decode",))
+    with pytest.raises(RuntimeError, match="k_pf_gemm"):
+        b.check_resources(ok, required=("k_moe_decode", "k_pf_gemm"))
+    with pytest.raises(RuntimeError, match="without spill"):
+        b.check_resources({"_Z1cv": {"scratch": 0}}, required=())

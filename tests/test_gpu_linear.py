@@ -161,6 +161,25 @@ def test_linear_dev_entry(ghip, pkg):
                      "dev exact=%d" % exact)
 
 
+def test_linear_dev_unaligned_y(ghip, pkg):
+    """The GEMM path (M >= 16) stores 16-byte vectors, so it needs a 16-byte
+    aligned y; a y two bytes off goes to the streaming GEMV (4 rows per
+    launch, 2-byte stores) instead. Checked at M = 32 against the oracle,
+    with the elements either side of y left untouched."""
+    M, N, K = 32, 1024, 2048
+    c, s, x = synth_linear(pkg.load(), 0x53, M, N, K)
+    want = O.fp8_linear(c, s, x, threads=8)
+    guard = np.full(M * N + 16, 0x7E57, np.uint16)
+    dc, ds, dx, dy = G.dev(c), G.dev(s), G.dev(x), G.dev(guard)
+    yp = ctypes.c_void_p(G.vp(dy).value + 2)
+    assert ghip.apus_ghip_fp8blk_linear_dev(G.vp(dc), G.vp(ds), G.vp(dx), yp, M, N, K, -1,
+                                            G.stream()) == 0, ghip.apus_ghip_last_error()
+    got = G.host(dy, np.uint16, guard.shape)
+    assert got[0] == 0x7E57 and np.all(got[1 + M * N:] == 0x7E57), "wrote outside y"
+    assert_close(got[1:1 + M * N].reshape(M, N), want, floor_linear(c, s, x),
+                 "unaligned y, M=32")
+
+
 def test_deterministic(ghip, pkg):
     c, s, x = synth_linear(pkg.load(), 0x52, 2, 4096, 4096)
     y1 = gpu_linear(ghip, c, s, x)

@@ -334,6 +334,7 @@ def test_moe_decode_tag_wrap(ghip):
             assert np.array_equal(G.host(bo, np.uint16, (dim,)), want), \
                 "launch %d (k=%d) across the tag wrap" % (65534 + n, k)
         assert np.array_equal(G.host(do, np.uint16, (dim,)), fresh[0])
+        assert status(ghip, s) == 0, "no device failure across 65,539 launches"
     finally:
         ghip.apus_ghip_store_close(s)
 
@@ -394,3 +395,58 @@ def test_moe_decode_back_to_back_calls(small):
                                              G.vp(do), G.stream()) == 0
     for (dx, di, dw, do, k), want in zip(bufs, alone):
         assert np.array_equal(G.host(do, np.uint16, (dim,)), want), "k=%d back to back" % k
+    assert status(ghip, s) == 0
+
+
+def status(ghip, s, clear=1, stream=None):
+    code = ctypes.c_uint32(0xFFFFFFFF)
+    assert ghip.apus_ghip_store_status(s, stream, clear, ctypes.byref(code)) == 0, \
+        ghip.apus_ghip_last_error()
+    return code.value
+
+
+def test_store_status_reports_dev_failures(small):
+    """The asynchronous entries return 0 once queued; an id outside the bank
+    is dropped on the device and ORed into the store's sticky error word
+    (bit 2), which apus_ghip_store_status reads after the stream and clears
+    on request. A valid call leaves the word at 0, and the host-pointer
+    decode reports only its own launch (it resets the word first)."""
+    ghip, s, slabs, (E, dim, inter) = small
+    assert status(ghip, s) == 0
+    rng = np.random.default_rng(808)
+    x = O.f32_to_bf16(rng.standard_normal(dim).astype(np.float32))
+    good = np.array([1, 4, 9], np.int32)
+    bad = np.array([1, E, 9], np.int32)                 # id E is outside the bank
+    w = np.array([0.5, 0.3, 0.2], np.float32)
+    dx, dw, do = G.dev(x), G.dev(w), G.empty(dim * 2)
+    dg, db = G.dev(good), G.dev(bad)
+    assert ghip.apus_ghip_moe_decode_dev(s, G.vp(dx), None, G.vp(dg), G.vp(dw), 3,
+                                         G.vp(do), G.stream()) == 0
+    assert status(ghip, s) == 0
+    assert ghip.apus_ghip_moe_decode_dev(s, G.vp(dx), None, G.vp(db), G.vp(dw), 3,
+                                         G.vp(do), G.stream()) == 0
+    assert status(ghip, s, clear=0) == 2                # read, kept
+    assert status(ghip, s) == 2                         # read, cleared
+    assert status(ghip, s) == 0
+    # the decode without the dropped id: same output as the valid pair alone
+    want = np.empty(dim, np.uint16)
+    two, w2 = np.array([1, 9], np.int32), np.array([0.5, 0.2], np.float32)
+    assert ghip.apus_ghip_moe_decode(s, O.ptr(x), O.ptr(two), O.ptr(w2), 2,
+                                     O.ptr(want)) == 0
+    assert np.array_equal(G.host(do, np.uint16, (dim,)), want)
+    # prefill: the same word, bit 2
+    T = 3
+    xs = O.f32_to_bf16(rng.standard_normal((T, dim)).astype(np.float32))
+    pidx = np.array([[0, 1], [2, E + 5], [3, 4]], np.int32)
+    pw = np.ones((T, 2), np.float32)
+    px, pi, pwd, po = G.dev(xs), G.dev(pidx), G.dev(pw), G.empty(T * dim * 2)
+    assert ghip.apus_ghip_moe_prefill_dev(s, G.vp(px), T, G.vp(pi), G.vp(pwd), 2,
+                                          G.vp(po), G.stream()) == 0
+    assert status(ghip, s) == 2
+    # a pending device failure is not reported by a later host-pointer call
+    assert ghip.apus_ghip_moe_decode_dev(s, G.vp(dx), None, G.vp(db), G.vp(dw), 3,
+                                         G.vp(do), G.stream()) == 0
+    out = np.empty(dim, np.uint16)
+    assert ghip.apus_ghip_moe_decode(s, O.ptr(x), O.ptr(good), O.ptr(w), 3,
+                                     O.ptr(out)) == 0, ghip.apus_ghip_last_error()
+    assert status(ghip, s) == 0

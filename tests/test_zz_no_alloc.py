@@ -1,9 +1,11 @@
 """The allocation-free prefill entry point (apus_ghip_moe_prefill_dev_noalloc)
 against the existing apus_ghip_moe_prefill_dev on the same inputs: bitwise
 equal outputs on two calls in a row (the second smaller, so the fixed
-workspace holds the first call's leftovers), one call past the fixed
-workspace rejected with a clear error, and a prefill through the regular
-entry point in between that leaves the no-alloc workspace to itself."""
+workspace holds the first call's leftovers), the device's free memory
+unchanged across the no-alloc calls (they allocate nothing, whatever the
+regular workspace holds), one call past the fixed workspace rejected with a
+clear error, and a prefill through the regular entry point in between that
+leaves the no-alloc workspace to itself."""
 import ctypes
 
 import numpy as np
@@ -40,7 +42,20 @@ def test_noalloc_prefill_matches_regular(ghip):
             x = O.f32_to_bf16(rng.standard_normal((T, dim)).astype(np.float32))
             idx, w = skewed_routing(rng, T, E, k, hot=hot)
             cases.append((x, idx, w))
-        got = [run(ghip, ghip.apus_ghip_moe_prefill_dev_noalloc, s, *c) for c in cases]
+        # the no-alloc calls come first in the process's life of this store
+        # and allocate nothing: the device's free memory is the same before
+        # and after them (their buffers are allocated beforehand)
+        bufs = [(G.dev(x), G.dev(idx), G.dev(w), G.empty(idx.shape[0] * dim * 2), idx.shape)
+                for x, idx, w in cases]
+        G.rt().synchronize()
+        free0 = G.rt().mem_info()[0]
+        for dx, di, dw, do, (T, k) in bufs:
+            rc = ghip.apus_ghip_moe_prefill_dev_noalloc(s, G.vp(dx), T, G.vp(di), G.vp(dw),
+                                                        k, G.vp(do), G.stream())
+            assert rc == 0, ghip.apus_ghip_last_error()
+        G.rt().synchronize()
+        assert G.rt().mem_info()[0] == free0, "the no-alloc entry point allocated"
+        got = [G.host(do, np.uint16, (T, dim)) for _, _, _, do, (T, k) in bufs]
         ref = [run(ghip, ghip.apus_ghip_moe_prefill_dev, s, *c) for c in cases]
         for (x, idx, w), g, r in zip(cases, got, ref):
             assert np.array_equal(g, r), "T=%d: no-alloc differs from the regular entry" % len(x)
