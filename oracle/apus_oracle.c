@@ -653,3 +653,325 @@ int apo_moe_forward(const uint8_t *const *slabs, int n_experts,
     free(eo);
     return rc;
 }
+
+/* GEMM over many activation rows for the grouped checker: rows go in
+ * blocks of 8, held transposed ([k][8] f32) so one vector holds the 8 rows'
+ * k-th activations, and each output's 8 row sums advance together, lane r
+ * being row r's strictly sequential k chain from +0 (one fp32 mul then
+ * one add per k, as c/bf16.h:27-37): bitwise the scalar anchor, M times
+ * faster than one chain at a time. Four weight rows share each block. */
+typedef struct {
+    const uint16_t *w;
+    const float *xt;      /* [ceil(M/8)][K][8] widened, transposed x (zero pad) */
+    uint16_t *y;
+    size_t M, O, K;
+} ApoRowvecJob;
+
+static inline float apo_wf(const uint16_t *w, size_t i) { return apo_bf16_f32(w[i]); }
+
+#if APO_X86
+__attribute__((target("avx2")))
+static void apo_gemm_rows_rowvec(void *vj, size_t o0, size_t o1) {
+    const ApoRowvecJob *j = (const ApoRowvecJob *)vj;
+    const size_t K = j->K, M = j->M, O = j->O;
+    float res[4][8];
+    /* the 4 weight rows of an o block widened once, interleaved [k][4] */
+    float *wf = (float *)malloc(K * 4 * sizeof(float));
+    if (!wf) abort();
+    for (size_t o = o0; o < o1; o += 4) {
+        const size_t oc = o1 - o < 4 ? o1 - o : 4;
+        for (size_t q = 0; q < 4; q++) {
+            const uint16_t *wr = j->w + (o + (q < oc ? q : 0)) * K;
+            for (size_t k = 0; k < K; k++) wf[k * 4 + q] = apo_wf(wr, k);
+        }
+        for (size_t m0 = 0; m0 < M; m0 += 8) {
+            const float *xb = j->xt + (m0 / 8) * K * 8;
+            const size_t mc = M - m0 < 8 ? M - m0 : 8;
+            __m256 a0 = _mm256_setzero_ps(), a1 = a0, a2 = a0, a3 = a0;
+            for (size_t k = 0; k < K; k++) {
+                const __m256 xv = _mm256_loadu_ps(xb + k * 8);
+                const float *wk = wf + k * 4;
+                a0 = _mm256_add_ps(a0, _mm256_mul_ps(_mm256_broadcast_ss(wk), xv));
+                a1 = _mm256_add_ps(a1, _mm256_mul_ps(_mm256_broadcast_ss(wk + 1), xv));
+                a2 = _mm256_add_ps(a2, _mm256_mul_ps(_mm256_broadcast_ss(wk + 2), xv));
+                a3 = _mm256_add_ps(a3, _mm256_mul_ps(_mm256_broadcast_ss(wk + 3), xv));
+            }
+            _mm256_storeu_ps(res[0], a0);
+            _mm256_storeu_ps(res[1], a1);
+            _mm256_storeu_ps(res[2], a2);
+            _mm256_storeu_ps(res[3], a3);
+            for (size_t q = 0; q < oc; q++)
+                for (size_t r = 0; r < mc; r++)
+                    j->y[(m0 + r) * O + o + q] = apo_bf16_bits(res[q][r]);
+        }
+    }
+    free(wf);
+}
+#endif
+
+static void apo_gemm_rows_rowvec_scalar(void *vj, size_t o0, size_t o1) {
+    const ApoRowvecJob *j = (const ApoRowvecJob *)vj;
+    const size_t K = j->K;
+    for (size_t m = 0; m < j->M; m++) {
+        const float *xb = j->xt + (m / 8) * K * 8 + (m % 8);
+        for (size_t o = o0; o < o1; o++) {
+            float acc = 0.0f;
+            for (size_t k = 0; k < K; k++) {
+                float p = apo_wf(j->w + o * K, k) * xb[k * 8];
+                acc = acc + p;
+            }
+            j->y[m * j->O + o] = apo_bf16_bits(acc);
+        }
+    }
+}
+
+static int apo_gemm_rowvec(const uint16_t *w, const uint16_t *x, uint16_t *y,
+                           size_t M, size_t O, size_t K, int threads) {
+    const size_t nb = (M + 7) / 8;
+    float *xt = (float *)calloc(nb * K * 8 > 0 ? nb * K * 8 : 1, sizeof(float));
+    if (!xt) return 1;
+    for (size_t m = 0; m < M; m++)
+        for (size_t k = 0; k < K; k++)
+            xt[(m / 8) * K * 8 + k * 8 + (m % 8)] = apo_bf16_f32(x[m * K + k]);
+    ApoRowvecJob j = { w, xt, y, M, O, K };
+#if APO_X86
+    if (__builtin_cpu_supports("avx2"))
+        apo_pool_run(O, apo_gemm_rows_rowvec, &j, threads);
+    else
+#endif
+        apo_pool_run(O, apo_gemm_rows_rowvec_scalar, &j, threads);
+    free(xt);
+    return 0;
+}
+
+/* The same GEMM with every dot product summed in f64 (the bf16 x bf16
+ * products are exact; an f64 sum of K <= 16384 of them is within ~2^-39
+ * relative of the exact sum), then rounded to f32 and to bf16: a yardstick
+ * free of any fp32 summation order, not a reference function. Rows in
+ * blocks of 4 (one f64 vector), 4 weight rows per block. */
+typedef struct {
+    const uint16_t *w;
+    const double *xt;     /* [ceil(M/4)][K][4] */
+    uint16_t *y;
+    size_t M, O, K;
+} ApoRowvec64Job;
+
+#if APO_X86
+__attribute__((target("avx2")))
+static void apo_gemm_rows_rowvec64(void *vj, size_t o0, size_t o1) {
+    const ApoRowvec64Job *j = (const ApoRowvec64Job *)vj;
+    const size_t K = j->K, M = j->M, O = j->O;
+    double res[4][4];
+    double *wf = (double *)malloc(K * 4 * sizeof(double));
+    if (!wf) abort();
+    for (size_t o = o0; o < o1; o += 4) {
+        const size_t oc = o1 - o < 4 ? o1 - o : 4;
+        for (size_t q = 0; q < 4; q++) {
+            const uint16_t *wr = j->w + (o + (q < oc ? q : 0)) * K;
+            for (size_t k = 0; k < K; k++) wf[k * 4 + q] = (double)apo_wf(wr, k);
+        }
+        for (size_t m0 = 0; m0 < M; m0 += 4) {
+            const double *xb = j->xt + (m0 / 4) * K * 4;
+            const size_t mc = M - m0 < 4 ? M - m0 : 4;
+            __m256d a0 = _mm256_setzero_pd(), a1 = a0, a2 = a0, a3 = a0;
+            for (size_t k = 0; k < K; k++) {
+                const __m256d xv = _mm256_loadu_pd(xb + k * 4);
+                const double *wk = wf + k * 4;
+                a0 = _mm256_add_pd(a0, _mm256_mul_pd(_mm256_broadcast_sd(wk), xv));
+                a1 = _mm256_add_pd(a1, _mm256_mul_pd(_mm256_broadcast_sd(wk + 1), xv));
+                a2 = _mm256_add_pd(a2, _mm256_mul_pd(_mm256_broadcast_sd(wk + 2), xv));
+                a3 = _mm256_add_pd(a3, _mm256_mul_pd(_mm256_broadcast_sd(wk + 3), xv));
+            }
+            _mm256_storeu_pd(res[0], a0);
+            _mm256_storeu_pd(res[1], a1);
+            _mm256_storeu_pd(res[2], a2);
+            _mm256_storeu_pd(res[3], a3);
+            for (size_t q = 0; q < oc; q++)
+                for (size_t r = 0; r < mc; r++)
+                    j->y[(m0 + r) * O + o + q] = apo_bf16_bits((float)res[q][r]);
+        }
+    }
+    free(wf);
+}
+#endif
+
+static void apo_gemm_rows_rowvec64_scalar(void *vj, size_t o0, size_t o1) {
+    const ApoRowvec64Job *j = (const ApoRowvec64Job *)vj;
+    const size_t K = j->K;
+    for (size_t m = 0; m < j->M; m++) {
+        const double *xb = j->xt + (m / 4) * K * 4 + (m % 4);
+        for (size_t o = o0; o < o1; o++) {
+            double acc = 0.0;
+            for (size_t k = 0; k < K; k++) acc += (double)apo_wf(j->w + o * K, k) * xb[k * 4];
+            j->y[m * j->O + o] = apo_bf16_bits((float)acc);
+        }
+    }
+}
+
+static int apo_gemm_rowvec64(const uint16_t *w, const uint16_t *x, uint16_t *y,
+                             size_t M, size_t O, size_t K, int threads) {
+    const size_t nb = (M + 3) / 4;
+    double *xt = (double *)calloc(nb * K * 4 > 0 ? nb * K * 4 : 1, sizeof(double));
+    if (!xt) return 1;
+    for (size_t m = 0; m < M; m++)
+        for (size_t k = 0; k < K; k++)
+            xt[(m / 4) * K * 4 + k * 4 + (m % 4)] = (double)apo_bf16_f32(x[m * K + k]);
+    ApoRowvec64Job j = { w, xt, y, M, O, K };
+#if APO_X86
+    if (__builtin_cpu_supports("avx2"))
+        apo_pool_run(O, apo_gemm_rows_rowvec64, &j, threads);
+    else
+#endif
+        apo_pool_run(O, apo_gemm_rows_rowvec64_scalar, &j, threads);
+    free(xt);
+    return 0;
+}
+
+/* apo_moe_forward computed expert by expert, for checks at full size: each
+ * used expert is dequantized once and its tokens run as one M-row GEMM per
+ * matrix (c/bf16.h:27-37 makes every output row M-independent, so the
+ * per-pair outputs are the per-token loop's bits), the per-pair outputs
+ * are kept, and each token's ascending-expert combine (c/gmoe.h:307-320)
+ * follows. Bitwise equal to apo_moe_forward. */
+static int apo_moe_grouped(const uint8_t *const *slabs, int n_experts,
+                           size_t dim, size_t inter, float limit,
+                           const uint16_t *x, size_t T, const int32_t *idx,
+                           const float *w, int topk, uint16_t *out,
+                           uint16_t *expert_out, double *floor_out, int threads,
+                           int sums64) {
+    int (*gemm)(const uint16_t *, const uint16_t *, uint16_t *, size_t, size_t, size_t,
+                int) = sums64 ? apo_gemm_rowvec64 : apo_gemm_rowvec;
+    const size_t P = T * (size_t)topk, pn = 3 * inter * dim;
+    int rc = 0;
+    /* kept pairs: the first slot of each expert id in a token */
+    int32_t *keep = (int32_t *)malloc((P ? P : 1) * sizeof(int32_t));
+    size_t *cnt = (size_t *)calloc((size_t)n_experts + 1, sizeof(size_t));
+    size_t *list = (size_t *)malloc((P ? P : 1) * sizeof(size_t));
+    uint16_t *eo = expert_out ? expert_out
+                              : (uint16_t *)malloc((P ? P : 1) * dim * 2);
+    uint16_t *payload = (uint16_t *)malloc(pn * 2);
+    /* floor_out: |down weights| of the current expert, and per pair the
+     * expert-output floor F[j] = sum_i |h_i * wd[j,i]| (bf16) */
+    uint16_t *dabs = floor_out ? (uint16_t *)malloc(dim * inter * 2) : NULL;
+    uint16_t *fe = floor_out ? (uint16_t *)malloc((P ? P : 1) * dim * 2) : NULL;
+    if (!keep || !cnt || !list || !eo || !payload || (floor_out && (!dabs || !fe))) rc = 1;
+    for (size_t p = 0; p < P && !rc; p++) {
+        const size_t t = p / (size_t)topk, j = p % (size_t)topk;
+        const int32_t e = idx[p];
+        int ok = e >= 0 && e < n_experts;
+        for (size_t jj = 0; jj < j && ok; jj++)
+            if (idx[t * (size_t)topk + jj] == e) ok = 0;
+        keep[p] = ok ? e : -1;
+        if (ok) cnt[e + 1]++;
+    }
+    for (int e = 0; e < n_experts && !rc; e++) cnt[e + 1] += cnt[e];
+    if (!rc) {
+        size_t *at = (size_t *)malloc(((size_t)n_experts + 1) * sizeof(size_t));
+        if (!at) rc = 1;
+        else {
+            memcpy(at, cnt, ((size_t)n_experts + 1) * sizeof(size_t));
+            for (size_t p = 0; p < P; p++)
+                if (keep[p] >= 0) list[at[keep[p]]++] = p;
+            free(at);
+        }
+    }
+    for (int e = 0; e < n_experts && !rc; e++) {
+        const size_t M = cnt[e + 1] - cnt[e];
+        if (!M) continue;
+        const size_t *pl = list + cnt[e];
+        uint16_t *xe = (uint16_t *)malloc(M * dim * 2);
+        uint16_t *g = (uint16_t *)malloc(M * inter * 2);
+        uint16_t *u = (uint16_t *)malloc(M * inter * 2);
+        uint16_t *oe = (uint16_t *)malloc(M * dim * 2);
+        if (!xe || !g || !u || !oe) rc = 1;
+        if (!rc) {
+            apo_slab_dequant(slabs[e], dim, inter, payload, threads);
+            for (size_t m = 0; m < M; m++)
+                memcpy(xe + m * dim, x + (pl[m] / (size_t)topk) * dim, dim * 2);
+            rc |= gemm(payload, xe, g, M, inter, dim, threads);
+            rc |= gemm(payload + inter * dim, xe, u, M, inter, dim, threads);
+            /* c/gmoe.h:217-225, the same steps as apo_swiglu_expert */
+            for (size_t i = 0; i < M * inter; i++) {
+                float gv = apo_bf16_f32(g[i]), uv = apo_bf16_f32(u[i]);
+                if (gv > limit) gv = limit;
+                if (uv > limit) uv = limit;
+                else if (uv < -limit) uv = -limit;
+                float hv = apo_bf16_round(gv * apo_sigmoid_np(gv));
+                g[i] = apo_bf16_bits(apo_bf16_round(hv * uv));
+            }
+            rc |= gemm(payload + 2 * inter * dim, g, oe, M, dim, inter, threads);
+            for (size_t m = 0; m < M; m++)
+                memcpy(eo + pl[m] * dim, oe + m * dim, dim * 2);
+            if (floor_out && !rc) {
+                /* |h| . |wd|^T: the sum of the down GEMM's term magnitudes */
+                const uint16_t *pd = payload + 2 * inter * dim;
+                for (size_t i = 0; i < dim * inter; i++) dabs[i] = pd[i] & 0x7fffu;
+                for (size_t i = 0; i < M * inter; i++) g[i] &= 0x7fffu;
+                rc |= apo_gemm_rowvec64(dabs, g, oe, M, dim, inter, threads);
+                for (size_t m = 0; m < M; m++)
+                    memcpy(fe + pl[m] * dim, oe + m * dim, dim * 2);
+            }
+        }
+        free(xe); free(g); free(u); free(oe);
+    }
+    /* c/gmoe.h:307-320 per token: ascending expert id over its kept pairs */
+    float *y = (float *)malloc(dim * sizeof(float));
+    if (!y) rc = 1;
+    for (size_t t = 0; t < T && !rc; t++) {
+        for (size_t i = 0; i < dim; i++) y[i] = 0.0f;
+        int last = -1;
+        for (;;) {
+            size_t best = P;
+            for (int j = 0; j < topk; j++) {
+                const size_t p = t * (size_t)topk + (size_t)j;
+                if (keep[p] > last && (best == P || keep[p] < keep[best])) best = p;
+            }
+            if (best == P) break;
+            last = keep[best];
+            const uint16_t *o = eo + best * dim;
+            const float wt = w[best];
+            for (size_t i = 0; i < dim; i++) {
+                float contrib = apo_bf16_round(apo_bf16_f32(o[i]) * wt);
+                y[i] = apo_bf16_round(y[i] + contrib);
+            }
+            if (floor_out)
+                for (size_t i = 0; i < dim; i++)
+                    floor_out[t * dim + i] += fabs((double)wt)
+                                              * (double)apo_bf16_f32(fe[best * dim + i]);
+        }
+        for (size_t i = 0; i < dim; i++) out[t * dim + i] = apo_bf16_bits(y[i]);
+    }
+    free(y);
+    free(dabs); free(fe);
+    free(keep); free(cnt); free(list); free(payload);
+    if (!expert_out) free(eo);
+    return rc;
+}
+
+int apo_moe_forward_grouped(const uint8_t *const *slabs, int n_experts,
+                            size_t dim, size_t inter, float limit,
+                            const uint16_t *x, size_t T, const int32_t *idx,
+                            const float *w, int topk, uint16_t *out,
+                            uint16_t *expert_out, int threads) {
+    return apo_moe_grouped(slabs, n_experts, dim, inter, limit, x, T, idx, w, topk, out,
+                           expert_out, NULL, threads, 0);
+}
+
+int apo_moe_floor_grouped(const uint8_t *const *slabs, int n_experts,
+                          size_t dim, size_t inter, float limit,
+                          const uint16_t *x, size_t T, const int32_t *idx,
+                          const float *w, int topk, uint16_t *out,
+                          double *floor_out, int threads) {
+    for (size_t i = 0; i < T * dim; i++) floor_out[i] = 0.0;
+    return apo_moe_grouped(slabs, n_experts, dim, inter, limit, x, T, idx, w, topk, out,
+                           NULL, floor_out, threads, 0);
+}
+
+int apo_moe_chain64_grouped(const uint8_t *const *slabs, int n_experts,
+                            size_t dim, size_t inter, float limit,
+                            const uint16_t *x, size_t T, const int32_t *idx,
+                            const float *w, int topk, uint16_t *out,
+                            uint16_t *expert_out, int threads) {
+    return apo_moe_grouped(slabs, n_experts, dim, inter, limit, x, T, idx, w, topk, out,
+                           expert_out, NULL, threads, 1);
+}

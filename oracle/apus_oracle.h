@@ -101,6 +101,38 @@ int apo_moe_forward(const uint8_t *const *slabs, int n_experts,
                     const float *w, int topk, uint16_t *out,
                     uint16_t *expert_out, int threads);
 
+/* The same result computed expert by expert (each used expert dequantized
+ * once, its tokens as one M-row GEMM per matrix; bitwise equal to
+ * apo_moe_forward by the M-independence of c/bf16.h:27-37), for checks at
+ * full size. expert_out (optional) [T, topk, dim]: out_e per kept (token,
+ * slot); the entries of dropped slots are left as they are. */
+int apo_moe_forward_grouped(const uint8_t *const *slabs, int n_experts,
+                            size_t dim, size_t inter, float limit,
+                            const uint16_t *x, size_t T, const int32_t *idx,
+                            const float *w, int topk, uint16_t *out,
+                            uint16_t *expert_out, int threads);
+
+/* Test yardstick, not a reference function: apo_moe_forward_grouped with
+ * every GEMM dot product summed in f64 (then rounded to f32 and bf16 at
+ * the reference's rounding points; SwiGLU and combine unchanged), free of
+ * any fp32 summation order. */
+int apo_moe_chain64_grouped(const uint8_t *const *slabs, int n_experts,
+                            size_t dim, size_t inter, float limit,
+                            const uint16_t *x, size_t T, const int32_t *idx,
+                            const float *w, int topk, uint16_t *out,
+                            uint16_t *expert_out, int threads);
+
+/* Test helper for the combine's tolerance floor (not a reference
+ * function): out as apo_moe_forward_grouped, and floor_out [T, dim] f64 =
+ * sum over the token's kept pairs of |w_e| * sum_i |h_i * wd_e[j,i]|, the
+ * expert-output floor (the down GEMM's term magnitudes, h the reference's)
+ * carried through the combine weights. */
+int apo_moe_floor_grouped(const uint8_t *const *slabs, int n_experts,
+                          size_t dim, size_t inter, float limit,
+                          const uint16_t *x, size_t T, const int32_t *idx,
+                          const float *w, int topk, uint16_t *out,
+                          double *floor_out, int threads);
+
 /* Harness routing (configs 2-4 of the bench spec; NOT the reference's
  * sigmoid router): idx = stable top-k of logits (ties -> lower index),
  * w = softmax over the k selected logits: m = logit[idx[0]],

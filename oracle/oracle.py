@@ -55,6 +55,12 @@ _ORACLE_SIGS = {
     "apo_slab_dequant": (None, [c_vp, c_size, c_size, c_vp, c_int]),
     "apo_moe_forward": (c_int, [c_vp, c_int, c_size, c_size, c_float, c_vp,
                                 c_size, c_vp, c_vp, c_int, c_vp, c_vp, c_int]),
+    "apo_moe_forward_grouped": (c_int, [c_vp, c_int, c_size, c_size, c_float, c_vp,
+                                        c_size, c_vp, c_vp, c_int, c_vp, c_vp, c_int]),
+    "apo_moe_chain64_grouped": (c_int, [c_vp, c_int, c_size, c_size, c_float, c_vp,
+                                        c_size, c_vp, c_vp, c_int, c_vp, c_vp, c_int]),
+    "apo_moe_floor_grouped": (c_int, [c_vp, c_int, c_size, c_size, c_float, c_vp,
+                                      c_size, c_vp, c_vp, c_int, c_vp, c_vp, c_int]),
     "apo_route_softmax": (None, [c_vp, c_int, c_int, c_vp, c_vp]),
     "apo_gate_dot": (c_float, [c_vp, c_vp, c_size]),
     "apo_gmoe_router": (None, [c_vp, c_vp, c_int, c_size, c_int, c_float, c_vp,
@@ -241,9 +247,11 @@ def route_softmax(logits, k):
 
 
 def moe_forward(slabs, dim, inter, x, idx, w, limit=10.0, threads=1,
-                want_expert_out=False):
+                want_expert_out=False, grouped=False, chain64=False):
     """slabs: list of uint8 arrays (one slab per expert id; None allowed for
-    experts no token routes to)."""
+    experts no token routes to). grouped: compute expert by expert
+    (apo_moe_forward_grouped, the same bits, far faster at many tokens).
+    chain64: the f64-sum yardstick (apo_moe_chain64_grouped) instead."""
     E = len(slabs)
     arr = (c_vp * E)()
     for e, s in enumerate(slabs):
@@ -255,8 +263,28 @@ def moe_forward(slabs, dim, inter, x, idx, w, limit=10.0, threads=1,
     k = idx.shape[1]
     out = np.empty((T, dim), np.uint16)
     eo = np.empty((T, k, dim), np.uint16) if want_expert_out else None
-    rc = lib().apo_moe_forward(arr, E, dim, inter, limit, ptr(x), T, ptr(idx),
-                               ptr(w), k, ptr(out),
-                               ptr(eo) if eo is not None else None, threads)
+    fn = (lib().apo_moe_chain64_grouped if chain64 else
+          lib().apo_moe_forward_grouped if grouped else lib().apo_moe_forward)
+    rc = fn(arr, E, dim, inter, limit, ptr(x), T, ptr(idx), ptr(w), k, ptr(out),
+            ptr(eo) if eo is not None else None, threads)
     assert rc == 0
     return (out, eo) if want_expert_out else out
+
+
+def moe_expert_floor(slabs, dim, inter, x, idx, w, limit=10.0, threads=1):
+    """Per output element, sum over the token's kept pairs of |w_e| *
+    sum_i |h_i * wd_e[j, i]| (f64, [T, dim]): the combine's tolerance floor
+    that carries each expert output's own floor (apo_moe_floor_grouped)."""
+    E = len(slabs)
+    arr = (c_vp * E)()
+    for e, s in enumerate(slabs):
+        arr[e] = s.ctypes.data if s is not None else None
+    x = np.ascontiguousarray(x, np.uint16).reshape(-1, dim)
+    T = x.shape[0]
+    idx = np.ascontiguousarray(idx, np.int32).reshape(T, -1)
+    w = np.ascontiguousarray(w, np.float32).reshape(T, -1)
+    out = np.empty((T, dim), np.uint16)
+    fl = np.empty((T, dim), np.float64)
+    assert lib().apo_moe_floor_grouped(arr, E, dim, inter, limit, ptr(x), T, ptr(idx),
+                                       ptr(w), idx.shape[1], ptr(out), ptr(fl), threads) == 0
+    return fl

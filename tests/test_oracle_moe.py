@@ -250,3 +250,97 @@ def test_slab_layout_arithmetic():
     r = O.lib().apo_slab_layout(200, 136)       # inter 136 -> 2 blocks, dim 2
     nb = 2 * 2 * 4
     assert r.bytes == 2 * (136 * 200 + nb) + 200 * 136 + nb
+
+
+@pytest.mark.parametrize("dim,inter", [(256, 128), (130, 70)])
+def test_grouped_forward_equals_per_token_loop(dim, inter):
+    """apo_moe_forward_grouped (expert by expert, M-row GEMMs) returns the
+    per-token loop's bits: outputs and per-pair expert outputs, with
+    repeated ids (first slot kept), ids outside the bank (dropped), ragged
+    experts (some empty, one in every token), ragged shapes (row counts and
+    output widths off the 8-row and 4-column blocks) and a thread-count
+    change."""
+    E, k, T = 9, 4, 37
+    rng = np.random.default_rng(99)
+    slabs = _bank(dim, inter, E, rng)
+    x = O.f32_to_bf16((rng.standard_normal((T, dim)) * 2).astype(np.float32))
+    idx = np.stack([np.concatenate([[2], rng.permutation([e for e in range(E - 2)
+                                                          if e != 2])[:k - 1]])
+                    for _ in range(T)]).astype(np.int32)
+    idx[3] = [5, 5, 1, 5]                               # repeats
+    idx[7, 2] = E + 3                                   # outside the bank
+    w = rng.uniform(0.05, 0.6, (T, k)).astype(np.float32)
+    want, eo = O.moe_forward(slabs, dim, inter, x, idx, w, want_expert_out=True)
+    for th in (1, 5):
+        got, geo = O.moe_forward(slabs, dim, inter, x, idx, w, want_expert_out=True,
+                                 grouped=True, threads=th)
+        assert np.array_equal(got, want)
+        for t in range(T):
+            seen = set()
+            for j in range(k):
+                e = int(idx[t, j])
+                if 0 <= e < E and e not in seen:
+                    assert np.array_equal(geo[t, j], eo[t, j]), (t, j)
+                seen.add(e)
+
+
+def test_chain64_yardstick_matches_numpy_f64():
+    """The f64-sum yardstick (apo_moe_chain64_grouped) against the same chain
+    written with numpy's f64 matmuls: one expert, top-1, weight 1, so the
+    output is the expert's own. The sums differ only in f64 order, far
+    below the f32 rounding that follows: equal almost everywhere, never
+    more than one bf16 ulp apart; and it is a different yardstick from the
+    fp32 oracle (some outputs differ)."""
+    dim, inter, T = 512, 256, 24
+    rng = np.random.default_rng(64)
+    slabs = _bank(dim, inter, 1, rng)
+    x = O.f32_to_bf16((rng.standard_normal((T, dim)) * 3).astype(np.float32))
+    idx = np.zeros((T, 1), np.int32)
+    w = np.ones((T, 1), np.float32)
+    got = O.moe_forward(slabs, dim, inter, x, idx, w, chain64=True, threads=4)
+    pl = np.empty(3 * inter * dim, np.uint16)
+    O.lib().apo_slab_dequant(O.ptr(slabs[0]), dim, inter, O.ptr(pl), 1)
+    f = O.bf16_to_f32(pl).astype(np.float64)
+    wg, wu = f[:inter * dim].reshape(inter, dim), f[inter * dim:2 * inter * dim].reshape(inter, dim)
+    wd = f[2 * inter * dim:].reshape(dim, inter)
+    r = lambda v: O.bf16_to_f32(O.f32_to_bf16(np.asarray(v, np.float32)))  # noqa: E731
+    xf = O.bf16_to_f32(x).astype(np.float64)
+    g = np.minimum(r(xf @ wg.T), np.float32(10))
+    u = np.clip(r(xf @ wu.T), -10, 10).astype(np.float32)
+    sig = np.vectorize(lambda v: O.lib().apo_sigmoid_np(float(v)), otypes=[np.float32])
+    h = r(r(g * sig(g)) * u)
+    want = O.f32_to_bf16((h.astype(np.float64) @ wd.T).astype(np.float32))
+    from tolerance import bf16_ord
+    d = np.abs(bf16_ord(got) - bf16_ord(want))
+    assert d.max() <= 1 and (d == 0).mean() >= 0.999, (d.max(), (d == 0).mean())
+    f32 = O.moe_forward(slabs, dim, inter, x, idx, w, grouped=True, threads=4)
+    assert not np.array_equal(f32, got)
+
+
+def test_expert_floor_helper():
+    """moe_expert_floor = sum over a token's kept pairs of |w_e| * sum_i
+    |h_i * wd_e[j, i]|, recomputed from the oracle's own h (swiglu_expert)
+    and the dequantized down weights in numpy (the helper rounds each
+    expert's sum to bf16: within 2^-8 relative)."""
+    dim, inter, E, k, T = 128, 64, 6, 3, 5
+    rng = np.random.default_rng(7)
+    slabs = _bank(dim, inter, E, rng)
+    x = O.f32_to_bf16((rng.standard_normal((T, dim)) * 2).astype(np.float32))
+    idx = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int32)
+    idx[1, 2] = idx[1, 0]                               # a repeat counts once
+    w = rng.uniform(-0.6, 0.6, (T, k)).astype(np.float32)
+    got = O.moe_expert_floor(slabs, dim, inter, x, idx, w, threads=2)
+    want = np.zeros((T, dim))
+    for t in range(T):
+        seen = set()
+        for j in range(k):
+            e = int(idx[t, j])
+            if e in seen:
+                continue
+            seen.add(e)
+            pg, pu, pd = _expert_of(slabs[e], dim, inter)
+            h = O.swiglu_expert(pg, pu, pd, x[t])[3]
+            F = np.abs(O.bf16_to_f32(pd).astype(np.float64)) @ np.abs(
+                O.bf16_to_f32(h).astype(np.float64))
+            want[t] += abs(float(w[t, j])) * F
+    assert np.allclose(got, want, rtol=2.0 ** -8, atol=0)

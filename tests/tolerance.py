@@ -9,7 +9,16 @@ meaningful where the exact result cancels to ~0:
   expert output      floor = sum_i |h_i * wd_i|         (the down GEMM's
                      terms: h comes out of the GPU's own gate/up GEMM, so an
                      ulp step of one h_i is a legitimate input difference)
-  MoE combine output floor = sum_e |contrib_e|         (the combined terms)
+  MoE combine output floor = sum_e |contrib_e|         (the combined terms),
+                     or, for the full-size checks, sum_e |w_e| * sum_i
+                     |h_i * wd_i| when larger: each expert output's own
+                     floor carried through the combine weights. Where an
+                     expert's down GEMM cancels (|o_e| << sum_i |h_i wd_i|)
+                     its legitimate one-ulp steps are of the terms' size,
+                     not of o_e's; measured at configs 3 and 4, every output
+                     above 1e-2 under the combine-only floor had the GPU on
+                     the f64-sum value and the reference's sequential sum
+                     off it.
 An fp32 reordering moves a sum by ~sqrt(K)*2^-24*sum|terms|, far below the
 floor; a wrong term or index moves it by O(|term|), far above 1e-2.
 GEMV/GEMM outputs (and a single expert's output) take the ulp test as is;
