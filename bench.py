@@ -161,6 +161,40 @@ def kernel_times(lib, rt, step, first, steps, n_ev, pairs):
             for name, (a, b) in pairs.items()}
 
 
+def store_errors(lib, store):
+    """The store's sticky device error word (apus_ghip_store_status: 2 = an
+    expert id was dropped, 4 = a decode hand-off wait ran out), read and
+    cleared after the timed work; 0 = every timed step ran in full."""
+    code = ctypes.c_uint32(0xFFFFFFFF)
+    rc = lib.apus_ghip_store_status(store, None, 1, ctypes.byref(code))
+    if rc:
+        raise RuntimeError("apus_ghip_store_status: %s" % lib.apus_ghip_last_error())
+    return int(code.value)
+
+
+def verify(r, cpu):
+    """The bench object's "verified" record: the device error words of the
+    timed work, and the output one step produced (outside the timed region)
+    against the reference CPU path's output for the same inputs, which the
+    cpu_baseline leg computes while it is timed (the leg's own check; None
+    without a CPU leg). Tolerance of tests/tolerance.py."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from tolerance import compare_combined, ULP_FRAC_MIN, REL_MAX
+    v = {"device_errors": r.get("_device_errors", 0), "output": None}
+    ok = v["device_errors"] == 0
+    ref = (cpu or {}).get("_ref_out")
+    if ref is not None and r.get("_gpu_out") is not None:
+        st = compare_combined(r["_gpu_out"], ref["out"], ref["floor"])
+        good = st["frac_le1ulp_scaled"] >= ULP_FRAC_MIN and st["max_rel"] <= REL_MAX
+        v["output"] = {"against": ref["what"], "n": st["n"],
+                       "frac_le1ulp": round(st["frac_le1ulp"], 6),
+                       "frac_le1ulp_scaled": round(st["frac_le1ulp_scaled"], 6),
+                       "max_rel": round(st["max_rel"], 6), "ok": bool(good)}
+        ok = ok and good
+    v["ok"] = bool(ok)
+    return v
+
+
 # --------------------------------------------------------------------------
 # config 2: MoE decode
 # --------------------------------------------------------------------------
@@ -213,6 +247,10 @@ def bench_moe_decode(lib, pkg, rt, steps, warmup, rotate=64):
     ms = timed(rt, st, step, warmup, steps)
     wall = time.perf_counter() - t0
     kt = kernel_times(lib, rt, step, warmup + steps, steps, 2, {"k_moe_decode": (0, 1)})
+    # checks outside the timed region: no step lost its work on the device,
+    # and rotation 0's output (every step of it writes the same bits)
+    errors = store_errors(lib, store)
+    out0 = d_out.download(np.uint16, (rotate, dim))[0]
     nbytes, flops, _ = moe_algorithmic_bytes(E, k, dim, inter)
     gbs = nbytes / (ms * 1e-3) / 1e9
     lib.apus_ghip_store_close(store)
@@ -221,7 +259,8 @@ def bench_moe_decode(lib, pkg, rt, steps, warmup, rotate=64):
             "kernel_bytes": nbytes, "kernel_flops": flops,
             "launch_ms": {n: round(v, 5) for n, v in kt.items()}}
     return {
-        "ms_per_step": ms, "value": gbs, "wall_s": wall,
+        "ms_per_step": ms, "value": gbs, "wall_s": wall, "one_launch_per_step": True,
+        "_device_errors": errors, "_gpu_out": out0,
         "weight_bytes": k * 3 * inter * dim,
         "bytes": nbytes, "flops": flops, **kern,
         "config": {"workload": "moe_decode (BASELINE config 2)", "experts": E,
@@ -270,6 +309,7 @@ def cpu_moe_decode(lib, budget_s=12.0):
     x = np.empty(dim, np.uint16)
     ntok, t_tok = 0, 0.0
     eo = np.empty(dim, np.uint16)
+    ref_out, floor = None, np.zeros(dim)
     while t_tok < budget_s and ntok < 4000:
         lib.apus_synth_bf16_normal(P(x), dim, seed, 31, ntok * dim)
         t0 = time.perf_counter()
@@ -282,7 +322,11 @@ def cpu_moe_decode(lib, budget_s=12.0):
                 eo[:] = O.swiglu_expert(g, u, d, x, threads=CPU_THREADS)[0]
             c = O.bf16_to_f32(O.f32_to_bf16(O.bf16_to_f32(eo) * np.float32(wsorted[e])))
             y = O.bf16_to_f32(O.f32_to_bf16(y + c))
+            if ntok == 0:
+                floor += np.abs(c.astype(np.float64))
         t_tok += time.perf_counter() - t0
+        if ntok == 0:
+            ref_out = O.f32_to_bf16(y)         # the bench's rotation 0 (x, logits)
         ntok += 1
     nbytes = moe_algorithmic_bytes(E, k, dim, inter)[0]
     per_tok = t_tok / ntok
@@ -295,6 +339,8 @@ def cpu_moe_decode(lib, budget_s=12.0):
                    "reported separately, not in value" % (ntok, per_tok * 1e3,
                                                           t_deq * 1e3)),
         "ms_per_token": per_tok * 1e3, "dequant_fill_ms": t_deq * 1e3,
+        "_ref_out": {"out": ref_out, "floor": floor,
+                     "what": "token 0: the reference's expert calls + combine"},
     }
 
 
@@ -342,8 +388,12 @@ def bench_dense_gemv(lib, pkg, rt, steps, warmup, M=1, cfg=1):
     ms = timed(rt, st, step, warmup, steps)
     kt = kernel_times(lib, rt, step, warmup + steps, steps, 2,
                       {"k_fp8_gemv": (0, 1)})
+    step(0)                        # weight copy 0, the CPU leg's inputs (untimed)
+    st.synchronize()
+    y0 = d_y.download(np.uint16, (M, N))
     nbytes = N * K + nsb * 4 + M * K * 2 + M * N * 2
     return {"ms_per_step": ms, "value": nbytes / (ms * 1e-3) / 1e9,
+            "one_launch_per_step": True, "_gpu_out": y0,
             "weight_bytes": N * K, "traffic_key": "k_fp8_gemv@config%d_M%d" % (cfg, M),
             "bytes": nbytes, "flops": 2 * M * N * K, "kernel": "k_fp8_gemv",
             "kernel_ms": kt["k_fp8_gemv"], "kernel_bytes": nbytes,
@@ -397,11 +447,19 @@ def cpu_dense_gemv(lib, M=1, cfg=1, budget_s=10.0):
             "sample": "%d calls of apus_bf16_gemm_mt on pre-dequantized BF16 weights "
                       "(%.2f ms/call)" % (n2, t2 / n2 * 1e3)}
         extra["scalar_anchor"] = scalar_anchor(O, codes, sc, x)
+    # the reference output of the timed call and its tolerance floor
+    # (2^-8 * sum_k |w * x|, f64 over the bit-exact BF16 weights)
+    ref_y = y.copy()
+    if use_ref:
+        O.ref().ref_fp8blk_linear_mt(P(codes), P(sc), P(x), P(ref_y), M, N, K)
+    floor = 2.0 ** -8 * O.absdot(O.dequant(codes, sc, threads=CPU_THREADS), x)
     return {"value": nbytes / (t / n) / 1e9, "unit": "GB/s", **extra,
             **cpu_common(O, use_ref),
             "kind": "reference" if use_ref else "port",
             "sample": "%d calls of dequant_mt + gemm_mt (c/gdsa.h:532-533), "
-                      "M=%d, %.1f ms/call" % (n, M, t / n * 1e3)}
+                      "M=%d, %.1f ms/call" % (n, M, t / n * 1e3),
+            "_ref_out": {"out": ref_y, "floor": floor,
+                         "what": "weight copy 0: the reference's dequant_mt + gemm_mt"}}
 
 
 def scalar_anchor(O, codes, sc, x):
@@ -689,11 +747,12 @@ def bench_moe_decode_router(lib, pkg, rt, steps, warmup, rotate=64):
     rt.synchronize()
     t_router = sum(e[0].elapsed_ms(e[1]) for e in evs) / n
     t_dec = sum(e[2].elapsed_ms(e[3]) for e in evs) / n
+    errors = store_errors(lib, store)
     lib.apus_ghip_store_close(store)
     full, _, _ = moe_algorithmic_bytes(E, k, dim, inter)
     nbytes = full - E * 4 + E * dim * 2 + E * 4         # gate_w + bias, no logits
     return {
-        "ms_per_step": ms, "value": nbytes / (ms * 1e-3) / 1e9,
+        "ms_per_step": ms, "value": nbytes / (ms * 1e-3) / 1e9, "_device_errors": errors,
         "weight_bytes": k * 3 * inter * dim + E * dim * 2,
         "bytes": nbytes, "flops": 2 * k * 3 * inter * dim + 2 * E * dim,
         "kernel": "k_moe_decode", "kernel_ms": t_dec, "kernel_bytes": full - E * 4,
@@ -956,6 +1015,12 @@ def bench_prefill(lib, pkg, rt, steps, warmup, name):
     kt = {nm: sum(ev[a].elapsed_ms(ev[b]) for ev in evs) / n
           for nm, (a, b) in {"k_pf_permute": (0, 1), "k_pf_gemm_gateup": (2, 3),
                              "k_pf_gemm_down": (4, 5), "k_pf_combine": (6, 7)}.items()}
+    # checks outside the timed region: the device error words of every
+    # layer's store, and layer 0's first rows (the CPU leg's sample)
+    errors = 0
+    for s_ in stores:
+        errors |= store_errors(lib, s_)
+    out0 = outs[0].download(np.uint16, (T, dim))[:PREFILL_CPU_TOKENS].copy()
     for s_ in stores:
         lib.apus_ghip_store_close(s_)
     P = T * k
@@ -969,6 +1034,7 @@ def bench_prefill(lib, pkg, rt, steps, warmup, name):
     gu_bytes = sum(touched) // L * gu_member + P * dim * 2 + P * inter * 2
     return {
         "ms_per_step": ms, "value": flops / (ms * 1e-3) / 1e12, "unit": "TFLOP/s",
+        "_device_errors": errors, "_gpu_out": out0,
         "weight_bytes": sum(touched) * 3 * inter * dim,
         "bytes": nbytes, "flops": flops, "kernel": "k_pf_gemm_gateup",
         "kernel_ms": kt["k_pf_gemm_gateup"], "kernel_flops": gu_flops,
@@ -1004,6 +1070,19 @@ def _cpu_prefill_expert(O, P, use_ref, item, idx, x, dim, inter, eo, out, acc):
         acc["deq"] += time.perf_counter() - t0
         mats.append(pl)
     g, u, d = mats
+    if "floor" in acc:
+        # untimed: each routed token's expert-output floor sum_i |h_i * wd_i|
+        # (the oracle's h), which the check carries through the combine
+        toks = np.nonzero((idx == e).any(1))[0]
+        slab = np.concatenate([np.ascontiguousarray(a).view(np.uint8).ravel()
+                               for cs in members for a in cs])
+        bank = [None] * (e + 1)
+        bank[e] = slab
+        fe = O.moe_expert_floor(bank, dim, inter, x[toks], np.full((len(toks), 1), e,
+                                np.int32), np.ones((len(toks), 1), np.float32),
+                                limit=MOE["limit"], threads=CPU_THREADS)
+        for r, t in enumerate(toks):
+            acc["floor"][(int(t), e)] = fe[r]
     for t in np.nonzero((idx == e).any(1))[0]:
         t0 = time.perf_counter()
         if use_ref:
@@ -1015,7 +1094,10 @@ def _cpu_prefill_expert(O, P, use_ref, item, idx, x, dim, inter, eo, out, acc):
         eo[(int(t), e)] = out.copy()
 
 
-def cpu_moe_prefill(lib, name, ntok=128):
+PREFILL_CPU_TOKENS = 128
+
+
+def cpu_moe_prefill(lib, name, ntok=PREFILL_CPU_TOKENS):
     """The reference has no grouped GEMM: its prefill is the per-token loop
     (c/gmoe.h:278-320), each token's selected experts (apus_gmoe_expert on
     BF16 payloads, c/gmoe.h:210-227) then the ascending-expert bf16-per-add
@@ -1062,7 +1144,7 @@ def cpu_moe_prefill(lib, name, ntok=128):
     experts = sorted(set(idx.ravel().tolist()))
     batches = [experts[i:i + CPU_THREADS] for i in range(0, len(experts), CPU_THREADS)]
     # generation runs in parallel between the timed parts, never beside them
-    acc = {"deq": 0.0, "exp": 0.0}
+    acc = {"deq": 0.0, "exp": 0.0, "floor": {}}
     with ThreadPoolExecutor(CPU_THREADS) as ex:
         for b in batches:
             for e, members in zip(b, list(ex.map(gen, b))):
@@ -1070,6 +1152,7 @@ def cpu_moe_prefill(lib, name, ntok=128):
                                     out, acc)
     t_deq, t_exp = acc["deq"], acc["exp"]
     t0 = time.perf_counter()
+    ref_out = np.empty((ntok, dim), np.uint16)
     for t in range(ntok):
         y = np.zeros(dim, np.float32)
         seen = set()
@@ -1079,7 +1162,17 @@ def cpu_moe_prefill(lib, name, ntok=128):
             seen.add(e)
             c = O.bf16_to_f32(O.f32_to_bf16(O.bf16_to_f32(eo[(t, e)]) * np.float32(wt)))
             y = O.bf16_to_f32(O.f32_to_bf16(y + c))
+        ref_out[t] = O.f32_to_bf16(y)
     t_comb = time.perf_counter() - t0
+    # the combine's tolerance floor (untimed): sum_e |contrib_e|, or each
+    # expert output's own floor carried through the weights when larger
+    floor_c, floor_e = np.zeros((ntok, dim)), np.zeros((ntok, dim))
+    for (t, e), o in eo.items():
+        wt = w[t][list(idx[t]).index(e)]
+        floor_c[t] += np.abs(O.bf16_to_f32(O.f32_to_bf16(O.bf16_to_f32(o) * np.float32(wt)))
+                             .astype(np.float64))
+        floor_e[t] += abs(float(wt)) * acc["floor"][(t, e)]
+    floor = np.maximum(floor_c, floor_e)
     pairs = len(eo)
     tsec = t_exp + t_comb
     full_pairs = cfg["layers"] * T * k
@@ -1091,7 +1184,10 @@ def cpu_moe_prefill(lib, name, ntok=128):
                        "value; the full config (%d pairs) extrapolates linearly to %.0f s"
                        % (ntok, pairs, len(set(idx.ravel().tolist())), t_exp, t_comb, t_deq,
                           full_pairs, tsec * full_pairs / pairs)),
-            "dequant_fill_s": t_deq}
+            "dequant_fill_s": t_deq,
+            "_ref_out": {"out": ref_out, "floor": floor,
+                         "what": "layer 0, tokens 0..%d: the reference's per-token loop"
+                                 % (ntok - 1)}}
 
 
 # --------------------------------------------------------------------------
@@ -1189,6 +1285,14 @@ def mfma_busy_from_profiles(key):
 def roofline_of(r):
     key = r.get("traffic_key", r["kernel"])
     traffic = traffic_from_profiles(key)
+    src = "dispatch-packet events"
+    if r.get("one_launch_per_step") and r["kernel_ms"] > r["ms_per_step"]:
+        # one launch per step: the back-to-back step bounds the launch from
+        # above; the per-launch events of short launches read longer than the
+        # step (they include the packet's own event writes)
+        src = ("back-to-back step (the dispatch-packet events read %.6f ms, above "
+               "the step)" % r["kernel_ms"])
+        r = dict(r, kernel_ms=r["ms_per_step"])
     mfma = r.get("unit") == "TFLOP/s" and r.get("bound", "mfma") == "mfma"
     if mfma:
         achieved = r["kernel_flops"] / (r["kernel_ms"] * 1e-3) / 1e12
@@ -1209,6 +1313,7 @@ def roofline_of(r):
         "algorithmic_bytes_per_launch": r["kernel_bytes"],
         "algorithmic_flops_per_launch": r["kernel_flops"],
         "avg_launch_ms": round(r["kernel_ms"], 6),
+        "launch_time_source": src,
         "launch_ms": r["launch_ms"],
         "mfma_tflops": round(r["kernel_flops"] / (r["kernel_ms"] * 1e-3) / 1e12, 3),
         "mfma_frac": round(r["kernel_flops"] / (r["kernel_ms"] * 1e-3) / 1e12
@@ -1254,6 +1359,11 @@ def run_workload(name, lib, pkg, rt, args, cpu_leg):
     return ("device copy HBM GB/s (read + write)", r, None)
 
 
+def public(d):
+    """d without its private (underscore) entries: the arrays a check used."""
+    return None if d is None else {k: v for k, v in d.items() if not k.startswith("_")}
+
+
 def line_of(metric, r, cpu, steps, warmup):
     line = {
         "metric": metric,
@@ -1270,7 +1380,8 @@ def line_of(metric, r, cpu, steps, warmup):
         "data": r.get("data", "synthetic (include/apus_synth.h generator, seeded)"),
         "config": r["config"],
         "roofline": roofline_of(r),
-        "cpu_baseline": cpu,
+        "cpu_baseline": public(cpu),
+        "verified": verify(r, cpu),
     }
     if "hbm_gbs" in r:
         line["hbm"] = {"achieved": round(r["hbm_gbs"], 2), "peak": HBM_PEAK_GBS,
@@ -1387,6 +1498,11 @@ def main():
             print("bench: %s done (%.4f ms/step)" % (name, r2["ms_per_step"]),
                   file=sys.stderr, flush=True)
     print(json.dumps(line))
+    objs = [line] + line.get("dense", []) + line.get("prefill", [])
+    bad = [o["config"].get("workload") for o in objs if not o["verified"]["ok"]]
+    if bad:
+        print("bench: verification failed for %s" % bad, file=sys.stderr)
+        sys.exit(1)
 
 
 if __name__ == "__main__":
