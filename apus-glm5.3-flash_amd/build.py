@@ -125,6 +125,9 @@ def build(verbose=False):
          + ["-lm"])
     os.replace(tmp, LIB)
     _run(["make", "-s", "-C", os.path.join(ROOT, "oracle")])
+    # the compiled C callers of the boundary (test programs, linked against
+    # the library just built and the oracle)
+    _run(["make", "-s", "-B", "-C", os.path.join(ROOT, "tests", "c")])
     return LIB
 
 
