@@ -58,6 +58,7 @@ SIGNATURES = {
     "apus_ghip_store_synth": (c_int, [c_vp, c_u64, c_int, c_float, c_float]),
     "apus_ghip_store_slab_dev": (c_vp, [c_vp, c_int]),
     "apus_ghip_store_get": (c_int, [c_vp, c_int, c_vp, c_size]),
+    "apus_ghip_store_put_shared": (c_int, [c_vp, c_vp, c_size]),
     "apus_ghip_store_load_container": (c_int, [c_vp, ctypes.c_char_p, c_int,
                                                ctypes.POINTER(c_int), ctypes.c_char_p,
                                                c_size]),

@@ -32,6 +32,7 @@
 __attribute__((weak)) ApusGhipHooks apus_ghip_hooks;
 
 #define GHIP_MAX_TOPK 16
+#define GHIP_HW_SLOTS (GHIP_MAX_TOPK + 1)   /* routed slots + the shared expert */
 
 /* ------------------------------------------------------------------------ */
 /* state                                                                    */
@@ -528,8 +529,9 @@ struct ApusGhipStore {
     size_t h_gw, h_gs, h_uw, h_us, h_dw, h_ds, h_bytes;
     /* device layout: same order, members 256-byte aligned */
     size_t d_gw, d_gs, d_uw, d_us, d_dw, d_ds, d_stride;
-    uint8_t *arena;
-    uint32_t *nan_flags;                 /* device [n_experts] */
+    uint8_t *arena;                      /* n_experts + 1 slabs (the last: shared) */
+    uint32_t *nan_flags;                 /* device [n_experts + 1] */
+    int has_shared;                      /* the shared slab is set */
     GhipMoeDecodeWs ws;
     /* decode staging for the host-pointer entry */
     uint16_t *d_x, *d_out;
@@ -574,7 +576,9 @@ int apus_ghip_store_open(ApusGhipStore **out, int n_experts, size_t dim,
     s->d_dw = s->d_us + up256(nbg);
     s->d_ds = s->d_dw + up256(dim * inter);
     s->d_stride = s->d_ds + up256(nbd);
-    size_t total = s->d_stride * (size_t)n_experts;
+    /* one slab more than the routed experts: the shared expert's (set by
+     * apus_ghip_store_put_shared) */
+    size_t total = s->d_stride * ((size_t)n_experts + 1);
     hipError_t e = hipMalloc((void **)&s->arena, total);
     if (e != hipSuccess) {
         ghip_seterr("store_open: hipMalloc(%zu) %s", total, hipGetErrorString(e));
@@ -582,10 +586,10 @@ int apus_ghip_store_open(ApusGhipStore **out, int n_experts, size_t dim,
         free(s);
         return 1;
     }
-    int bad = hipMalloc((void **)&s->nan_flags, (size_t)n_experts * 4) != hipSuccess
-           || hipMemset(s->nan_flags, 0, (size_t)n_experts * 4) != hipSuccess
-           || hipMalloc((void **)&s->ws.hw, GHIP_MAX_TOPK * inter * 4) != hipSuccess
-           || hipMemset(s->ws.hw, 0, GHIP_MAX_TOPK * inter * 4) != hipSuccess
+    int bad = hipMalloc((void **)&s->nan_flags, ((size_t)n_experts + 1) * 4) != hipSuccess
+           || hipMemset(s->nan_flags, 0, ((size_t)n_experts + 1) * 4) != hipSuccess
+           || hipMalloc((void **)&s->ws.hw, GHIP_HW_SLOTS * inter * 4) != hipSuccess
+           || hipMemset(s->ws.hw, 0, GHIP_HW_SLOTS * inter * 4) != hipSuccess
            || (s->ws.hw_inter = (uint32_t)inter) == 0
            || hipMalloc((void **)&s->ws.err, 4) != hipSuccess
            || hipMemset(s->ws.err, 0, 4) != hipSuccess
@@ -638,6 +642,8 @@ static int store_scan(ApusGhipStore *s, int e, hipStream_t st) {
     return 0;
 }
 
+static int store_upload(ApusGhipStore *s, int expert, const void *slab);
+
 int apus_ghip_store_put(ApusGhipStore *s, int expert, const void *slab,
                         size_t nbytes) {
     if (!s || expert < 0 || expert >= s->n_experts || nbytes != s->h_bytes) {
@@ -645,6 +651,32 @@ int apus_ghip_store_put(ApusGhipStore *s, int expert, const void *slab,
                     expert, nbytes, s ? s->h_bytes : 0);
         return 1;
     }
+    return store_upload(s, expert, slab);
+}
+
+int apus_ghip_store_put_shared(ApusGhipStore *s, const void *slab, size_t nbytes) {
+    if (!s) {
+        ghip_seterr("store_put_shared: no store");
+        return 1;
+    }
+    if (!slab) {                         /* remove: routed experts only */
+        HIPCHK(hipStreamSynchronize(G.stream));
+        s->has_shared = 0;
+        return 0;
+    }
+    if (nbytes != s->h_bytes) {
+        ghip_seterr("store_put_shared: slab size %zu (want %zu: the shared expert's "
+                    "intermediate must be the store's)", nbytes, s->h_bytes);
+        return 1;
+    }
+    if (store_upload(s, s->n_experts, slab)) return 1;
+    s->has_shared = 1;
+    return 0;
+}
+
+/* One H2D copy of a host slab into arena slot `expert` (n_experts = the
+ * shared expert's) and its NaN-code scan. */
+static int store_upload(ApusGhipStore *s, int expert, const void *slab) {
     uint8_t *b = s->arena + (size_t)expert * s->d_stride;
     const uint8_t *h = (const uint8_t *)slab;
     int same = s->d_gs == s->h_gs && s->d_uw == s->h_uw && s->d_us == s->h_us
@@ -946,6 +978,7 @@ static void store_bank(const ApusGhipStore *s, GhipBank *bk) {
     bk->inter = (uint32_t)s->inter;
     bk->nan_flags = s->nan_flags;
     bk->err = s->ws.err;
+    bk->has_shared = (uint32_t)s->has_shared;
 }
 
 int apus_ghip_store_status(ApusGhipStore *s, void *stream, int clear,
@@ -1118,9 +1151,10 @@ int apus_ghip_moe_prefill_reserve(const ApusGhipStore *s, size_t tokens,
         G.pf.n_cu = G.n_cu;
         G.pf_inited = 1;
     }
-    const size_t P = tokens * (size_t)topk;
+    /* a shared expert adds one pair per token (and one expert) */
+    const size_t P = tokens * ((size_t)topk + (s->has_shared ? 1 : 0));
     if (P == 0) return 0;
-    const uint32_t E = (uint32_t)s->n_experts;
+    const uint32_t E = (uint32_t)s->n_experts + (s->has_shared ? 1u : 0u);
     _Static_assert(PF_HDR_Q + 16 <= PF_HDR_WORDS, "prefill header holds the queues");
     const size_t need[8] = {
         PF_HDR_WORDS * sizeof(uint32_t),
@@ -1154,7 +1188,7 @@ int apus_ghip_moe_prefill_dev(ApusGhipStore *s, const uint16_t *x, size_t T,
         return 1;
     }
     if (T == 0) return 0;
-    if (s->dim % 256 || s->inter % 128 || s->n_experts > 1024) {
+    if (s->dim % 256 || s->inter % 128 || s->n_experts + s->has_shared > 1024) {
         ghip_seterr("moe_prefill: needs dim %% 256 == 0, inter %% 128 == 0 and "
                     "<= 1024 experts (dim=%zu inter=%zu E=%d)", s->dim, s->inter,
                     s->n_experts);
@@ -1189,14 +1223,15 @@ int apus_ghip_moe_prefill_dev_noalloc(ApusGhipStore *s, const uint16_t *x, size_
         return 1;
     }
     if (T == 0) return 0;
-    if (s->dim % 256 || s->inter % 128 || s->n_experts > 1024) {
+    if (s->dim % 256 || s->inter % 128 || s->n_experts + s->has_shared > 1024) {
         ghip_seterr("moe_prefill_noalloc: needs dim %% 256 == 0, inter %% 128 == 0 and "
                     "<= 1024 experts (dim=%zu inter=%zu E=%d)", s->dim, s->inter,
                     s->n_experts);
         return 1;
     }
-    const size_t P = T * (size_t)topk;
-    const size_t need = ghip_pf_scratch_need(P, (uint32_t)s->n_experts, (uint32_t)s->dim,
+    const size_t P = T * ((size_t)topk + (s->has_shared ? 1 : 0));
+    const uint32_t Ep = (uint32_t)s->n_experts + (s->has_shared ? 1u : 0u);
+    const size_t need = ghip_pf_scratch_need(P, Ep, (uint32_t)s->dim,
                                              (uint32_t)s->inter);
     if (need > GHIP_PF_SCRATCH_BYTES) {
         ghip_seterr("moe_prefill_noalloc: %zu tokens x top-%d need %zu bytes of workspace, "
@@ -1205,7 +1240,7 @@ int apus_ghip_moe_prefill_dev_noalloc(ApusGhipStore *s, const uint16_t *x, size_
         return 1;
     }
     GhipMoePrefillWs ws;
-    hipError_t e = ghip_pf_scratch_ws(G.device, P, (uint32_t)s->n_experts, (uint32_t)s->dim,
+    hipError_t e = ghip_pf_scratch_ws(G.device, P, Ep, (uint32_t)s->dim,
                                       (uint32_t)s->inter, G.n_cu, &ws);
     if (e != hipSuccess) {
         ghip_seterr("moe_prefill_noalloc: scratch: %s", hipGetErrorString(e));

@@ -46,7 +46,7 @@ hipError_t ghip_launch_bf16_linear(const uint16_t *w, const uint16_t *x,
  * 0..15, the writing launch's tag in 16..31; zero-filled at creation), an
  * error word, and the host's current tag. */
 typedef struct {
-    uint32_t *hw;         /* device [16 slots, hw_inter] u32 */
+    uint32_t *hw;         /* device [17 slots, hw_inter] u32: 16 routed + the shared expert */
     uint32_t hw_inter;    /* inter the words were sized for */
     uint32_t *err;        /* device u32: 2 = invalid expert id, 4 = hand-off wait ran out */
     uint32_t n_cu;        /* grid: one workgroup per CU */
@@ -70,6 +70,8 @@ typedef struct {
     uint32_t *err;               /* device u32, the store's sticky error word (2 = an
                                     invalid expert id was dropped, 4 = a decode hand-off
                                     wait ran out) or NULL */
+    uint32_t has_shared;         /* 1: a shared expert's slab at index n_experts (same
+                                    layout and inter), added last to every token */
 } GhipBank;
 
 /* K3: routed MoE decode for one token (routing, gate/up + SwiGLU, down +

@@ -182,7 +182,14 @@ struct MdShared {
     uint32_t nsel;
     float red[GU_IPW][2][2][16];
     float oq[MD_MAXK][16];
+    float sred[MD_NW][16];       /* shared expert: gate/up partials per wave */
+    float sdown[MD_NW][16];      /* shared expert: down partials per wave */
 };
+
+#define MD_SH_SLOT MD_MAXK       /* the shared expert's h words: slot 16 */
+#define SH_GRP 5                 /* shared gate/up chunks in flight per wave (x: <= 128
+                                    vectors, two per lane) */
+#define SD_GRP 4                 /* shared down chunks in flight per wave */
 
 /* Phase A, wave 0 only: the routing picks into sh.sel / sh.nsel. Given
  * idx/w: a repeated id keeps its first slot (c/gmoe.h:309-312), invalid ids
@@ -352,6 +359,135 @@ __device__ __forceinline__ void md_phase_gateup(const GhipBank &bank, const uint
     }
 }
 
+/* The shared expert's gate/up rows 8hb .. 8hb + 7 (c/gmoe.h:325-336: every
+ * token runs it, so it needs no routing and waves 1..7 stream it while
+ * wave 0 routes). One 16-row chunk holds the gate rows (chunk rows 0..7)
+ * and the up rows (chunk rows 8..15) of one 128-wide k block, each half
+ * dequantized with its own matrix's block scale, so one MFMA chunk gives
+ * both. Wave w = 1..7 takes k blocks [(w-1) nch / 7, w nch / 7), all of
+ * them requested before the first is used (SH_GRP at a time), with its x
+ * slices staged in its own LDS area, and leaves its fp32 partial sums in
+ * sh.sred[w] (summed in a fixed order after the routing barrier).
+ * wbuf: the wave's 8 KB area (two 2 KB chunk slots, then the x slices). */
+template <bool EXACT>
+__device__ __forceinline__ void md_shared_gu_blocks(const uint8_t *gw, const uint8_t *uw,
+                                                    const float *sg, const float *su,
+                                                    const uint16_t *__restrict__ x,
+                                                    const ghip_cdma &d, uint32_t c0,
+                                                    uint32_t c1, uint8_t *wbuf,
+                                                    ghip_f32x4 &acc) {
+    const uint32_t lane = threadIdx.x & 63u, n = lane & 15u, g = lane >> 4;
+    uint16_t *xw = (uint16_t *)(wbuf + 4096u);
+    for (uint32_t cb = c0; cb < c1; cb += SH_GRP) {
+        const uint32_t cn = min(c1 - cb, (uint32_t)SH_GRP);
+        /* the x slice first (its wait then covers it alone), then the
+         * chunks: cn * 16 <= 80 vectors of 16 bytes, two per lane (index
+         * clamped, a duplicate rewrites the last vector with its own value) */
+        const uint32_t xv_i = min(lane, cn * 16u - 1u), xv_j = min(lane + 64u, cn * 16u - 1u);
+        const ghip_u32x4 xv = *(const ghip_u32x4 *)(x + (size_t)cb * 128u + 8u * xv_i);
+        const ghip_u32x4 xw2 = *(const ghip_u32x4 *)(x + (size_t)cb * 128u + 8u * xv_j);
+        ghip_u32x4 a0[SH_GRP], a1[SH_GRP];
+#pragma unroll
+        for (uint32_t j = 0; j < SH_GRP; j++) {
+            const uint32_t cj = cb + min(j, cn - 1u);
+            const uint8_t *pg = gw + (size_t)cj * 128u, *pu = uw + (size_t)cj * 128u;
+            a0[j] = __builtin_nontemporal_load((const ghip_u32x4 *)(pg + d.off0));
+            a1[j] = __builtin_nontemporal_load((const ghip_u32x4 *)(pu + d.off1));
+        }
+        ((ghip_u32x4 *)xw)[xv_i] = xv;
+        ((ghip_u32x4 *)xw)[xv_j] = xw2;
+#pragma unroll
+        for (uint32_t j = 0; j < SH_GRP; j++) {
+            if (j < cn) {
+                uint8_t *buf = wbuf + (j & 1u) * 2048u;
+                ghip_rl_store(buf, lane, a0[j], a1[j]);
+                const ghip_chunk ck = ghip_cdma_read(buf, n, g);
+                ghip_bf16x8 xa[4];
+                ghip_read_a4(xw + j * 128u + 32u * g, xa);
+                const float scg = ghip_sload(sg, cb + j), scu = ghip_sload(su, cb + j);
+                ghip_chunk_mfma_a<EXACT>(ck, n < 8u ? scg : scu, xa, acc);
+            }
+        }
+    }
+}
+
+__device__ __forceinline__ void md_shared_gateup(const GhipBank &bank,
+                                                 const uint16_t *__restrict__ x,
+                                                 uint8_t *wbuf, uint32_t hb, MdShared &sh) {
+    const uint32_t dim = bank.dim, lane = threadIdx.x & 63u;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t nch = dim >> 7, nkb = dim >> 7;
+    const uint32_t c0 = (wv - 1u) * nch / (MD_NW - 1u), c1 = wv * nch / (MD_NW - 1u);
+    const uint32_t E = bank.n_experts, r0 = hb * 8u;
+    const uint8_t *slab = bank.base + (size_t)E * bank.stride;
+    /* gate rows r0.. at chunk rows 0..7; up rows r0.. at chunk rows 8..15,
+     * whose offsets (ghip_cdma_offsets) count from chunk row 0: the up base
+     * is taken 8 rows back */
+    const uint8_t *gw = slab + bank.off_gw + (size_t)r0 * dim;
+    const uint8_t *uw = slab + bank.off_uw + (size_t)r0 * dim - (size_t)8u * dim;
+    const float *sg = (const float *)(slab + bank.off_gs) + (size_t)(r0 >> 7) * nkb;
+    const float *su = (const float *)(slab + bank.off_us) + (size_t)(r0 >> 7) * nkb;
+    const ghip_cdma d = ghip_cdma_offsets(lane, dim);
+    ghip_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    if (ghip_sload_u32(bank.nan_flags, E) != 0u)
+        md_shared_gu_blocks<true>(gw, uw, sg, su, x, d, c0, c1, wbuf, acc);
+    else
+        md_shared_gu_blocks<false>(gw, uw, sg, su, x, d, c0, c1, wbuf, acc);
+    if ((lane >> 4) == 0) sh.sred[wv][lane] = acc[0];
+}
+
+/* After the routing barrier: the shared expert's 8 h values of rows 8hb..
+ * (lane j < 8 of the calling wave): the partial sums of waves 1..7 in that
+ * order, the reference's bf16 roundings and SwiGLU, stored as tagged words
+ * (as the routed slots' h) in slot MD_SH_SLOT. */
+__device__ __forceinline__ void md_shared_h(const MdShared &sh, uint32_t hb, uint32_t inter,
+                                            float limit, uint32_t *hw, uint32_t tag) {
+    const uint32_t lane = threadIdx.x & 63u;
+    if (lane < 8u) {
+        float gs = sh.sred[1][lane], us = sh.sred[1][8u + lane];
+#pragma unroll
+        for (uint32_t w = 2; w < MD_NW; w++) {
+            gs = gs + sh.sred[w][lane];
+            us = us + sh.sred[w][8u + lane];
+        }
+        const uint32_t hv = ghip_swiglu(ghip_bf16_round(gs), ghip_bf16_round(us), limit);
+        __hip_atomic_store(hw + (size_t)MD_SH_SLOT * inter + hb * 8u + lane, (tag << 16) | hv,
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+/* The shared expert's down rows r0 .. r0 + 15 over the calling wave's
+ * share of inter, k blocks [wv nchd / 8, (wv + 1) nchd / 8), with that
+ * share of its h already staged at hss; the fp32 partials go to
+ * sh.sdown[wv] (summed in wave order by the combine). Uses the wave's first
+ * two down LDS slots before its routed rows do. */
+template <bool EXACT>
+__device__ __forceinline__ void md_shared_down_blocks(const uint8_t *rows, const float *srow,
+                                                      const uint16_t *hss,
+                                                      const ghip_cdma &d, uint32_t c0,
+                                                      uint32_t c1, uint8_t *ring,
+                                                      ghip_f32x4 &acc) {
+    const uint32_t lane = threadIdx.x & 63u, n = lane & 15u, g = lane >> 4;
+    for (uint32_t cb = c0; cb < c1; cb += SD_GRP) {
+        const uint32_t cn = min(c1 - cb, (uint32_t)SD_GRP);
+        ghip_u32x4 a0[SD_GRP], a1[SD_GRP];
+#pragma unroll
+        for (uint32_t j = 0; j < SD_GRP; j++)
+            ghip_rl_load(rows, d, cb + min(j, cn - 1u), a0[j], a1[j]);
+#pragma unroll
+        for (uint32_t j = 0; j < SD_GRP; j++) {
+            if (j < cn) {
+                uint8_t *buf = ring + (j & 1u) * DN_STG;
+                ghip_rl_store(buf, lane, a0[j], a1[j]);
+                const ghip_chunk ck = ghip_cdma_read(buf, n, g);
+                ghip_bf16x8 ha[4];
+                ghip_read_a4(hss + (cb - c0 + j) * 128u + 32u * g, ha);
+                ghip_chunk_mfma_a<EXACT>(ck, ghip_sload(srow, cb + j), ha, acc);
+            }
+        }
+    }
+}
+
 /* Phase C, down + ordered combine for the 16 output rows at r0: wave q
  * streams slot base + q's 16 rows of Wd over inter through registers and
  * its DN_R LDS slots with h of that slot (in LDS at hs + q * inter) as the
@@ -464,6 +600,7 @@ __device__ __forceinline__ void md_phase_down(const GhipBank &bank, MdShared &sh
 /* the ascending-expert combine of the nsel expert outputs in sh.oq: y =
  * bf16(y + bf16(bf16(o) * w)), from +0 (c/gmoe.h:307-320). Call after a
  * barrier. */
+template <bool SHARED>
 __device__ __forceinline__ void md_combine(const MdShared &sh, uint32_t r0,
                                            uint16_t *__restrict__ out) {
     const uint32_t tid = threadIdx.x;
@@ -476,23 +613,32 @@ __device__ __forceinline__ void md_combine(const MdShared &sh, uint32_t r0,
             float c = ghip_bf16_round(eo * sh.wt[q]);
             y = ghip_bf16_round(y + c);
         }
+        if constexpr (SHARED) {
+            /* the shared expert's output (its waves' partials in wave
+             * order, one bf16 rounding), added last with one more rounding
+             * and no weight (c/gmoe.h:325-336) */
+            float so = sh.sdown[0][tid];
+#pragma unroll
+            for (uint32_t w = 1; w < MD_NW; w++) so = so + sh.sdown[w][tid];
+            y = y + ghip_bf16_round(so);
+        }
         out[r0 + tid] = (uint16_t)ghip_bf16_bits(y);
     }
 }
 
-/* h of slot q into LDS (hs [inter] bf16) by the calling wave alone, from
- * the tagged words hw (value in bits 0..15, the writing launch's tag in
- * 16..31): the lanes load their words with device-coherent loads and
+/* inter h values into LDS (hs [inter] bf16) by the calling wave alone, from
+ * the tagged words at src (one slot's words, or a range of them; value in
+ * bits 0..15, the writing launch's tag in 16..31): the lanes load their
+ * words with device-coherent loads and
  * re-poll the ones that do not carry this launch's tag yet (their gate/up
  * item is still running on another CU), at most MD_SPIN_MAX rounds.
  * Returns false (the same in every lane) when a word is still missing
  * then. No workgroup barrier: each wave goes on to its own slot's rows as
  * soon as that slot's h is in. */
-__device__ __forceinline__ bool md_stage_h_wave(const uint32_t *hw, uint32_t q, uint32_t inter,
+__device__ __forceinline__ bool md_stage_h_wave(const uint32_t *src, uint32_t inter,
                                                 uint32_t tag, uint16_t *hs) {
     constexpr uint32_t PER = 16;
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t *src = hw + (size_t)q * inter;
     for (uint32_t i0 = 0; i0 < inter; i0 += 64u * PER) {
         uint32_t v[PER];
 #pragma unroll
@@ -542,6 +688,7 @@ __device__ __forceinline__ bool md_stage_h_wave(const uint32_t *hw, uint32_t q, 
  * polls) flags err |= 4 and that wave skips its down rows (in every later
  * row group too) instead of hanging, so the launch always ends, and its
  * output is invalid whenever the word holds 4 afterwards. */
+template <bool SHARED>
 __global__ __launch_bounds__(MD_NW * 64, 1) void k_moe_decode(
     GhipBank bank, const uint16_t *__restrict__ x, const float *__restrict__ logits,
     const int32_t *__restrict__ idx, const float *__restrict__ w, int topk, float limit,
@@ -552,6 +699,7 @@ __global__ __launch_bounds__(MD_NW * 64, 1) void k_moe_decode(
     const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t dim = bank.dim, inter = bank.inter;
     uint16_t *xs = (uint16_t *)dl;
+    uint8_t *gu_ring = dl + ((dim * 2u + 1023u) & ~1023u);
 
     /* --- phase A: route (wave 0) while x goes to LDS ------------------- */
     {
@@ -562,6 +710,10 @@ __global__ __launch_bounds__(MD_NW * 64, 1) void k_moe_decode(
         if (wv == 0)
             md_route_ids(logits, idx, w, topk, (int)bank.n_experts, sh,
                          blockIdx.x == 0 ? err : nullptr);
+        else if (SHARED && blockIdx.x * 8u < inter)
+            /* the other waves stream the shared expert's gate/up rows of
+             * this workgroup meanwhile (no routing needed) */
+            md_shared_gateup(bank, x, gu_ring + wv * (GU_R * GU_STG), blockIdx.x, sh);
         asm volatile("" ::"v"(x0));
         if (tid < n16) ((ghip_u32x4 *)xs)[tid] = x0;
         for (uint32_t i = tid + MD_NW * 64; i < n16; i += MD_NW * 64)
@@ -570,10 +722,12 @@ __global__ __launch_bounds__(MD_NW * 64, 1) void k_moe_decode(
          * flight into the streaming loops */
         GHIP_VMCNT(0);
         __syncthreads();
+        if (SHARED && wv == 1 && blockIdx.x * 8u < inter)
+            md_shared_h(sh, blockIdx.x, inter, limit, hw, tag);
     }
 
     /* --- phase B: gate/up + SwiGLU -> tagged h words ------------------- */
-    md_phase_gateup(bank, xs, dl + ((dim * 2u + 1023u) & ~1023u), sh, limit, hw, tag);
+    md_phase_gateup(bank, xs, gu_ring, sh, limit, hw, tag);
 
     /* --- phase C: down + combine per 16 output rows -------------------- */
     const uint32_t nsel = __builtin_amdgcn_readfirstlane(sh.nsel);
@@ -584,8 +738,37 @@ __global__ __launch_bounds__(MD_NW * 64, 1) void k_moe_decode(
      * out: the wave then computes no down rows at all, in this row group
      * or in a later one that reuses the staged h) */
     bool hs_ok = true;
+    /* shared expert: wave w's share of inter, k blocks [sc0, sc1), and its
+     * h values staged once at hss (after the down rings) */
+    const uint32_t nchd = inter >> 7;
+    const uint32_t sc0 = wv * nchd / MD_NW, sc1 = (wv + 1u) * nchd / MD_NW;
+    uint16_t *hss = (uint16_t *)(ring + (size_t)MD_NW * DN_R * DN_STG) + wv * (nchd / MD_NW + 1u) * 128u;
+    bool hss_ok = true;
     for (uint32_t rg = blockIdx.x; rg * MD_T < dim; rg += gridDim.x) {
         const uint32_t r0 = rg * MD_T;
+        if constexpr (SHARED) {
+            /* the shared expert's down rows over this wave's share of
+             * inter, while the routed slots' h is still on its way */
+            if (rg == blockIdx.x && sc1 > sc0)
+                hss_ok = md_stage_h_wave(hw + (size_t)MD_SH_SLOT * inter + sc0 * 128u,
+                                         (sc1 - sc0) * 128u, tag, hss);
+            ghip_f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
+            if (hss_ok && sc1 > sc0) {
+                const uint32_t nkb = inter >> 7;
+                const uint8_t *slab = bank.base + (size_t)bank.n_experts * bank.stride;
+                const uint8_t *rows = slab + bank.off_dw + (size_t)r0 * inter;
+                const float *srow = (const float *)(slab + bank.off_ds) + (size_t)(r0 >> 7) * nkb;
+                const ghip_cdma d = ghip_cdma_offsets(tid & 63u, inter);
+                uint8_t *wring = ring + wv * (DN_R * DN_STG);
+                if (ghip_sload_u32(bank.nan_flags, bank.n_experts) != 0u)
+                    md_shared_down_blocks<true>(rows, srow, hss, d, sc0, sc1, wring, sacc);
+                else
+                    md_shared_down_blocks<false>(rows, srow, hss, d, sc0, sc1, wring, sacc);
+            } else if (!hss_ok && (tid & 63u) == 0) {
+                atomicOr(err, 4u);
+            }
+            if ((tid & 63u) < 16u) sh.sdown[wv][tid & 63u] = sacc[0];
+        }
         for (uint32_t base = 0; base < nsel; base += MD_NW) {
             /* the down rows' first chunks stream while h is awaited */
             MdDownHead hd = md_down_prologue(bank, sh, r0, base);
@@ -593,7 +776,8 @@ __global__ __launch_bounds__(MD_NW * 64, 1) void k_moe_decode(
              * pass), then at once its down rows; a wave whose wait runs
              * out flags the error and computes nothing */
             if (base + wv < nsel && (base > 0 || rg == blockIdx.x || nsel > MD_NW))
-                hs_ok = md_stage_h_wave(hw, base + wv, inter, tag, hs + (size_t)wv * inter);
+                hs_ok = md_stage_h_wave(hw + (size_t)(base + wv) * inter, inter, tag,
+                                        hs + (size_t)wv * inter);
             const bool ok = hs_ok;
             if (ok) {
                 md_phase_down(bank, sh, r0, base, hs, ring, hd);
@@ -603,7 +787,8 @@ __global__ __launch_bounds__(MD_NW * 64, 1) void k_moe_decode(
             }
             __syncthreads();
         }
-        md_combine(sh, r0, out);
+        if (SHARED && nsel == 0) __syncthreads();  /* the shared partials are in */
+        md_combine<SHARED>(sh, r0, out);
         __syncthreads();                          /* sh.oq is reused by the next rows */
     }
 }
@@ -817,11 +1002,17 @@ extern "C" hipError_t ghip_launch_moe_decode(const GhipBank *bank,
         || (bank->off_gw & 15) || (bank->off_uw & 15) || (bank->off_dw & 15)
         || (bank->off_gs & 3) || (bank->off_us & 3) || (bank->off_ds & 3))
         return hipErrorInvalidValue;
+    const bool shared = bank->has_shared != 0;
     const size_t lds_gu = (((size_t)dim * 2 + 1023) & ~(size_t)1023) + GU_NW * GU_R * GU_STG;
-    const size_t lds_dn = (size_t)MD_NW * inter * 2 + MD_NW * DN_R * DN_STG;
+    /* down: the slots' h, the chunk rings and, with a shared expert, each
+     * wave's share of its h */
+    const size_t lds_dn = (size_t)MD_NW * inter * 2 + MD_NW * DN_R * DN_STG
+                        + (shared ? (size_t)MD_NW * (inter / 128 / MD_NW + 1) * 256 : 0);
     const size_t lds = lds_gu > lds_dn ? lds_gu : lds_dn;
     if (lds > MD_LDS_MAX || ws->n_cu == 0 || !ws->hw || !ws->err || inter > ws->hw_inter)
         return hipErrorInvalidValue;
+    /* the shared expert's gate/up rows go 8 to a workgroup, in one pass */
+    if (shared && (size_t)inter > (size_t)ws->n_cu * 8) return hipErrorInvalidValue;
     /* the tag is host state advanced per call, so a launch recorded into a
      * graph would replay with a stale tag: refuse to be captured */
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
@@ -833,17 +1024,26 @@ extern "C" hipError_t ghip_launch_moe_decode(const GhipBank *bank,
      * 65535 launches ago cannot pass for this launch's */
     hipError_t e;
     if (++ws->tag > 0xffffu) {
-        if ((e = ghip_launch_fill_u32(ws->hw, (size_t)MD_MAXK * inter, 0u, st)) != hipSuccess)
+        if ((e = ghip_launch_fill_u32(ws->hw, (size_t)(MD_MAXK + 1) * inter, 0u, st))
+            != hipSuccess)
             return e;
         ws->tag = 1;
     }
-    GHIP_LAUNCH(ev ? ev[0] : nullptr, ev ? ev[1] : nullptr, k_moe_decode, dim3(ws->n_cu),
-                dim3(MD_NW * 64), lds, st, *bank, x, logits, idx, w, topk, limit, ws->hw,
-                ws->tag, ws->err, out);
+    if (shared)
+        GHIP_LAUNCH(ev ? ev[0] : nullptr, ev ? ev[1] : nullptr, k_moe_decode<true>,
+                    dim3(ws->n_cu), dim3(MD_NW * 64), lds, st, *bank, x, logits, idx, w,
+                    topk, limit, ws->hw, ws->tag, ws->err, out);
+    else
+        GHIP_LAUNCH(ev ? ev[0] : nullptr, ev ? ev[1] : nullptr, k_moe_decode<false>,
+                    dim3(ws->n_cu), dim3(MD_NW * 64), lds, st, *bank, x, logits, idx, w,
+                    topk, limit, ws->hw, ws->tag, ws->err, out);
     return hipGetLastError();
 }
 
 extern "C" hipError_t ghip_moe_decode_init(void) {
-    return hipFuncSetAttribute((const void *)k_moe_decode,
+    hipError_t e = hipFuncSetAttribute((const void *)k_moe_decode<false>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, MD_LDS_MAX);
+    if (e != hipSuccess) return e;
+    return hipFuncSetAttribute((const void *)k_moe_decode<true>,
                                hipFuncAttributeMaxDynamicSharedMemorySize, MD_LDS_MAX);
 }

@@ -68,26 +68,32 @@ typedef float ghip_f32x16 __attribute__((ext_vector_type(16)));
 /* permutation                                                              */
 /* ------------------------------------------------------------------------ */
 
-/* One workgroup per PF_CHUNK pairs (pair p = t * topk + j). eid[p] = the
- * expert of p, or -1 when the id is out of range (flags hdr[PF_HDR_ERR] and,
+/* One workgroup per PF_CHUNK pairs. A token has topk_p = topk + shared
+ * pair slots: pair p = t * topk_p + j is (token t, idx[t * topk + j]) for
+ * j < topk, and (token t, the shared expert, id E) for j == topk when the
+ * bank has one (c/gmoe.h:325-336: every token runs it). eid[p] = the expert
+ * of p, or -1 when a routed id is out of range (flags hdr[PF_HDR_ERR] and,
  * when given, bit 2 of the store's sticky error word serr) or repeats an
- * earlier slot of the same token. cnt[chunk][e] = count. */
+ * earlier slot of the same token. cnt[chunk][e] = count (E + shared
+ * experts). */
 __global__ __launch_bounds__(1024) void k_pf_count(
-    const int32_t *__restrict__ idx, uint32_t P, uint32_t topk, uint32_t E,
-    uint32_t *__restrict__ cnt, int32_t *__restrict__ eid,
+    const int32_t *__restrict__ idx, uint32_t P, uint32_t topk, uint32_t topk_p,
+    uint32_t E, uint32_t *__restrict__ cnt, int32_t *__restrict__ eid,
     uint32_t *__restrict__ hdr, uint32_t *__restrict__ serr) {
     extern __shared__ uint32_t hist[];
-    for (uint32_t i = threadIdx.x; i < E; i += 1024) hist[i] = 0;
+    const uint32_t Ep = E + (topk_p - topk);
+    for (uint32_t i = threadIdx.x; i < Ep; i += 1024) hist[i] = 0;
     __syncthreads();
     const uint32_t p = blockIdx.x * PF_CHUNK + threadIdx.x;
     if (p < P) {
-        const int32_t e = idx[p];
-        const uint32_t t = p / topk, j = p - t * topk;
-        bool ok = e >= 0 && (uint32_t)e < E;
-        if (!ok) {
+        const uint32_t t = p / topk_p, j = p - t * topk_p;
+        const int32_t e = j < topk ? idx[(size_t)t * topk + j] : (int32_t)E;
+        bool ok = e >= 0 && (uint32_t)e < Ep;
+        if (!ok || (j < topk && (uint32_t)e == E)) {
+            ok = false;
             atomicOr(&hdr[PF_HDR_ERR], 1u);
             if (serr) atomicOr(serr, 2u);
-        } else {
+        } else if (j < topk) {
             for (uint32_t jj = 0; jj < j; jj++)
                 if (idx[(size_t)t * topk + jj] == e) { ok = false; break; }
         }
@@ -95,8 +101,8 @@ __global__ __launch_bounds__(1024) void k_pf_count(
         if (ok) atomicAdd(&hist[e], 1u);
     }
     __syncthreads();
-    for (uint32_t i = threadIdx.x; i < E; i += 1024)
-        cnt[(size_t)blockIdx.x * E + i] = hist[i];
+    for (uint32_t i = threadIdx.x; i < Ep; i += 1024)
+        cnt[(size_t)blockIdx.x * Ep + i] = hist[i];
 }
 
 /* Inclusive scan of one value per thread over a 1024-thread workgroup. */
@@ -992,22 +998,27 @@ __global__ __launch_bounds__(256) void k_splitk_sum(const float *__restrict__ pa
 __global__ __launch_bounds__(256) void k_pf_combine(
     const uint16_t *__restrict__ O, const int32_t *__restrict__ pos,
     const int32_t *__restrict__ idx, const float *__restrict__ w, uint32_t T,
-    uint32_t topk, uint32_t dim, uint16_t *__restrict__ out) {
+    uint32_t topk, uint32_t topk_p, uint32_t dim, uint16_t *__restrict__ out) {
     __shared__ int32_t srow[PF_MAXK];
     __shared__ float sw[PF_MAXK];
     __shared__ uint32_t sn;
+    __shared__ int32_t sshared;
     const uint32_t cpt = (dim + 2047) / 2048;          /* workgroups per token */
     const uint32_t t = blockIdx.x / cpt, c = blockIdx.x - t * cpt;
     const uint32_t tid = threadIdx.x;
     if (tid < 64) {
-        /* lane j holds pair j; a kept pair's rank among the kept pairs by
-         * expert id is its slot in the ordered list (ids of kept pairs are
-         * distinct: repeats were dropped by the permutation) */
+        /* lane j holds routed pair j; a kept pair's rank among the kept
+         * pairs by expert id is its slot in the ordered list (ids of kept
+         * pairs are distinct: repeats were dropped by the permutation). The
+         * shared expert's pair (slot topk, when topk_p > topk) is added
+         * after them. */
         const uint32_t j = tid;
         const size_t p = (size_t)t * topk + j;
-        const int32_t s = j < topk ? pos[p] : -1;
+        const int32_t s = j < topk ? pos[(size_t)t * topk_p + j] : -1;
         const int32_t e = s >= 0 ? idx[p] : 0x7fffffff;
         const float wj = j < topk ? w[p] : 0.0f;
+        if (tid == 0)
+            sshared = topk_p > topk ? pos[(size_t)t * topk_p + topk] : -1;
         uint32_t rank = 0;
         for (uint32_t q = 0; q < topk; q++) {
             const int32_t eq = __shfl(e, (int)q, 64);
@@ -1044,6 +1055,14 @@ __global__ __launch_bounds__(256) void k_pf_combine(
             }
         }
     }
+    const int32_t ss = sshared;
+    if (ss >= 0) {
+        /* the shared expert, last, one more rounding: out = bf16(y + sh) */
+        const ghip_u32x4 v = *(const ghip_u32x4 *)(O + (size_t)ss * dim + d);
+#pragma unroll
+        for (int q = 0; q < 8; q++)
+            y[q] = y[q] + ghip_bf16_f32((v[q >> 1] >> (16 * (q & 1))) & 0xffffu);
+    }
     ghip_u32x4 r;
 #pragma unroll
     for (int q = 0; q < 4; q++)
@@ -1071,11 +1090,15 @@ extern "C" hipError_t ghip_launch_moe_prefill(const GhipBank *bank,
     if (!bank || !ws || !x || !idx || !w || !out) return hipErrorInvalidValue;
     if (T == 0) return hipSuccess;
     const uint32_t dim = bank->dim, inter = bank->inter, E = bank->n_experts;
-    if (topk <= 0 || topk > PF_MAXK || E == 0 || E > PF_MAXE)
+    /* with a shared expert every token has one more pair (the shared
+     * expert, id E, slot topk): Ep experts, topk_p slots per token */
+    const uint32_t sh = bank->has_shared ? 1u : 0u, Ep = E + sh;
+    const uint32_t topk_p = (uint32_t)topk + sh;
+    if (topk <= 0 || topk > PF_MAXK || E == 0 || Ep > PF_MAXE)
         return hipErrorInvalidValue;
     if (dim == 0 || inter == 0 || dim % 256 || inter % 128) return hipErrorInvalidValue;
     if (dim / 128 > PF_SCT_MAX || inter / 128 > PF_SCT_MAX) return hipErrorInvalidValue;
-    const size_t P = T * (size_t)topk;
+    const size_t P = T * (size_t)topk_p;
     if (P > ws->cap_pairs || P > 0x7fffffffu) return hipErrorInvalidValue;
     if (ws->n_cu == 0 || ws->n_cu % 8) return hipErrorInvalidValue;
     if (((uintptr_t)x & 15) || ((uintptr_t)out & 15) || ((uintptr_t)bank->base & 15)
@@ -1084,21 +1107,22 @@ extern "C" hipError_t ghip_launch_moe_prefill(const GhipBank *bank,
         || (bank->off_ds & 3))
         return hipErrorInvalidValue;
     const uint32_t nch = (uint32_t)ghip_moe_prefill_chunks(P);
-    const size_t mt = ghip_moe_prefill_max_tiles(P, E);
+    const size_t mt = ghip_moe_prefill_max_tiles(P, Ep);
     hipEvent_t e0 = ev ? ev[0] : nullptr, e1 = ev ? ev[1] : nullptr;
     hipEvent_t e2 = ev ? ev[2] : nullptr, e3 = ev ? ev[3] : nullptr;
     hipEvent_t e4 = ev ? ev[4] : nullptr, e5 = ev ? ev[5] : nullptr;
     hipEvent_t e6 = ev ? ev[6] : nullptr, e7 = ev ? ev[7] : nullptr;
     hipError_t e;
     if ((e = ghip_launch_fill_u32(ws->hdr, PF_HDR_WORDS, 0u, st)) != hipSuccess) return e;
-    GHIP_LAUNCH(e0, nullptr, k_pf_count, dim3(nch), dim3(1024), E * 4, st, idx,
-                (uint32_t)P, (uint32_t)topk, E, ws->cnt, ws->eid, ws->hdr, bank->err);
+    GHIP_LAUNCH(e0, nullptr, k_pf_count, dim3(nch), dim3(1024), Ep * 4, st, idx,
+                (uint32_t)P, (uint32_t)topk, topk_p, E, ws->cnt, ws->eid, ws->hdr,
+                bank->err);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(k_pf_scan, dim3(1), dim3(1024), 0, st, ws->cnt, nch, E,
+    hipLaunchKernelGGL(k_pf_scan, dim3(1), dim3(1024), 0, st, ws->cnt, nch, Ep,
                        bank->nan_flags, (uint4 *)ws->tiles, ws->hdr);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    GHIP_LAUNCH(nullptr, e1, k_pf_scatter, dim3(nch), dim3(1024), 16 * E * 4, st,
-                ws->eid, (uint32_t)P, E, ws->cnt, ws->perm, ws->pos);
+    GHIP_LAUNCH(nullptr, e1, k_pf_scatter, dim3(nch), dim3(1024), 16 * Ep * 4, st,
+                ws->eid, (uint32_t)P, Ep, ws->cnt, ws->perm, ws->pos);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     const size_t lds = PF_LDS, lds8 = PF_LDS_WB;
     (void)mt;
@@ -1107,28 +1131,29 @@ extern "C" hipError_t ghip_launch_moe_prefill(const GhipBank *bank,
      * least half a 256-row tile per expert): one wave's MFMAs cover the
      * other's DMA issue; sparse routings (mostly short tiles) keep one wave
      * per SIMD, which wastes no MFMAs on a half-empty row split */
-    const bool full = P >= (size_t)E * (PF_BM / 2);
+    const bool full = P >= (size_t)Ep * (PF_BM / 2);
     if (full)
         GHIP_LAUNCH(e2, e3, (k_pf_gemm<0, 8>), dim3(g0), dim3(512), lds8, st, *bank,
                     x, ws->perm, (const uint4 *)ws->tiles, ws->hdr, inter / 128,
-                    (uint32_t)topk, limit, ws->h);
+                    topk_p, limit, ws->h);
     else
         GHIP_LAUNCH(e2, e3, (k_pf_gemm<0, 4>), dim3(g0), dim3(256), lds, st, *bank,
                     x, ws->perm, (const uint4 *)ws->tiles, ws->hdr, inter / 128,
-                    (uint32_t)topk, limit, ws->h);
+                    topk_p, limit, ws->h);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (full)
         GHIP_LAUNCH(e4, e5, (k_pf_gemm<1, 8>), dim3(g1), dim3(512), lds8, st, *bank,
                     ws->h, ws->perm, (const uint4 *)ws->tiles, ws->hdr, dim / 256,
-                    (uint32_t)topk, limit, ws->o);
+                    topk_p, limit, ws->o);
     else
         GHIP_LAUNCH(e4, e5, (k_pf_gemm<1, 4>), dim3(g1), dim3(256), lds, st, *bank,
                     ws->h, ws->perm, (const uint4 *)ws->tiles, ws->hdr, dim / 256,
-                    (uint32_t)topk, limit, ws->o);
+                    topk_p, limit, ws->o);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     const size_t nblk_c = T * (size_t)((dim + 2047) / 2048);
     GHIP_LAUNCH(e6, e7, k_pf_combine, dim3((uint32_t)nblk_c), dim3(256),
-                0, st, ws->o, ws->pos, idx, w, (uint32_t)T, (uint32_t)topk, dim, out);
+                0, st, ws->o, ws->pos, idx, w, (uint32_t)T, (uint32_t)topk, topk_p, dim,
+                out);
     return hipGetLastError();
 }
 

@@ -214,13 +214,38 @@ def moe_algorithmic_bytes(E, k, dim, inter):
             k * gu + dim * 2 + E * 4 + k * inter * 2)
 
 
-def bench_moe_decode(lib, pkg, rt, steps, warmup, rotate=64):
+def synth_slab(lib, seed, bank, e, dim, inter):
+    """Host slab of expert e of `bank` from the shared generator (the
+    streams apus_ghip_store_synth uses; e = E gives the shared expert's)."""
+    nb = lambda n: (n + 127) // 128  # noqa: E731
+    parts = []
+    for j, (o, kk) in enumerate([(inter, dim), (inter, dim), (dim, inter)]):
+        c = np.empty(o * kk, np.uint8)
+        lib.apus_synth_fp8_codes(c.ctypes.data_as(ctypes.c_void_p), c.size, seed,
+                                 lib.apus_synth_expert_stream(bank, e, 2 * j), 0)
+        sc = np.empty(nb(o) * nb(kk), np.float32)
+        lib.apus_synth_scales(sc.ctypes.data_as(ctypes.c_void_p), sc.size, seed,
+                              lib.apus_synth_expert_stream(bank, e, 2 * j + 1),
+                              ctypes.c_float(1e-4), ctypes.c_float(1e-2))
+        parts += [c, sc.view(np.uint8)]
+    return np.concatenate(parts)
+
+
+def bench_moe_decode(lib, pkg, rt, steps, warmup, rotate=64, shared=False):
+    """Config 2 (one token, 8 routed experts of the 288-expert bank, device
+    top-8 + softmax of f32 logits); with shared=True the layer's shared
+    expert (c/gmoe.h:325-336) is added last, as every GLM-5.3-Flash MoE
+    layer has one (reference/config.json: n_shared_experts 1)."""
     E, k, dim, inter, seed = (MOE[x] for x in ("E", "k", "dim", "inter", "seed"))
     store = ctypes.c_void_p()
     err = ctypes.create_string_buffer(256)
     pkg.check(lib.apus_ghip_store_open(ctypes.byref(store), E, dim, inter,
                                        MOE["limit"], err, 256), "store_open")
     pkg.check(lib.apus_ghip_store_synth(store, seed, 0, 1e-4, 1e-2), "store_synth")
+    if shared:
+        sl = synth_slab(lib, seed, 0, E, dim, inter)
+        pkg.check(lib.apus_ghip_store_put_shared(store, sl.ctypes.data_as(ctypes.c_void_p),
+                                                 sl.nbytes), "store_put_shared")
     logits = np.empty((rotate, E), np.float32)
     lib.apus_synth_f32_normal(logits.ctypes.data_as(ctypes.c_void_p), logits.size,
                               seed, 30, 0)
@@ -251,26 +276,32 @@ def bench_moe_decode(lib, pkg, rt, steps, warmup, rotate=64):
     # and rotation 0's output (every step of it writes the same bits)
     errors = store_errors(lib, store)
     out0 = d_out.download(np.uint16, (rotate, dim))[0]
-    nbytes, flops, _ = moe_algorithmic_bytes(E, k, dim, inter)
+    nbytes, flops, _ = moe_algorithmic_bytes(E, k + (1 if shared else 0), dim, inter)
     gbs = nbytes / (ms * 1e-3) / 1e9
     lib.apus_ghip_store_close(store)
     # the step is one launch: routing, gate/up, hand-off, down + combine
     kern = {"kernel": "k_moe_decode", "kernel_ms": kt["k_moe_decode"],
             "kernel_bytes": nbytes, "kernel_flops": flops,
             "launch_ms": {n: round(v, 5) for n, v in kt.items()}}
+    cfg = {"workload": "moe_decode (BASELINE config 2)", "experts": E,
+           "topk": k, "dim": dim, "inter": inter, "tokens": 1,
+           "rotated_tokens": rotate, "weights": "fp8-e4m3 128x128 blocks",
+           "routing": "device top-8 of f32 logits, softmax"}
+    if shared:
+        cfg["workload"] = ("moe_decode_shared (BASELINE config 2 + the layer's shared "
+                           "expert, c/gmoe.h:325-336)")
+        cfg["shared_experts"] = 1
     return {
         "ms_per_step": ms, "value": gbs, "wall_s": wall, "one_launch_per_step": True,
         "_device_errors": errors, "_gpu_out": out0,
-        "weight_bytes": k * 3 * inter * dim,
+        "weight_bytes": (k + (1 if shared else 0)) * 3 * inter * dim,
         "bytes": nbytes, "flops": flops, **kern,
-        "config": {"workload": "moe_decode (BASELINE config 2)", "experts": E,
-                   "topk": k, "dim": dim, "inter": inter, "tokens": 1,
-                   "rotated_tokens": rotate, "weights": "fp8-e4m3 128x128 blocks",
-                   "routing": "device top-8 of f32 logits, softmax"},
+        "traffic_key": "k_moe_decode@shared" if shared else "k_moe_decode",
+        "config": cfg,
     }
 
 
-def cpu_moe_decode(lib, budget_s=12.0):
+def cpu_moe_decode(lib, budget_s=12.0, shared=False):
     """Reference CPU path for config 2 on this host: per token, the 8
     routed experts (c/gmoe.h:210-227 on BF16 payloads, dequantized on fill as
     c/gcache.h:413-426) and the ordered combine (c/gmoe.h:307-320). The
@@ -305,6 +336,26 @@ def cpu_moe_decode(lib, budget_s=12.0):
             t_deq += time.perf_counter() - t0
             mats.append(out)
         payloads.append((e, mats))
+    if shared:
+        # the shared expert's payload (dequantized at open by the reference,
+        # c/gmodel.h:962-997; timed with the fills), added after the routed sum
+        mats = []
+        for j, (o, kk) in enumerate([(inter, dim), (inter, dim), (dim, inter)]):
+            c = np.empty((o, kk), np.uint8)
+            lib.apus_synth_fp8_codes(P(c), c.size, seed,
+                                     lib.apus_synth_expert_stream(0, E, 2 * j), 0)
+            sc_ = np.empty((O.nblocks(o), O.nblocks(kk)), np.float32)
+            lib.apus_synth_scales(P(sc_), sc_.size, seed,
+                                  lib.apus_synth_expert_stream(0, E, 2 * j + 1), 1e-4, 1e-2)
+            out = np.empty((o, kk), np.uint16)
+            t0 = time.perf_counter()
+            if use_ref:
+                O.ref().ref_fp8blk_dequant_mt(P(c), P(sc_), P(out), o, kk)
+            else:
+                O.lib().apo_fp8blk_dequant_mt(P(c), P(sc_), P(out), o, kk, CPU_THREADS)
+            t_deq += time.perf_counter() - t0
+            mats.append(out)
+        shared_pl = mats
     wsorted = {int(i): float(v) for i, v in zip(idx, w)}
     x = np.empty(dim, np.uint16)
     ntok, t_tok = 0, 0.0
@@ -324,20 +375,30 @@ def cpu_moe_decode(lib, budget_s=12.0):
             y = O.bf16_to_f32(O.f32_to_bf16(y + c))
             if ntok == 0:
                 floor += np.abs(c.astype(np.float64))
+        if shared:
+            g, u, d = shared_pl
+            if use_ref:
+                O.ref().ref_gmoe_expert(P(g), P(u), P(d), P(x), dim, inter,
+                                        MOE["limit"], P(eo))
+            else:
+                eo[:] = O.swiglu_expert(g, u, d, x, threads=CPU_THREADS)[0]
+            y = O.bf16_to_f32(O.f32_to_bf16(y + O.bf16_to_f32(eo)))   # c/gmoe.h:325-336
+            if ntok == 0:
+                floor += np.abs(O.bf16_to_f32(eo).astype(np.float64))
         t_tok += time.perf_counter() - t0
         if ntok == 0:
             ref_out = O.f32_to_bf16(y)         # the bench's rotation 0 (x, logits)
         ntok += 1
-    nbytes = moe_algorithmic_bytes(E, k, dim, inter)[0]
+    nbytes = moe_algorithmic_bytes(E, k + (1 if shared else 0), dim, inter)[0]
     per_tok = t_tok / ntok
     return {
         "value": nbytes / per_tok / 1e9, "unit": "GB/s",
         **cpu_common(O, use_ref),
         "kind": "reference" if use_ref else "port",
-        "sample": ("%d decode tokens x 8 experts on pre-dequantized BF16 payloads "
-                   "(%.1f ms/token); dequant-on-fill of the 8 experts %.1f ms "
-                   "reported separately, not in value" % (ntok, per_tok * 1e3,
-                                                          t_deq * 1e3)),
+        "sample": ("%d decode tokens x %d experts on pre-dequantized BF16 payloads "
+                   "(%.1f ms/token); dequant-on-fill of those experts %.1f ms "
+                   "reported separately, not in value"
+                   % (ntok, k + (1 if shared else 0), per_tok * 1e3, t_deq * 1e3)),
         "ms_per_token": per_tok * 1e3, "dequant_fill_ms": t_deq * 1e3,
         "_ref_out": {"out": ref_out, "floor": floor,
                      "what": "token 0: the reference's expert calls + combine"},
@@ -1328,6 +1389,10 @@ def run_workload(name, lib, pkg, rt, args, cpu_leg):
         r = bench_moe_decode(lib, pkg, rt, args.steps, args.warmup)
         return ("FP8 MoE decode GEMV HBM GB/s", r,
                 cpu_moe_decode(lib) if cpu_leg else None)
+    if name == "moe_decode_shared":
+        r = bench_moe_decode(lib, pkg, rt, args.steps, args.warmup, shared=True)
+        return ("FP8 MoE decode GEMV HBM GB/s (routed + shared expert)", r,
+                cpu_moe_decode(lib, shared=True) if cpu_leg else None)
     if name in ("dense_gemv", "dense_gemv_c0"):
         cfg = 0 if name == "dense_gemv_c0" else 1
         r = bench_dense_gemv(lib, pkg, rt, args.steps, args.warmup, M=args.m, cfg=cfg)
@@ -1417,7 +1482,8 @@ def main():
                     help="untimed warmup steps (default per workload: 500 for "
                          "the decode GEMVs, 2 for prefill, 20 otherwise)")
     ap.add_argument("--workload", default="moe_decode",
-                    choices=["moe_decode", "dense_gemv", "dense_gemv_c0", "dense_gemm",
+                    choices=["moe_decode", "moe_decode_shared", "dense_gemv", "dense_gemv_c0",
+                             "dense_gemm",
                              "bf16_gemv",
                              "moe_decode_router", "store_load", "prefill_zipf",
                              "prefill_stack", "copy", "library_gemm"])
@@ -1438,6 +1504,7 @@ def main():
     # the GPU, so the timed steps measure the device, not Python's jitter
     # (same kernel times; 20 warmup steps read ~7% lower step rates).
     dflt = {"moe_decode": (2000, 500), "moe_decode_router": (2000, 500),
+            "moe_decode_shared": (2000, 500),
             "dense_gemv": (2000, 500), "dense_gemv_c0": (2000, 500),
             "bf16_gemv": (2000, 500),
             "prefill_zipf": (40, 5), "prefill_stack": (5, 2),
@@ -1482,6 +1549,14 @@ def main():
             line["dense"].append(line_of("FP8 dense decode GEMV HBM GB/s", r2, c2, ds, dw))
             print("bench: config %d M=%d done (%.4f ms/step)" % (cfg, M, r2["ms_per_step"]),
                   file=sys.stderr, flush=True)
+    if args.workload == "moe_decode" and not args.no_dense:
+        # the decode as the model runs it: the layer's shared expert added
+        # after the routed sum (c/gmoe.h:325-336), one launch
+        line["decode_variants"] = []
+        m2, r2, c2 = run_workload("moe_decode_shared", lib, pkg, rt, args, cpu is not None)
+        line["decode_variants"].append(line_of(m2, r2, c2, args.steps, args.warmup))
+        print("bench: moe_decode_shared done (%.4f ms/step)" % r2["ms_per_step"],
+              file=sys.stderr, flush=True)
     if args.workload == "moe_decode" and not args.no_prefill:
         # the metric's second half ("...; prefill grouped-GEMM
         # TFLOP/s (%MFMA)"): configs 4 and 3, each a full step of its own
@@ -1498,7 +1573,8 @@ def main():
             print("bench: %s done (%.4f ms/step)" % (name, r2["ms_per_step"]),
                   file=sys.stderr, flush=True)
     print(json.dumps(line))
-    objs = [line] + line.get("dense", []) + line.get("prefill", [])
+    objs = ([line] + line.get("dense", []) + line.get("decode_variants", [])
+            + line.get("prefill", []))
     bad = [o["config"].get("workload") for o in objs if not o["verified"]["ok"]]
     if bad:
         print("bench: verification failed for %s" % bad, file=sys.stderr)

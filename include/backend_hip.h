@@ -177,6 +177,17 @@ int apus_ghip_store_synth(ApusGhipStore *s, uint64_t seed, int bank,
 /* Device address of expert e's slab (NULL when out of range): members in
  * the same order at 256-byte aligned offsets. */
 const void *apus_ghip_store_slab_dev(const ApusGhipStore *s, int expert);
+/* The layer's shared expert (c/gmoe.h:325-336; every token runs it and its
+ * output is added last, with one more bf16 rounding and no weight: out =
+ * bf16(routed + shared)). The slab has the routed experts' layout and
+ * intermediate size (n_shared_experts = 1 makes the shared intermediate
+ * moe_intermediate_size, c/gmodel.h:963-964); one H2D copy into a slot the
+ * store reserves after the routed experts. Once set, apus_ghip_moe_decode*
+ * and apus_ghip_moe_prefill* include it; slab NULL removes it. The decode
+ * with a shared expert needs inter <= 8 x the device's CUs (2048 on 256
+ * CUs). Extension: the reference dequantizes the shared expert at open
+ * and runs it on the CPU. */
+int apus_ghip_store_put_shared(ApusGhipStore *s, const void *slab, size_t nbytes);
 /* Read expert e's slab back in the host slab format (row-major members,
  * c/gcache.h:852-861 order): the inverse of apus_ghip_store_put.
  * Extension; no counterpart in the reference. */
@@ -223,7 +234,8 @@ int apus_ghip_moe_router_dev(const uint16_t *x, const uint16_t *gate_w,
                              int32_t *idx, float *w, void *stream);
 
 /* --- routed MoE decode (one token): SwiGLU experts + ordered combine,
- * c/gmoe.h:210-227 + 307-320 without the router and shared expert. One
+ * c/gmoe.h:210-227 + 307-320 (+ 325-336 when the store holds a shared
+ * expert, apus_ghip_store_put_shared), without the router. One
  * persistent launch (one workgroup per CU, all resident at once): routing,
  * gate/up GEMVs with the SwiGLU epilogue (activations to HBM as words
  * tagged with the launch), then down GEMVs, each wave starting as soon as

@@ -607,16 +607,23 @@ void apo_slab_dequant(const uint8_t *slab, size_t dim, size_t inter,
     }
 }
 
-int apo_moe_forward(const uint8_t *const *slabs, int n_experts,
-                    size_t dim, size_t inter, float limit,
-                    const uint16_t *x, size_t T, const int32_t *idx,
-                    const float *w, int topk, uint16_t *out,
-                    uint16_t *expert_out, int threads) {
+/* c/gmoe.h:294-336 per token: the routed experts in ascending id (one bf16
+ * rounding per add), then, when shared_slab is given, the shared expert's
+ * output added last with one more rounding: out = bf16(y + sh) (no weight,
+ * c/gmoe.h:325-336; the shared expert's intermediate is inter, as
+ * n_shared_experts = 1 makes it, c/gmodel.h:963-964). */
+static int apo_moe_loop(const uint8_t *const *slabs, int n_experts,
+                        const uint8_t *shared_slab, size_t dim, size_t inter,
+                        float limit, const uint16_t *x, size_t T, const int32_t *idx,
+                        const float *w, int topk, uint16_t *out,
+                        uint16_t *expert_out, uint16_t *shared_out, int threads) {
     const size_t pn = 3 * inter * dim;
     uint16_t **payload = (uint16_t **)calloc((size_t)n_experts, sizeof(*payload));
     float *y = (float *)malloc(dim * sizeof(float));
     uint16_t *eo = (uint16_t *)malloc(dim * 2);
-    int rc = (!payload || !y || !eo);
+    uint16_t *spl = shared_slab ? (uint16_t *)malloc(pn * 2) : NULL;
+    int rc = (!payload || !y || !eo || (shared_slab && !spl));
+    if (!rc && spl) apo_slab_dequant(shared_slab, dim, inter, spl, threads);
     for (size_t t = 0; t < T && !rc; t++) {
         const int32_t *it = idx + t * (size_t)topk;
         for (size_t i = 0; i < dim; i++) y[i] = 0.0f;
@@ -644,6 +651,13 @@ int apo_moe_forward(const uint8_t *const *slabs, int n_experts,
                 y[i] = apo_bf16_round(y[i] + contrib);
             }
         }
+        if (spl && !rc) {
+            rc |= apo_swiglu_expert(spl, spl + inter * dim, spl + 2 * inter * dim,
+                                    x + t * dim, dim, inter, limit, eo,
+                                    NULL, NULL, NULL, threads);
+            if (shared_out) memcpy(shared_out + t * dim, eo, dim * 2);
+            for (size_t i = 0; i < dim; i++) y[i] = y[i] + apo_bf16_f32(eo[i]);
+        }
         for (size_t i = 0; i < dim; i++) out[t * dim + i] = apo_bf16_bits(y[i]);
     }
     if (payload)
@@ -651,7 +665,26 @@ int apo_moe_forward(const uint8_t *const *slabs, int n_experts,
     free(payload);
     free(y);
     free(eo);
+    free(spl);
     return rc;
+}
+
+int apo_moe_forward(const uint8_t *const *slabs, int n_experts,
+                    size_t dim, size_t inter, float limit,
+                    const uint16_t *x, size_t T, const int32_t *idx,
+                    const float *w, int topk, uint16_t *out,
+                    uint16_t *expert_out, int threads) {
+    return apo_moe_loop(slabs, n_experts, NULL, dim, inter, limit, x, T, idx, w, topk,
+                        out, expert_out, NULL, threads);
+}
+
+int apo_moe_forward_shared(const uint8_t *const *slabs, int n_experts,
+                           const uint8_t *shared_slab, size_t dim, size_t inter,
+                           float limit, const uint16_t *x, size_t T, const int32_t *idx,
+                           const float *w, int topk, uint16_t *out,
+                           uint16_t *expert_out, uint16_t *shared_out, int threads) {
+    return apo_moe_loop(slabs, n_experts, shared_slab, dim, inter, limit, x, T, idx, w,
+                        topk, out, expert_out, shared_out, threads);
 }
 
 /* GEMM over many activation rows for the grouped checker: rows go in
@@ -834,7 +867,8 @@ static int apo_gemm_rowvec64(const uint16_t *w, const uint16_t *x, uint16_t *y,
  * are kept, and each token's ascending-expert combine (c/gmoe.h:307-320)
  * follows. Bitwise equal to apo_moe_forward. */
 static int apo_moe_grouped(const uint8_t *const *slabs, int n_experts,
-                           size_t dim, size_t inter, float limit,
+                           const uint8_t *shared_slab, size_t dim, size_t inter,
+                           float limit,
                            const uint16_t *x, size_t T, const int32_t *idx,
                            const float *w, int topk, uint16_t *out,
                            uint16_t *expert_out, double *floor_out, int threads,
@@ -914,6 +948,38 @@ static int apo_moe_grouped(const uint8_t *const *slabs, int n_experts,
         }
         free(xe); free(g); free(u); free(oe);
     }
+    /* the shared expert over all T tokens (c/gmoe.h:325-336): its output
+     * sh [T, dim] and, for floor_out, its expert-output floor */
+    uint16_t *sh = shared_slab ? (uint16_t *)malloc((T ? T : 1) * dim * 2) : NULL;
+    uint16_t *fsh = shared_slab && floor_out ? (uint16_t *)malloc((T ? T : 1) * dim * 2)
+                                             : NULL;
+    if (shared_slab && (!sh || (floor_out && !fsh))) rc = 1;
+    if (shared_slab && !rc && T) {
+        uint16_t *g = (uint16_t *)malloc(T * inter * 2);
+        uint16_t *u = (uint16_t *)malloc(T * inter * 2);
+        if (!g || !u) rc = 1;
+        if (!rc) {
+            apo_slab_dequant(shared_slab, dim, inter, payload, threads);
+            rc |= gemm(payload, x, g, T, inter, dim, threads);
+            rc |= gemm(payload + inter * dim, x, u, T, inter, dim, threads);
+            for (size_t i = 0; i < T * inter; i++) {
+                float gv = apo_bf16_f32(g[i]), uv = apo_bf16_f32(u[i]);
+                if (gv > limit) gv = limit;
+                if (uv > limit) uv = limit;
+                else if (uv < -limit) uv = -limit;
+                float hv = apo_bf16_round(gv * apo_sigmoid_np(gv));
+                g[i] = apo_bf16_bits(apo_bf16_round(hv * uv));
+            }
+            rc |= gemm(payload + 2 * inter * dim, g, sh, T, dim, inter, threads);
+            if (floor_out && !rc) {
+                const uint16_t *pd = payload + 2 * inter * dim;
+                for (size_t i = 0; i < dim * inter; i++) dabs[i] = pd[i] & 0x7fffu;
+                for (size_t i = 0; i < T * inter; i++) g[i] &= 0x7fffu;
+                rc |= apo_gemm_rowvec64(dabs, g, fsh, T, dim, inter, threads);
+            }
+        }
+        free(g); free(u);
+    }
     /* c/gmoe.h:307-320 per token: ascending expert id over its kept pairs */
     float *y = (float *)malloc(dim * sizeof(float));
     if (!y) rc = 1;
@@ -939,9 +1005,16 @@ static int apo_moe_grouped(const uint8_t *const *slabs, int n_experts,
                     floor_out[t * dim + i] += fabs((double)wt)
                                               * (double)apo_bf16_f32(fe[best * dim + i]);
         }
+        if (sh) {
+            for (size_t i = 0; i < dim; i++) y[i] = y[i] + apo_bf16_f32(sh[t * dim + i]);
+            if (floor_out)
+                for (size_t i = 0; i < dim; i++)
+                    floor_out[t * dim + i] += (double)apo_bf16_f32(fsh[t * dim + i]);
+        }
         for (size_t i = 0; i < dim; i++) out[t * dim + i] = apo_bf16_bits(y[i]);
     }
     free(y);
+    free(sh); free(fsh);
     free(dabs); free(fe);
     free(keep); free(cnt); free(list); free(payload);
     if (!expert_out) free(eo);
@@ -949,29 +1022,29 @@ static int apo_moe_grouped(const uint8_t *const *slabs, int n_experts,
 }
 
 int apo_moe_forward_grouped(const uint8_t *const *slabs, int n_experts,
-                            size_t dim, size_t inter, float limit,
-                            const uint16_t *x, size_t T, const int32_t *idx,
+                            const uint8_t *shared_slab, size_t dim, size_t inter,
+                            float limit, const uint16_t *x, size_t T, const int32_t *idx,
                             const float *w, int topk, uint16_t *out,
                             uint16_t *expert_out, int threads) {
-    return apo_moe_grouped(slabs, n_experts, dim, inter, limit, x, T, idx, w, topk, out,
-                           expert_out, NULL, threads, 0);
+    return apo_moe_grouped(slabs, n_experts, shared_slab, dim, inter, limit, x, T, idx, w,
+                           topk, out, expert_out, NULL, threads, 0);
 }
 
 int apo_moe_floor_grouped(const uint8_t *const *slabs, int n_experts,
-                          size_t dim, size_t inter, float limit,
-                          const uint16_t *x, size_t T, const int32_t *idx,
+                          const uint8_t *shared_slab, size_t dim, size_t inter,
+                          float limit, const uint16_t *x, size_t T, const int32_t *idx,
                           const float *w, int topk, uint16_t *out,
                           double *floor_out, int threads) {
     for (size_t i = 0; i < T * dim; i++) floor_out[i] = 0.0;
-    return apo_moe_grouped(slabs, n_experts, dim, inter, limit, x, T, idx, w, topk, out,
-                           NULL, floor_out, threads, 0);
+    return apo_moe_grouped(slabs, n_experts, shared_slab, dim, inter, limit, x, T, idx, w,
+                           topk, out, NULL, floor_out, threads, 0);
 }
 
 int apo_moe_chain64_grouped(const uint8_t *const *slabs, int n_experts,
-                            size_t dim, size_t inter, float limit,
-                            const uint16_t *x, size_t T, const int32_t *idx,
+                            const uint8_t *shared_slab, size_t dim, size_t inter,
+                            float limit, const uint16_t *x, size_t T, const int32_t *idx,
                             const float *w, int topk, uint16_t *out,
                             uint16_t *expert_out, int threads) {
-    return apo_moe_grouped(slabs, n_experts, dim, inter, limit, x, T, idx, w, topk, out,
-                           expert_out, NULL, threads, 1);
+    return apo_moe_grouped(slabs, n_experts, shared_slab, dim, inter, limit, x, T, idx, w,
+                           topk, out, expert_out, NULL, threads, 1);
 }

@@ -101,13 +101,26 @@ int apo_moe_forward(const uint8_t *const *slabs, int n_experts,
                     const float *w, int topk, uint16_t *out,
                     uint16_t *expert_out, int threads);
 
+/* apo_moe_forward plus the shared expert (c/gmoe.h:325-336): after the
+ * routed combine, out = bf16(y + sh) with sh the shared expert's bf16
+ * output on the shared slab (same layout; intermediate = inter, as
+ * n_shared_experts = 1 gives, c/gmodel.h:963-964). shared_out (optional)
+ * [T, dim]: sh. */
+int apo_moe_forward_shared(const uint8_t *const *slabs, int n_experts,
+                           const uint8_t *shared_slab, size_t dim, size_t inter,
+                           float limit, const uint16_t *x, size_t T, const int32_t *idx,
+                           const float *w, int topk, uint16_t *out,
+                           uint16_t *expert_out, uint16_t *shared_out, int threads);
+
 /* The same result computed expert by expert (each used expert dequantized
  * once, its tokens as one M-row GEMM per matrix; bitwise equal to
- * apo_moe_forward by the M-independence of c/bf16.h:27-37), for checks at
- * full size. expert_out (optional) [T, topk, dim]: out_e per kept (token,
- * slot); the entries of dropped slots are left as they are. */
+ * apo_moe_forward, or to apo_moe_forward_shared with shared_slab non-NULL,
+ * by the M-independence of c/bf16.h:27-37), for checks at full size.
+ * expert_out (optional) [T, topk, dim]: out_e per kept (token, slot); the
+ * entries of dropped slots are left as they are. */
 int apo_moe_forward_grouped(const uint8_t *const *slabs, int n_experts,
-                            size_t dim, size_t inter, float limit,
+                            const uint8_t *shared_slab, size_t dim, size_t inter,
+                            float limit,
                             const uint16_t *x, size_t T, const int32_t *idx,
                             const float *w, int topk, uint16_t *out,
                             uint16_t *expert_out, int threads);
@@ -117,7 +130,8 @@ int apo_moe_forward_grouped(const uint8_t *const *slabs, int n_experts,
  * the reference's rounding points; SwiGLU and combine unchanged), free of
  * any fp32 summation order. */
 int apo_moe_chain64_grouped(const uint8_t *const *slabs, int n_experts,
-                            size_t dim, size_t inter, float limit,
+                            const uint8_t *shared_slab, size_t dim, size_t inter,
+                            float limit,
                             const uint16_t *x, size_t T, const int32_t *idx,
                             const float *w, int topk, uint16_t *out,
                             uint16_t *expert_out, int threads);
@@ -128,7 +142,8 @@ int apo_moe_chain64_grouped(const uint8_t *const *slabs, int n_experts,
  * expert-output floor (the down GEMM's term magnitudes, h the reference's)
  * carried through the combine weights. */
 int apo_moe_floor_grouped(const uint8_t *const *slabs, int n_experts,
-                          size_t dim, size_t inter, float limit,
+                          const uint8_t *shared_slab, size_t dim, size_t inter,
+                          float limit,
                           const uint16_t *x, size_t T, const int32_t *idx,
                           const float *w, int topk, uint16_t *out,
                           double *floor_out, int threads);

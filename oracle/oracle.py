@@ -55,12 +55,14 @@ _ORACLE_SIGS = {
     "apo_slab_dequant": (None, [c_vp, c_size, c_size, c_vp, c_int]),
     "apo_moe_forward": (c_int, [c_vp, c_int, c_size, c_size, c_float, c_vp,
                                 c_size, c_vp, c_vp, c_int, c_vp, c_vp, c_int]),
-    "apo_moe_forward_grouped": (c_int, [c_vp, c_int, c_size, c_size, c_float, c_vp,
+    "apo_moe_forward_grouped": (c_int, [c_vp, c_int, c_vp, c_size, c_size, c_float, c_vp,
                                         c_size, c_vp, c_vp, c_int, c_vp, c_vp, c_int]),
-    "apo_moe_chain64_grouped": (c_int, [c_vp, c_int, c_size, c_size, c_float, c_vp,
+    "apo_moe_chain64_grouped": (c_int, [c_vp, c_int, c_vp, c_size, c_size, c_float, c_vp,
                                         c_size, c_vp, c_vp, c_int, c_vp, c_vp, c_int]),
-    "apo_moe_floor_grouped": (c_int, [c_vp, c_int, c_size, c_size, c_float, c_vp,
+    "apo_moe_floor_grouped": (c_int, [c_vp, c_int, c_vp, c_size, c_size, c_float, c_vp,
                                       c_size, c_vp, c_vp, c_int, c_vp, c_vp, c_int]),
+    "apo_moe_forward_shared": (c_int, [c_vp, c_int, c_vp, c_size, c_size, c_float, c_vp,
+                                       c_size, c_vp, c_vp, c_int, c_vp, c_vp, c_vp, c_int]),
     "apo_route_softmax": (None, [c_vp, c_int, c_int, c_vp, c_vp]),
     "apo_gate_dot": (c_float, [c_vp, c_vp, c_size]),
     "apo_gmoe_router": (None, [c_vp, c_vp, c_int, c_size, c_int, c_float, c_vp,
@@ -86,6 +88,8 @@ _REF_SIGS = {
     "ref_gmoe_expert": (c_int, [c_vp, c_vp, c_vp, c_vp, c_size, c_size,
                                 c_float, c_vp]),
     "ref_pool_threads": (c_int, []),
+    "ref_gmoe_forward2": (None, [c_vp, c_int, c_size, c_size, c_vp, c_size, c_float, c_vp,
+                                 c_vp, c_int, c_float, c_vp, c_size, c_vp, c_vp, c_vp]),
     "ref_gmoe_router": (None, [c_vp, c_vp, c_int, c_size, c_int, c_float, c_vp,
                                c_vp, c_vp, c_vp]),
 }
@@ -247,11 +251,12 @@ def route_softmax(logits, k):
 
 
 def moe_forward(slabs, dim, inter, x, idx, w, limit=10.0, threads=1,
-                want_expert_out=False, grouped=False, chain64=False):
+                want_expert_out=False, grouped=False, chain64=False, shared=None):
     """slabs: list of uint8 arrays (one slab per expert id; None allowed for
     experts no token routes to). grouped: compute expert by expert
     (apo_moe_forward_grouped, the same bits, far faster at many tokens).
-    chain64: the f64-sum yardstick (apo_moe_chain64_grouped) instead."""
+    chain64: the f64-sum yardstick (apo_moe_chain64_grouped) instead.
+    shared: the shared expert's slab (uint8), added last (c/gmoe.h:325-336)."""
     E = len(slabs)
     arr = (c_vp * E)()
     for e, s in enumerate(slabs):
@@ -263,15 +268,23 @@ def moe_forward(slabs, dim, inter, x, idx, w, limit=10.0, threads=1,
     k = idx.shape[1]
     out = np.empty((T, dim), np.uint16)
     eo = np.empty((T, k, dim), np.uint16) if want_expert_out else None
-    fn = (lib().apo_moe_chain64_grouped if chain64 else
-          lib().apo_moe_forward_grouped if grouped else lib().apo_moe_forward)
-    rc = fn(arr, E, dim, inter, limit, ptr(x), T, ptr(idx), ptr(w), k, ptr(out),
-            ptr(eo) if eo is not None else None, threads)
+    sp = ptr(shared) if shared is not None else None
+    eop = ptr(eo) if eo is not None else None
+    if chain64 or grouped:
+        fn = lib().apo_moe_chain64_grouped if chain64 else lib().apo_moe_forward_grouped
+        rc = fn(arr, E, sp, dim, inter, limit, ptr(x), T, ptr(idx), ptr(w), k, ptr(out),
+                eop, threads)
+    elif shared is not None:
+        rc = lib().apo_moe_forward_shared(arr, E, sp, dim, inter, limit, ptr(x), T,
+                                          ptr(idx), ptr(w), k, ptr(out), eop, None, threads)
+    else:
+        rc = lib().apo_moe_forward(arr, E, dim, inter, limit, ptr(x), T, ptr(idx), ptr(w),
+                                   k, ptr(out), eop, threads)
     assert rc == 0
     return (out, eo) if want_expert_out else out
 
 
-def moe_expert_floor(slabs, dim, inter, x, idx, w, limit=10.0, threads=1):
+def moe_expert_floor(slabs, dim, inter, x, idx, w, limit=10.0, threads=1, shared=None):
     """Per output element, sum over the token's kept pairs of |w_e| *
     sum_i |h_i * wd_e[j, i]| (f64, [T, dim]): the combine's tolerance floor
     that carries each expert output's own floor (apo_moe_floor_grouped)."""
@@ -285,6 +298,7 @@ def moe_expert_floor(slabs, dim, inter, x, idx, w, limit=10.0, threads=1):
     w = np.ascontiguousarray(w, np.float32).reshape(T, -1)
     out = np.empty((T, dim), np.uint16)
     fl = np.empty((T, dim), np.float64)
-    assert lib().apo_moe_floor_grouped(arr, E, dim, inter, limit, ptr(x), T, ptr(idx),
+    sp = ptr(shared) if shared is not None else None
+    assert lib().apo_moe_floor_grouped(arr, E, sp, dim, inter, limit, ptr(x), T, ptr(idx),
                                        ptr(w), idx.shape[1], ptr(out), ptr(fl), threads) == 0
     return fl

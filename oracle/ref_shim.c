@@ -21,6 +21,8 @@
  *   apus_gmoe_topk_stable        c/gmoe.h:175-189
  *   apus_gmoe_expert             c/gmoe.h:210-227
  *   apus_gmoe_router             c/gmoe.h:191-208
+ *   apus_gmoe_forward2           c/gmoe.h:265-337 (router, routed experts,
+ *                                shared expert; with its scratch init/free)
  */
 #define APUS_GMHC_IMPLEMENTATION
 #define APUS_GMOE_IMPLEMENTATION
@@ -32,6 +34,7 @@
 #include "fp8blk.h"
 
 #include <stdlib.h>
+#include <string.h>
 
 #define REF_API __attribute__((visibility("default")))
 
@@ -114,4 +117,50 @@ REF_API void ref_gmoe_router(const uint16_t *gate_w, const float *gate_bias, int
     float *b = (float *)malloc((size_t)(E > 0 ? E : 1) * sizeof(float));
     apus_gmoe_router(&r, x, scores, idx, w, b);
     free(b);
+}
+/* The whole MoE sublayer (c/gmoe.h:265-337) on BF16 payloads: per token
+ * the router, the routed experts in ascending id, then the shared expert
+ * added last. payloads[e] = expert e's [gate | up | down] (inter rows each);
+ * shared = the shared expert's payload (sinter rows). x / out [s, dim];
+ * idx_out / w_out [s, topk] (the router's picks; may be NULL). */
+REF_API void ref_gmoe_forward2(const uint16_t *const *payloads, int E, size_t dim,
+                               size_t inter, const uint16_t *shared, size_t sinter,
+                               float limit, const uint16_t *gate_w,
+                               const float *gate_bias, int topk, float route_scale,
+                               const uint16_t *x, size_t s, uint16_t *out,
+                               int32_t *idx_out, float *w_out) {
+    const uint16_t **eg = (const uint16_t **)malloc((size_t)E * sizeof(*eg));
+    const uint16_t **eu = (const uint16_t **)malloc((size_t)E * sizeof(*eu));
+    const uint16_t **ed = (const uint16_t **)malloc((size_t)E * sizeof(*ed));
+    for (int e = 0; e < E; e++) {
+        eg[e] = payloads[e];
+        eu[e] = payloads[e] + inter * dim;
+        ed[e] = payloads[e] + 2 * inter * dim;
+    }
+    ApusGmoeW w;
+    memset(&w, 0, sizeof w);
+    w.router.E = E;
+    w.router.topk = topk;
+    w.router.dim = dim;
+    w.router.route_scale = route_scale;
+    w.router.gate_w = gate_w;
+    w.router.gate_bias = gate_bias;
+    w.inter = inter;
+    w.eg = eg;
+    w.eu = eu;
+    w.ed = ed;
+    w.sg = shared;
+    w.su = shared + sinter * dim;
+    w.sd = shared + 2 * sinter * dim;
+    w.sinter = sinter;
+    w.limit = limit;
+    ApusGmoeInterm im;
+    memset(&im, 0, sizeof im);
+    im.router_idx = idx_out;
+    im.router_w = w_out;
+    ApusGmoeScratch sc;
+    apus_gmoe_scratch_init(&sc, &w, s);
+    apus_gmoe_forward2(&w, x, s, out, &im, &sc, NULL);
+    apus_gmoe_scratch_free(&sc);
+    free(eg); free(eu); free(ed);
 }

@@ -7,6 +7,7 @@ golden fixtures written by the reference's apus_gmoe_expert
 (c/gmoe.h:210-227). combine: order/rounding invariants of c/gmoe.h:307-320
 and the config-2 golden (reference expert outputs, reference loop).
 """
+import ctypes
 import json
 import os
 
@@ -344,3 +345,47 @@ def test_expert_floor_helper():
                 O.bf16_to_f32(h).astype(np.float64))
             want[t] += abs(float(w[t, j])) * F
     assert np.allclose(got, want, rtol=2.0 ** -8, atol=0)
+
+
+def _payload_of(slab, dim, inter):
+    pl = np.empty(3 * inter * dim, np.uint16)
+    O.lib().apo_slab_dequant(O.ptr(slab), dim, inter, O.ptr(pl), 1)
+    return pl
+
+
+@pytest.mark.skipif(not O.ref_available(), reason="reference build absent")
+def test_shared_expert_forward_vs_reference_forward2():
+    """The whole MoE sublayer of the reference (apus_gmoe_forward2,
+    c/gmoe.h:265-337: router, routed experts in ascending id, the shared
+    expert added last with one more bf16 rounding), built from the
+    reference sources, against the oracle's router (apo_gmoe_router) feeding
+    apo_moe_forward_shared, and the grouped form: bitwise, on payloads
+    dequantized from FP8 slabs (c/gmodel.h:962-997 dequantizes the shared
+    expert at open)."""
+    dim, inter, E, k, T = 256, 128, 12, 4, 9
+    rng = np.random.default_rng(325)
+    slabs = _bank(dim, inter, E, rng)
+    shared = _bank(dim, inter, 1, rng)[0]
+    gate_w = O.f32_to_bf16((rng.standard_normal((E, dim)) / 16).astype(np.float32))
+    bias = (rng.standard_normal(E) * 0.05).astype(np.float32)
+    x = O.f32_to_bf16((rng.standard_normal((T, dim)) * 2).astype(np.float32))
+    pls = [_payload_of(s, dim, inter) for s in slabs]
+    spl = _payload_of(shared, dim, inter)
+    arr = (ctypes.c_void_p * E)(*[p.ctypes.data for p in pls])
+    ref = np.empty((T, dim), np.uint16)
+    ridx = np.empty((T, k), np.int32)
+    rw = np.empty((T, k), np.float32)
+    O.ref().ref_gmoe_forward2(arr, E, dim, inter, O.ptr(spl), inter, 10.0, O.ptr(gate_w),
+                              O.ptr(bias), k, 2.5, O.ptr(x), T, O.ptr(ref), O.ptr(ridx),
+                              O.ptr(rw))
+    idx = np.empty((T, k), np.int32)
+    w = np.empty((T, k), np.float32)
+    for t in range(T):
+        _, idx[t], w[t] = O.gmoe_router(gate_w, bias, x[t], k, 2.5)
+    assert np.array_equal(idx, ridx) and np.array_equal(w, rw)
+    got = O.moe_forward(slabs, dim, inter, x, idx, w, shared=shared)
+    assert np.array_equal(got, ref)
+    grp = O.moe_forward(slabs, dim, inter, x, idx, w, shared=shared, grouped=True, threads=3)
+    assert np.array_equal(grp, ref)
+    # the shared add is a real step: without it the outputs differ
+    assert not np.array_equal(O.moe_forward(slabs, dim, inter, x, idx, w), ref)
