@@ -72,6 +72,8 @@ SIGNATURES = {
                                          c_vp, c_vp]),
     "apus_ghip_moe_router_dev": (c_int, [c_vp, c_vp, c_vp, c_vp, c_int, c_size, c_int,
                                          c_float, c_vp, c_vp, c_vp, c_vp]),
+    "apus_ghip_moe_decode_router_dev": (c_int, [c_vp, c_vp, c_vp, c_vp, c_float, c_int,
+                                                c_vp, c_vp, c_vp, c_vp]),
     "apus_ghip_moe_prefill_reserve": (c_int, [c_vp, c_size, c_int]),
     "apus_ghip_moe_prefill": (c_int, [c_vp, c_vp, c_size, c_vp, c_vp, c_int,
                                       c_vp]),

@@ -593,6 +593,8 @@ int apus_ghip_store_open(ApusGhipStore **out, int n_experts, size_t dim,
            || (s->ws.hw_inter = (uint32_t)inter) == 0
            || hipMalloc((void **)&s->ws.err, 4) != hipSuccess
            || hipMemset(s->ws.err, 0, 4) != hipSuccess
+           || hipMalloc((void **)&s->ws.lw, 512 * sizeof(uint64_t)) != hipSuccess
+           || hipMemset(s->ws.lw, 0, 512 * sizeof(uint64_t)) != hipSuccess
            || (s->ws.n_cu = G.n_cu_dev) == 0
            || hipMalloc((void **)&s->d_x, dim * 2) != hipSuccess
            || hipMalloc((void **)&s->d_out, dim * 2) != hipSuccess
@@ -615,6 +617,7 @@ void apus_ghip_store_close(ApusGhipStore *s) {
     hipFree(s->nan_flags);
     hipFree(s->ws.hw);
     hipFree(s->ws.err);
+    hipFree(s->ws.lw);
     hipFree(s->d_x);
     hipFree(s->d_out);
     hipFree(s->d_idx);
@@ -1044,12 +1047,40 @@ int apus_ghip_moe_decode_dev(ApusGhipStore *s, const uint16_t *x,
     }
     GhipBank bk;
     store_bank(s, &bk);
-    hipError_t e = ghip_launch_moe_decode(&bk, x, logits, idx, w, topk,
+    hipError_t e = ghip_launch_moe_decode(&bk, x, logits, idx, w, NULL, topk,
                                           s->limit, out, &s->ws,
                                           G.trace_n >= 2 ? G.trace_ev : NULL,
                                           (hipStream_t)stream);
     if (e != hipSuccess) {
         ghip_seterr("moe_decode launch: %s", hipGetErrorString(e));
+        return 1;
+    }
+    G.dispatches++;
+    return 0;
+}
+
+int apus_ghip_moe_decode_router_dev(ApusGhipStore *s, const uint16_t *x,
+                                    const uint16_t *gate_w, const float *gate_bias,
+                                    float route_scale, int topk, uint16_t *out,
+                                    int32_t *idx_out, float *w_out, void *stream) {
+    if (!s) { ghip_seterr("moe_decode_router: no store"); return 1; }
+    if (topk <= 0 || topk > GHIP_MAX_TOPK || topk > s->n_experts || s->n_experts > 512
+        || !gate_w || !gate_bias || (!idx_out) != (!w_out)) {
+        ghip_seterr("moe_decode_router: bad arguments (E=%d topk=%d; gate_w and bias "
+                    "required, idx_out and w_out both or neither, E <= 512)",
+                    s->n_experts, topk);
+        return 1;
+    }
+    GhipBank bk;
+    store_bank(s, &bk);
+    GhipRouterArgs ra = {gate_w, gate_bias, route_scale, idx_out, w_out};
+    hipError_t e = ghip_launch_moe_decode(&bk, x, NULL, NULL, NULL, &ra, topk, s->limit,
+                                          out, &s->ws,
+                                          G.trace_n >= 2 ? G.trace_ev : NULL,
+                                          (hipStream_t)stream);
+    if (e != hipSuccess) {
+        ghip_seterr("moe_decode_router launch: %s (16-byte x / gate_w; E <= 8 x CUs)",
+                    hipGetErrorString(e));
         return 1;
     }
     G.dispatches++;

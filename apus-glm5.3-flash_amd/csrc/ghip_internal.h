@@ -49,9 +49,22 @@ typedef struct {
     uint32_t *hw;         /* device [17 slots, hw_inter] u32: 16 routed + the shared expert */
     uint32_t hw_inter;    /* inter the words were sized for */
     uint32_t *err;        /* device u32: 2 = invalid expert id, 4 = hand-off wait ran out */
+    uint64_t *lw;         /* device [512] u64: the router-fed decode's tagged gate logits
+                             (the launch's tag in bits 32..47, the f32 logit in 0..31) */
     uint32_t n_cu;        /* grid: one workgroup per CU */
     uint32_t tag;         /* host: the last launch's tag (0 before the first) */
 } GhipMoeDecodeWs;
+
+/* The reference router's inputs for the router-fed decode (c/gmoe.h:191-208):
+ * gate_w [E, dim] bf16 (16-byte aligned), bias [E] f32 (selection only),
+ * route_scale; idx_out / w_out [topk] (both or neither) receive the picks. */
+typedef struct {
+    const uint16_t *gate_w;
+    const float *bias;
+    float route_scale;
+    int32_t *idx_out;
+    float *w_out;
+} GhipRouterArgs;
 
 /* Streaming GEMV set-up (dynamic-LDS limits, persistent grid bound). */
 hipError_t ghip_linear_init(uint32_t n_cu);
@@ -75,14 +88,16 @@ typedef struct {
 } GhipBank;
 
 /* K3: routed MoE decode for one token (routing, gate/up + SwiGLU, down +
- * ordered combine) as one cooperative launch on st (ws->n_cu workgroups);
- * ev: NULL or 2 events recorded around it. Either logits (device f32
- * [n_experts]; top-k + softmax on the device) or idx/w (device [topk]) must
- * be given. out: device [dim] bf16. Advances ws->tag. Launches that
+ * ordered combine, + the shared expert when the bank has one) as one launch
+ * on st (ws->n_cu workgroups); ev: NULL or 2 events recorded around it. The
+ * routing is one of: router (the reference router computed in the launch),
+ * logits (device f32 [n_experts]; top-k + softmax on the device) or idx/w
+ * (device [topk]). out: device [dim] bf16. Advances ws->tag. Launches that
  * share a workspace must not overlap in time. */
 hipError_t ghip_launch_moe_decode(const GhipBank *bank, const uint16_t *x,
                                   const float *logits, const int32_t *idx,
-                                  const float *w, int topk, float limit,
+                                  const float *w, const GhipRouterArgs *router,
+                                  int topk, float limit,
                                   uint16_t *out, GhipMoeDecodeWs *ws,
                                   const hipEvent_t *ev, hipStream_t st);
 

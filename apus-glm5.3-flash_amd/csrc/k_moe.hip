@@ -675,6 +675,199 @@ __device__ __forceinline__ bool md_stage_h_wave(const uint32_t *src, uint32_t in
 }
 
 /* ------------------------------------------------------------------------ */
+/* router with the reference semantics (c/gmoe.h:191-208)                   */
+/* ------------------------------------------------------------------------ */
+
+/* Gate logit of one row by one wave: sum_k w[k] * x[k] in f32, lane-strided
+ * partial sums (lane l takes k = 8l + 512i, ascending i) and a fixed
+ * xor-butterfly reduction: a GEMV of the same tolerance class as every
+ * other one here (the reference's sequential-k dot is c/gmoe.h:168-173).
+ * Eight row segments per lane are loaded before any is used, so a row
+ * costs one memory round trip, not one per segment. dim % 8 == 0, 16-byte
+ * aligned rows. */
+__device__ __forceinline__ float rt_gate_dot(const uint16_t *__restrict__ row,
+                                             const uint16_t *__restrict__ x, uint32_t dim,
+                                             uint32_t lane) {
+    float acc = 0.0f;
+    auto fma8 = [&](const ghip_u32x4 &wv, const ghip_u32x4 &xv) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            acc = acc + __uint_as_float(wv[q] << 16) * __uint_as_float(xv[q] << 16);
+            acc = acc + __uint_as_float(wv[q] & 0xffff0000u) *
+                            __uint_as_float(xv[q] & 0xffff0000u);
+        }
+    };
+    uint32_t k = lane * 8u;
+    for (; k + 7u * 512u < dim; k += 8u * 512u) {
+        ghip_u32x4 wv[8], xv[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            wv[u] = *(const ghip_u32x4 *)(row + k + 512u * u);
+            xv[u] = *(const ghip_u32x4 *)(x + k + 512u * u);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) fma8(wv[u], xv[u]);
+    }
+    for (; k < dim; k += 512u)
+        fma8(*(const ghip_u32x4 *)(row + k), *(const ghip_u32x4 *)(x + k));
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) acc = acc + __shfl_xor(acc, off, 64);
+    return acc;
+}
+
+/* Selection and weights from one wave's logits (c/gmoe.h:191-208): lane l
+ * holds the logits lv and biases bv of experts R l .. R l + R - 1 (those
+ * past E ignored); scores = numpy-stable sigmoid (device expf), the stable
+ * top-k (larger first, ties to the lower id) of score + bias -- the bias
+ * selects, it never weighs -- then w_j = score[idx_j] / (pairwise_sum +
+ * 1e-20) * route_scale, with numpy's float32 pairwise sum of the k
+ * selected scores in selection order (c/gmhc.h:165-185). Lane j < topk
+ * returns pick j's id and weight (selection order, as the reference
+ * returns them). sc: LDS [E] for the scores; scores (may be NULL): global
+ * [E] copy. */
+template <int R>
+__device__ __forceinline__ void rt_router_core(const float (&lv)[R], const float (&bv)[R],
+                                               uint32_t E, int topk, float scale, float *sc,
+                                               float *__restrict__ scores, int &myid,
+                                               float &myw) {
+    const int lane = threadIdx.x & 63;
+    uint32_t key[R];
+#pragma unroll
+    for (int s = 0; s < R; s++) {
+        const uint32_t i = (uint32_t)lane * R + s;
+        key[s] = 0u;
+        if (i < E) {
+            const float v = ghip_sigmoid_np(lv[s]);
+            sc[i] = v;
+            if (scores) scores[i] = v;
+            key[s] = rt_key(v + bv[s]);
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);           /* lgkmcnt(0) */
+    __builtin_amdgcn_wave_barrier();
+    uint32_t mk;
+    myid = rt_select<R>(key, topk, mk);
+    myw = lane < topk ? sc[myid] : 0.0f;
+    /* numpy float32 pairwise sum of the k selected scores (k <= 16) */
+    const float myv = myw;
+    auto at = [&](int i) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, myv), i));
+    };
+    float sum;
+    if (topk < 8) {
+        sum = at(0);
+        for (int i = 1; i < topk; i++) sum = sum + at(i);
+    } else {
+        float r[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) r[q] = at(q);
+        int i = 8;
+        if (topk >= 16) {
+#pragma unroll
+            for (int q = 0; q < 8; q++) r[q] = r[q] + at(8 + q);
+            i = 16;
+        }
+        sum = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+        for (; i < topk; i++) sum = sum + at(i);
+    }
+    myw = myv / (sum + 1e-20f) * scale;
+}
+
+/* The router's selection from logits read by lg(i) (one wave). */
+template <int R, typename Logit>
+__device__ __forceinline__ void rt_sigmoid_select(Logit lg, const float *__restrict__ bias,
+                                                  uint32_t E, int topk, float scale,
+                                                  float *sc, float *__restrict__ scores,
+                                                  int32_t *__restrict__ idx,
+                                                  float *__restrict__ w) {
+    const int lane = threadIdx.x & 63;
+    /* logits and biases of all R slots are loaded (clamped index, no
+     * predicated load) before any is used: one memory round trip */
+    float lv[R], bv[R];
+#pragma unroll
+    for (int s = 0; s < R; s++) {
+        const uint32_t i = (uint32_t)lane * R + s, ic = i < E ? i : E - 1u;
+        lv[s] = lg(ic);
+        bv[s] = bias[ic];
+    }
+#pragma unroll
+    for (int s = 0; s < R; s++) asm volatile("" ::"v"(lv[s]), "v"(bv[s]));
+    int myid;
+    float myw;
+    rt_router_core<R>(lv, bv, E, topk, scale, sc, scores, myid, myw);
+    if (lane < topk) {
+        idx[lane] = myid;
+        w[lane] = myw;
+    }
+}
+
+/* Phase A of the router-fed decode, wave 0 of every workgroup: the gate
+ * logits of all E experts, published by the workgroups that computed them
+ * as 64-bit words (this launch's tag in bits 32..47, the f32 logit in
+ * 0..31; device-coherent stores and loads, as the h hand-off), polled until
+ * each carries the tag (bounded: on a run-out nothing is selected and
+ * err |= 4), then the reference router's selection and weights
+ * (rt_router_core) into the slots: sel/wt in selection order, ord the
+ * ascending-id combine order. Workgroup 0 also writes the picks to
+ * idx_out / w_out when given. sc: LDS [E]. */
+template <int R>
+__device__ __forceinline__ void md_route_router(const uint64_t *lw, const float *__restrict__ bias,
+                                                uint32_t E, int topk, float scale,
+                                                uint32_t tag, float *sc, MdShared &sh,
+                                                uint32_t *__restrict__ err,
+                                                int32_t *__restrict__ idx_out,
+                                                float *__restrict__ w_out) {
+    const uint32_t lane = threadIdx.x & 63u;
+    uint64_t v[R];
+    float bv[R];
+#pragma unroll
+    for (int s = 0; s < R; s++) {
+        const uint32_t i = lane * R + s, ic = i < E ? i : E - 1u;
+        v[s] = __hip_atomic_load(lw + ic, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        bv[s] = bias[ic];
+    }
+    for (uint32_t it = 0;; it++) {
+        uint32_t miss = 0;
+#pragma unroll
+        for (int s = 0; s < R; s++)
+            miss |= (lane * R + s < E && (uint32_t)(v[s] >> 32) != tag) ? 1u << s : 0u;
+        if (!__builtin_amdgcn_readfirstlane((uint32_t)(__ballot(miss != 0u) != 0ull))) break;
+        if (it >= MD_SPIN_MAX) {
+            if (lane == 0) {
+                sh.nsel = 0;
+                atomicOr(err, 4u);
+            }
+            return;
+        }
+        __builtin_amdgcn_s_sleep(2);
+#pragma unroll
+        for (int s = 0; s < R; s++)
+            if ((miss >> s) & 1u)
+                v[s] = __hip_atomic_load(lw + lane * R + s, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+    }
+    float lv[R];
+#pragma unroll
+    for (int s = 0; s < R; s++) lv[s] = __uint_as_float((uint32_t)v[s]);
+    int myid;
+    float myw;
+    rt_router_core<R>(lv, bv, E, topk, scale, sc, nullptr, myid, myw);
+    const int id_or_max = (int)lane < topk ? myid : 0x7fffffff;
+    int rank = 0;
+    for (int j = 0; j < topk; j++) rank += __builtin_amdgcn_readlane(id_or_max, j) < id_or_max;
+    if ((int)lane < topk) {
+        sh.sel[lane] = myid;
+        sh.wt[lane] = myw;
+        sh.ord[rank] = lane;
+        if (idx_out && blockIdx.x == 0) {
+            idx_out[lane] = myid;
+            w_out[lane] = myw;
+        }
+    }
+    if (lane == 0) sh.nsel = (uint32_t)topk;
+}
+
+/* ------------------------------------------------------------------------ */
 /* the decode launch                                                        */
 /* ------------------------------------------------------------------------ */
 
@@ -688,11 +881,22 @@ __device__ __forceinline__ bool md_stage_h_wave(const uint32_t *src, uint32_t in
  * polls) flags err |= 4 and that wave skips its down rows (in every later
  * row group too) instead of hanging, so the launch always ends, and its
  * output is invalid whenever the word holds 4 afterwards. */
-template <bool SHARED>
+/* The reference router's inputs and outputs for the router-fed decode. */
+struct MdRouter {
+    const uint16_t *gate_w;      /* [E, dim] bf16 */
+    const float *bias;           /* [E] f32, selection only */
+    float scale;                 /* route_scale (routed_scaling_factor) */
+    uint64_t *lw;                /* [E] tagged logit words (workspace) */
+    int32_t *idx_out;            /* [topk] or NULL */
+    float *w_out;                /* [topk] or NULL */
+};
+
+template <bool SHARED, bool ROUTER>
 __global__ __launch_bounds__(MD_NW * 64, 1) void k_moe_decode(
     GhipBank bank, const uint16_t *__restrict__ x, const float *__restrict__ logits,
     const int32_t *__restrict__ idx, const float *__restrict__ w, int topk, float limit,
-    uint32_t *hw, uint32_t tag, uint32_t *__restrict__ err, uint16_t *__restrict__ out) {
+    uint32_t *hw, uint32_t tag, uint32_t *__restrict__ err, uint16_t *__restrict__ out,
+    MdRouter rtr) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t dl[];
     __shared__ MdShared sh;
     const uint32_t tid = threadIdx.x;
@@ -707,10 +911,31 @@ __global__ __launch_bounds__(MD_NW * 64, 1) void k_moe_decode(
          * the routing wave's piece does not cost a round trip after it */
         const uint32_t n16 = dim >> 3;
         const ghip_u32x4 x0 = ((const ghip_u32x4 *)x)[tid < n16 ? tid : n16 - 1];
-        if (wv == 0)
-            md_route_ids(logits, idx, w, topk, (int)bank.n_experts, sh,
-                         blockIdx.x == 0 ? err : nullptr);
-        else if (SHARED && blockIdx.x * 8u < inter)
+        if constexpr (ROUTER) {
+            /* the gate logits: wave v of workgroup b computes expert
+             * b + v * G's, published as a tagged word (c/gmoe.h:168-173) */
+            const uint32_t r = blockIdx.x + wv * gridDim.x;
+            if (r < bank.n_experts) {
+                const float acc = rt_gate_dot(rtr.gate_w + (size_t)r * dim, x, dim, tid & 63u);
+                if ((tid & 63u) == 0)
+                    __hip_atomic_store(rtr.lw + r, ((uint64_t)tag << 32) | __float_as_uint(acc),
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        if (wv == 0) {
+            if constexpr (ROUTER) {
+                float *rsc = (float *)gu_ring;            /* wave 0's area: idle in phase A */
+                if (bank.n_experts <= 5 * 64)
+                    md_route_router<5>(rtr.lw, rtr.bias, bank.n_experts, topk, rtr.scale, tag,
+                                       rsc, sh, err, rtr.idx_out, rtr.w_out);
+                else
+                    md_route_router<8>(rtr.lw, rtr.bias, bank.n_experts, topk, rtr.scale, tag,
+                                       rsc, sh, err, rtr.idx_out, rtr.w_out);
+            } else {
+                md_route_ids(logits, idx, w, topk, (int)bank.n_experts, sh,
+                             blockIdx.x == 0 ? err : nullptr);
+            }
+        } else if (SHARED && blockIdx.x * 8u < inter)
             /* the other waves stream the shared expert's gate/up rows of
              * this workgroup meanwhile (no routing needed) */
             md_shared_gateup(bank, x, gu_ring + wv * (GU_R * GU_STG), blockIdx.x, sh);
@@ -733,7 +958,7 @@ __global__ __launch_bounds__(MD_NW * 64, 1) void k_moe_decode(
     const uint32_t nsel = __builtin_amdgcn_readfirstlane(sh.nsel);
     uint16_t *hs = (uint16_t *)dl;
     uint8_t *ring = dl + (size_t)MD_NW * inter * 2u;
-    if (wv == 0 && logits) md_route_finish(sh, topk);
+    if (!ROUTER && wv == 0 && logits) md_route_finish(sh, topk);
     /* whether this wave's staged h is this launch's (false once a wait ran
      * out: the wave then computes no down rows at all, in this row group
      * or in a later one that reuses the staged h) */
@@ -790,116 +1015,6 @@ __global__ __launch_bounds__(MD_NW * 64, 1) void k_moe_decode(
         if (SHARED && nsel == 0) __syncthreads();  /* the shared partials are in */
         md_combine<SHARED>(sh, r0, out);
         __syncthreads();                          /* sh.oq is reused by the next rows */
-    }
-}
-
-/* ------------------------------------------------------------------------ */
-/* router with the reference semantics (c/gmoe.h:191-208)                   */
-/* ------------------------------------------------------------------------ */
-
-/* Gate logit of one row by one wave: sum_k w[k] * x[k] in f32, lane-strided
- * partial sums (lane l takes k = 8l + 512i, ascending i) and a fixed
- * xor-butterfly reduction: a GEMV of the same tolerance class as every
- * other one here (the reference's sequential-k dot is c/gmoe.h:168-173).
- * Eight row segments per lane are loaded before any is used, so a row
- * costs one memory round trip, not one per segment. dim % 8 == 0, 16-byte
- * aligned rows. */
-__device__ __forceinline__ float rt_gate_dot(const uint16_t *__restrict__ row,
-                                             const uint16_t *__restrict__ x, uint32_t dim,
-                                             uint32_t lane) {
-    float acc = 0.0f;
-    auto fma8 = [&](const ghip_u32x4 &wv, const ghip_u32x4 &xv) {
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            acc = acc + __uint_as_float(wv[q] << 16) * __uint_as_float(xv[q] << 16);
-            acc = acc + __uint_as_float(wv[q] & 0xffff0000u) *
-                            __uint_as_float(xv[q] & 0xffff0000u);
-        }
-    };
-    uint32_t k = lane * 8u;
-    for (; k + 7u * 512u < dim; k += 8u * 512u) {
-        ghip_u32x4 wv[8], xv[8];
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            wv[u] = *(const ghip_u32x4 *)(row + k + 512u * u);
-            xv[u] = *(const ghip_u32x4 *)(x + k + 512u * u);
-        }
-#pragma unroll
-        for (int u = 0; u < 8; u++) fma8(wv[u], xv[u]);
-    }
-    for (; k < dim; k += 512u)
-        fma8(*(const ghip_u32x4 *)(row + k), *(const ghip_u32x4 *)(x + k));
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) acc = acc + __shfl_xor(acc, off, 64);
-    return acc;
-}
-
-/* Selection and weights from the logits, one wave (c/gmoe.h:191-208):
- * scores = numpy-stable sigmoid (device expf), the stable top-k (larger
- * first, ties to the lower id) of score + bias -- the bias selects, it
- * never weighs -- then w_j = score[idx_j] / (pairwise_sum + 1e-20) *
- * route_scale, with numpy's float32 pairwise sum of the k selected scores
- * in selection order (c/gmhc.h:165-185). idx / w in selection order, as the
- * reference returns them. lg(i) loads logit i; sc is LDS [E]. */
-template <int R, typename Logit>
-__device__ __forceinline__ void rt_sigmoid_select(Logit lg, const float *__restrict__ bias,
-                                                  uint32_t E, int topk, float scale,
-                                                  float *sc, float *__restrict__ scores,
-                                                  int32_t *__restrict__ idx,
-                                                  float *__restrict__ w) {
-    const int lane = threadIdx.x & 63;
-    /* logits and biases of all R slots are loaded (clamped index, no
-     * predicated load) before any is used: one memory round trip */
-    float lv[R], bv[R];
-#pragma unroll
-    for (int s = 0; s < R; s++) {
-        const uint32_t i = (uint32_t)lane * R + s, ic = i < E ? i : E - 1u;
-        lv[s] = lg(ic);
-        bv[s] = bias[ic];
-    }
-#pragma unroll
-    for (int s = 0; s < R; s++) asm volatile("" ::"v"(lv[s]), "v"(bv[s]));
-    uint32_t key[R];
-#pragma unroll
-    for (int s = 0; s < R; s++) {
-        const uint32_t i = (uint32_t)lane * R + s;
-        key[s] = 0u;
-        if (i < E) {
-            const float v = ghip_sigmoid_np(lv[s]);
-            sc[i] = v;
-            if (scores) scores[i] = v;
-            key[s] = rt_key(v + bv[s]);
-        }
-    }
-    __builtin_amdgcn_s_waitcnt(0xc07f);           /* lgkmcnt(0) */
-    __builtin_amdgcn_wave_barrier();
-    uint32_t mk;
-    const int myid = rt_select<R>(key, topk, mk);
-    const float myw = lane < topk ? sc[myid] : 0.0f;
-    /* numpy float32 pairwise sum of the k selected scores (k <= 16) */
-    auto at = [&](int i) {
-        return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, myw), i));
-    };
-    float sum;
-    if (topk < 8) {
-        sum = at(0);
-        for (int i = 1; i < topk; i++) sum = sum + at(i);
-    } else {
-        float r[8];
-#pragma unroll
-        for (int q = 0; q < 8; q++) r[q] = at(q);
-        int i = 8;
-        if (topk >= 16) {
-#pragma unroll
-            for (int q = 0; q < 8; q++) r[q] = r[q] + at(8 + q);
-            i = 16;
-        }
-        sum = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
-        for (; i < topk; i++) sum = sum + at(i);
-    }
-    if (lane < topk) {
-        idx[lane] = myid;
-        w[lane] = myw / (sum + 1e-20f) * scale;
     }
 }
 
@@ -986,6 +1101,7 @@ extern "C" hipError_t ghip_launch_moe_decode(const GhipBank *bank,
                                              const uint16_t *x,
                                              const float *logits,
                                              const int32_t *idx, const float *w,
+                                             const GhipRouterArgs *router,
                                              int topk, float limit,
                                              uint16_t *out,
                                              GhipMoeDecodeWs *ws,
@@ -995,13 +1111,23 @@ extern "C" hipError_t ghip_launch_moe_decode(const GhipBank *bank,
     const uint32_t dim = bank->dim, inter = bank->inter;
     if (topk <= 0 || topk > MD_MAXK || (uint32_t)topk > bank->n_experts)
         return hipErrorInvalidValue;
-    if (!logits && (!idx || !w)) return hipErrorInvalidValue;
+    if (!router && !logits && (!idx || !w)) return hipErrorInvalidValue;
     if (dim == 0 || inter == 0 || dim % 128 || inter % 128) return hipErrorInvalidValue;
-    if (logits && bank->n_experts > RT_MAXE) return hipErrorInvalidValue;
+    if ((logits || router) && bank->n_experts > RT_MAXE) return hipErrorInvalidValue;
     if (((uintptr_t)x & 15) || ((uintptr_t)bank->base & 15) || (bank->stride & 15)
         || (bank->off_gw & 15) || (bank->off_uw & 15) || (bank->off_dw & 15)
         || (bank->off_gs & 3) || (bank->off_us & 3) || (bank->off_ds & 3))
         return hipErrorInvalidValue;
+    MdRouter rtr = {nullptr, nullptr, 0.0f, nullptr, nullptr, nullptr};
+    if (router) {
+        /* the gate rows go one to a wave, at most MD_NW per workgroup */
+        if (!router->gate_w || !router->bias || !ws->lw || ((uintptr_t)router->gate_w & 15)
+            || (size_t)bank->n_experts > (size_t)MD_NW * ws->n_cu
+            || (!router->idx_out) != (!router->w_out))
+            return hipErrorInvalidValue;
+        rtr = {router->gate_w, router->bias, router->route_scale, ws->lw, router->idx_out,
+               router->w_out};
+    }
     const bool shared = bank->has_shared != 0;
     const size_t lds_gu = (((size_t)dim * 2 + 1023) & ~(size_t)1023) + GU_NW * GU_R * GU_STG;
     /* down: the slots' h, the chunk rings and, with a shared expert, each
@@ -1019,31 +1145,44 @@ extern "C" hipError_t ghip_launch_moe_decode(const GhipBank *bank,
     if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
         return hipErrorStreamCaptureUnsupported;
     /* one workgroup per CU (the LDS use keeps it at one); the tag names
-     * this launch's h words: 1..65535, and when it wraps the words are
-     * cleared first (by a fill kernel, ordered on st), so a word left from
-     * 65535 launches ago cannot pass for this launch's */
+     * this launch's h and logit words: 1..65535, and when it wraps the
+     * words are cleared first (by fill kernels, ordered on st), so a word
+     * left from 65535 launches ago cannot pass for this launch's */
     hipError_t e;
     if (++ws->tag > 0xffffu) {
         if ((e = ghip_launch_fill_u32(ws->hw, (size_t)(MD_MAXK + 1) * inter, 0u, st))
             != hipSuccess)
             return e;
+        if (ws->lw && (e = ghip_launch_fill_u32((uint32_t *)ws->lw, 2 * (size_t)RT_MAXE, 0u,
+                                                st)) != hipSuccess)
+            return e;
         ws->tag = 1;
     }
-    if (shared)
-        GHIP_LAUNCH(ev ? ev[0] : nullptr, ev ? ev[1] : nullptr, k_moe_decode<true>,
-                    dim3(ws->n_cu), dim3(MD_NW * 64), lds, st, *bank, x, logits, idx, w,
-                    topk, limit, ws->hw, ws->tag, ws->err, out);
-    else
-        GHIP_LAUNCH(ev ? ev[0] : nullptr, ev ? ev[1] : nullptr, k_moe_decode<false>,
-                    dim3(ws->n_cu), dim3(MD_NW * 64), lds, st, *bank, x, logits, idx, w,
-                    topk, limit, ws->hw, ws->tag, ws->err, out);
+    hipEvent_t e0 = ev ? ev[0] : nullptr, e1 = ev ? ev[1] : nullptr;
+    const dim3 grid(ws->n_cu), blk(MD_NW * 64);
+#define MD_LAUNCH(S, R_)                                                               \
+    GHIP_LAUNCH(e0, e1, (k_moe_decode<S, R_>), grid, blk, lds, st, *bank, x, logits, idx, \
+                w, topk, limit, ws->hw, ws->tag, ws->err, out, rtr)
+    if (shared) {
+        if (router) MD_LAUNCH(true, true);
+        else MD_LAUNCH(true, false);
+    } else {
+        if (router) MD_LAUNCH(false, true);
+        else MD_LAUNCH(false, false);
+    }
+#undef MD_LAUNCH
     return hipGetLastError();
 }
 
 extern "C" hipError_t ghip_moe_decode_init(void) {
-    hipError_t e = hipFuncSetAttribute((const void *)k_moe_decode<false>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, MD_LDS_MAX);
-    if (e != hipSuccess) return e;
-    return hipFuncSetAttribute((const void *)k_moe_decode<true>,
-                               hipFuncAttributeMaxDynamicSharedMemorySize, MD_LDS_MAX);
+    const void *k[4] = {(const void *)k_moe_decode<false, false>,
+                        (const void *)k_moe_decode<false, true>,
+                        (const void *)k_moe_decode<true, false>,
+                        (const void *)k_moe_decode<true, true>};
+    for (int i = 0; i < 4; i++) {
+        hipError_t e = hipFuncSetAttribute(k[i], hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           MD_LDS_MAX);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }

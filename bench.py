@@ -736,38 +736,56 @@ def cpu_bf16_gemv(lib, M=1, budget_s=10.0):
 ROUTE_SCALE = 2.5      # routed_scaling_factor of the reference's model config
 
 
+def router_inputs(lib, E, dim, seed):
+    """gate_w [E, dim] bf16 ~ N(0, 1/dim) (N(0, 1) scaled by 2^-6, exact in
+    bf16) and bias [E] ~ 0.05 N(0, 1). With N(0, 1) weights the logits
+    against an N(0, 1) x have std 64, the sigmoid saturates at 1.0 for ~40%
+    of the experts, and the selection-only bias then picks nearly the same
+    experts every token (30 distinct over 64 tokens), served from the MALL
+    instead of HBM; trained routers' logits are O(1)."""
+    gwh = np.empty(E * dim, np.uint16)
+    lib.apus_synth_bf16_normal(gwh.ctypes.data_as(ctypes.c_void_p), gwh.size, seed, 40, 0)
+    gwf = (gwh.astype(np.uint32) << 16).view(np.float32) * np.float32(1.0 / 64.0)
+    gw = (gwf.view(np.uint32) >> 16).astype(np.uint16).reshape(E, dim)
+    bias = np.empty(E, np.float32)
+    lib.apus_synth_f32_normal(bias.ctypes.data_as(ctypes.c_void_p), E, seed, 41, 0)
+    return gw, (bias * np.float32(0.05)).astype(np.float32)
+
+
 def bench_moe_decode_router(lib, pkg, rt, steps, warmup, rotate=64):
-    """One step = apus_ghip_moe_router_dev (gate GEMV over gate_w [288, 4096]
-    BF16, sigmoid, stable top-8 of score + bias, pairwise normalization x 2.5,
-    c/gmoe.h:191-208) feeding apus_ghip_moe_decode_dev with the selected
-    ids/weights, both on one stream with no host round trip. Bytes = 8 expert
-    slabs + x + out + gate_w + bias."""
+    """One step = the engine's decode step with the reference router
+    (sigmoid, stable top-8 of score + bias, pairwise normalization x 2.5,
+    c/gmoe.h:191-208) in ONE launch, apus_ghip_moe_decode_router_dev: the
+    gate GEMV over gate_w [288, 4096] BF16, the selection, the 8 experts and
+    the combine. The two-launch form (apus_ghip_moe_router_dev, then
+    apus_ghip_moe_decode_dev with its picks, on one stream) is timed beside
+    it. Bytes = 8 expert slabs + x + out + gate_w + bias."""
     E, k, dim, inter, seed = (MOE[x] for x in ("E", "k", "dim", "inter", "seed"))
     store = ctypes.c_void_p()
     err = ctypes.create_string_buffer(256)
     pkg.check(lib.apus_ghip_store_open(ctypes.byref(store), E, dim, inter,
                                        MOE["limit"], err, 256), "store_open")
     pkg.check(lib.apus_ghip_store_synth(store, seed, 0, 1e-4, 1e-2), "store_synth")
-    # gate_w ~ N(0, 1/dim) (N(0, 1) scaled by 2^-6, exact in bf16), so the
-    # logits against an N(0, 1) x are O(1) as a trained router's are: with
-    # N(0, 1) weights the logits have std 64, the sigmoid saturates at 1.0
-    # for ~40% of the experts, the selection-only bias then picks nearly the
-    # same experts every token (30 distinct over 64 tokens) and their slabs
-    # come from the MALL instead of HBM
-    gwh = np.empty(E * dim, np.uint16)
-    lib.apus_synth_bf16_normal(gwh.ctypes.data_as(ctypes.c_void_p), gwh.size, seed, 40, 0)
-    gwf = (gwh.astype(np.uint32) << 16).view(np.float32) * np.float32(1.0 / 64.0)
-    gw = rt.DevBuf.of((gwf.view(np.uint32) >> 16).astype(np.uint16))
-    bias = np.empty(E, np.float32)
-    lib.apus_synth_f32_normal(bias.ctypes.data_as(ctypes.c_void_p), E, seed, 41, 0)
-    d_bias = rt.DevBuf.of((bias * np.float32(0.05)).astype(np.float32))
+    gwh, bias = router_inputs(lib, E, dim, seed)
+    gw = rt.DevBuf.of(gwh)
+    d_bias = rt.DevBuf.of(bias)
     xs = np.empty((rotate, dim), np.uint16)
     lib.apus_synth_bf16_normal(xs.ctypes.data_as(ctypes.c_void_p), xs.size, seed, 31, 0)
     d_x = rt.DevBuf.of(xs)
     d_out = rt.DevBuf(rotate * dim * 2)
+    d_out2 = rt.DevBuf(rotate * dim * 2)
     d_idx = rt.DevBuf(64 * 4)
     d_w = rt.DevBuf(64 * 4)
     st = rt.Stream()
+
+    def fused(i):
+        j = i % rotate
+        rc = lib.apus_ghip_moe_decode_router_dev(
+            store, ctypes.c_void_p(d_x.ptr + j * dim * 2), gw.vp, d_bias.vp,
+            ctypes.c_float(ROUTE_SCALE), k, ctypes.c_void_p(d_out.ptr + j * dim * 2),
+            None, None, st.vp)
+        if rc:
+            pkg.check(rc, "moe_decode_router_dev")
 
     def router(i):
         j = i % rotate
@@ -782,63 +800,59 @@ def bench_moe_decode_router(lib, pkg, rt, steps, warmup, rotate=64):
         j = i % rotate
         rc = lib.apus_ghip_moe_decode_dev(store, ctypes.c_void_p(d_x.ptr + j * dim * 2),
                                           None, d_idx.vp, d_w.vp, k,
-                                          ctypes.c_void_p(d_out.ptr + j * dim * 2), st.vp)
+                                          ctypes.c_void_p(d_out2.ptr + j * dim * 2), st.vp)
         if rc:
             pkg.check(rc, "moe_decode_dev")
 
-    for i in range(warmup):
-        router(i)
-        decode(i)
     def both(i):
         router(i)
         decode(i)
 
-    ms = timed(rt, st, both, warmup, steps)
-    # per-launch times: the router and the decode launch, each with its own
-    # events
-    n = steps
-    evs = [[rt.Event() for _ in range(4)] for _ in range(n)]
-    arr2 = ctypes.c_void_p * 2
-    for i in range(n):
-        lib.apus_ghip_set_trace_events(arr2(*[e.handle for e in evs[i][:2]]), 2)
-        router(warmup + steps + i)
-        lib.apus_ghip_set_trace_events(arr2(*[e.handle for e in evs[i][2:]]), 2)
-        decode(warmup + steps + i)
-    lib.apus_ghip_set_trace_events(None, 0)
-    rt.synchronize()
-    t_router = sum(e[0].elapsed_ms(e[1]) for e in evs) / n
-    t_dec = sum(e[2].elapsed_ms(e[3]) for e in evs) / n
+    for i in range(warmup):
+        fused(i)
+    ms = timed(rt, st, fused, warmup, steps)
+    kt = kernel_times(lib, rt, fused, warmup + steps, steps, 2, {"k_moe_decode": (0, 1)})
+    for i in range(warmup):
+        both(i)
+    ms2 = timed(rt, st, both, warmup, steps)
     errors = store_errors(lib, store)
+    out0 = d_out.download(np.uint16, (rotate, dim))[0]
+    same = bool(np.array_equal(d_out.download(np.uint16, (rotate, dim)),
+                               d_out2.download(np.uint16, (rotate, dim))))
     lib.apus_ghip_store_close(store)
     full, _, _ = moe_algorithmic_bytes(E, k, dim, inter)
     nbytes = full - E * 4 + E * dim * 2 + E * 4         # gate_w + bias, no logits
     return {
         "ms_per_step": ms, "value": nbytes / (ms * 1e-3) / 1e9, "_device_errors": errors,
+        "_gpu_out": out0, "one_launch_per_step": True,
         "weight_bytes": k * 3 * inter * dim + E * dim * 2,
         "bytes": nbytes, "flops": 2 * k * 3 * inter * dim + 2 * E * dim,
-        "kernel": "k_moe_decode", "kernel_ms": t_dec, "kernel_bytes": full - E * 4,
-        "kernel_flops": 2 * k * 3 * inter * dim, "traffic_key": "k_moe_decode@given_routing",
-        "launch_ms": {"k_router": round(t_router, 5), "k_moe_decode": round(t_dec, 5)},
+        "kernel": "k_moe_decode", "kernel_ms": kt["k_moe_decode"], "kernel_bytes": nbytes,
+        "kernel_flops": 2 * k * 3 * inter * dim + 2 * E * dim,
+        "traffic_key": "k_moe_decode@router",
+        "launch_ms": {n_: round(v, 5) for n_, v in kt.items()},
+        "two_launch": {"ms_per_step": round(ms2, 6),
+                       "value": round(nbytes / (ms2 * 1e-3) / 1e9, 2),
+                       "outputs_bitwise_equal_to_one_launch": same},
         "config": {"workload": "moe_decode_router (BASELINE config 2 shapes, routed by "
-                               "the reference router c/gmoe.h:191-208)",
-                   "experts": E, "topk": k, "dim": dim, "inter": inter,
-                   "route_scale": ROUTE_SCALE, "rotated_tokens": rotate,
-                   "weights": "fp8-e4m3 128x128 blocks; gate_w bf16"},
+                               "the reference router in the same launch)", "experts": E,
+                   "topk": k, "dim": dim, "inter": inter, "tokens": 1,
+                   "rotated_tokens": rotate, "route_scale": ROUTE_SCALE,
+                   "weights": "fp8-e4m3 128x128 blocks",
+                   "routing": "sigmoid + selection-only bias, pairwise-sum x 2.5"},
     }
 
 
 def cpu_moe_decode_router(lib, budget_s=3.0):
-    """The reference router (apus_gmoe_router, c/gmoe.h:191-208) on this host,
-    added to the config-2 expert sample of cpu_moe_decode."""
+    """The reference router (apus_gmoe_router, c/gmoe.h:191-208) on this
+    host, timed and added to the config-2 expert sample of cpu_moe_decode;
+    and, untimed, the reference output of the bench's token 0 (its router
+    picks, those experts on BF16 payloads, the combine) for the check."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
     P = O.ptr
     E, k, dim, inter, seed = (MOE[x] for x in ("E", "k", "dim", "inter", "seed"))
-    gw = np.empty((E, dim), np.uint16)
-    lib.apus_synth_bf16_normal(P(gw), gw.size, seed, 40, 0)
-    bias = np.empty(E, np.float32)
-    lib.apus_synth_f32_normal(P(bias), E, seed, 41, 0)
-    bias = (bias * np.float32(0.05)).astype(np.float32)
+    gw, bias = router_inputs(lib, E, dim, seed)
     x = np.empty(dim, np.uint16)
     lib.apus_synth_bf16_normal(P(x), dim, seed, 31, 0)
     sc, idx, w = (np.empty(E, np.float32), np.empty(k, np.int32), np.empty(k, np.float32))
@@ -850,17 +864,41 @@ def cpu_moe_decode_router(lib, budget_s=3.0):
             O.ref().ref_gmoe_router(P(gw), P(bias), E, dim, k, ROUTE_SCALE, P(x), P(sc),
                                     P(idx), P(w))
         else:
-            O.gmoe_router(gw, bias, x, k, ROUTE_SCALE)
+            sc, idx, w = O.gmoe_router(gw, bias, x, k, ROUTE_SCALE)
         t += time.perf_counter() - t0
         n += 1
     experts = cpu_moe_decode(lib)
     per_tok = experts["ms_per_token"] * 1e-3 + t / n
     nbytes = moe_algorithmic_bytes(E, k, dim, inter)[0] - E * 4 + E * dim * 2 + E * 4
+    # the check's reference: token 0 through the router's picks
+    y = np.zeros(dim, np.float32)
+    floor = np.zeros(dim)
+    eo = np.empty(dim, np.uint16)
+    for e, wt in sorted(zip(idx.tolist(), w.tolist())):
+        mats = []
+        for j, (o, kk) in enumerate([(inter, dim), (inter, dim), (dim, inter)]):
+            c = np.empty((o, kk), np.uint8)
+            lib.apus_synth_fp8_codes(P(c), c.size, seed,
+                                     lib.apus_synth_expert_stream(0, e, 2 * j), 0)
+            s_ = np.empty((O.nblocks(o), O.nblocks(kk)), np.float32)
+            lib.apus_synth_scales(P(s_), s_.size, seed,
+                                  lib.apus_synth_expert_stream(0, e, 2 * j + 1), 1e-4, 1e-2)
+            mats.append(O.dequant(c, s_, threads=CPU_THREADS))
+        if use_ref:
+            O.ref().ref_gmoe_expert(P(mats[0]), P(mats[1]), P(mats[2]), P(x), dim, inter,
+                                    MOE["limit"], P(eo))
+        else:
+            eo[:] = O.swiglu_expert(*mats, x, threads=CPU_THREADS)[0]
+        c_ = O.bf16_to_f32(O.f32_to_bf16(O.bf16_to_f32(eo) * np.float32(wt)))
+        y = O.bf16_to_f32(O.f32_to_bf16(y + c_))
+        floor += np.abs(c_.astype(np.float64))
     experts.update({
         "value": nbytes / per_tok / 1e9,
         "sample": experts["sample"] + "; router %d calls, %.3f ms/call, added"
                   % (n, t / n * 1e3),
-        "router_ms": t / n * 1e3})
+        "router_ms": t / n * 1e3,
+        "_ref_out": {"out": O.f32_to_bf16(y), "floor": floor,
+                     "what": "token 0: the reference router's picks, experts, combine"}})
     return experts
 
 
@@ -1448,6 +1486,8 @@ def line_of(metric, r, cpu, steps, warmup):
         "cpu_baseline": public(cpu),
         "verified": verify(r, cpu),
     }
+    if "two_launch" in r:
+        line["two_launch"] = r["two_launch"]
     if "hbm_gbs" in r:
         line["hbm"] = {"achieved": round(r["hbm_gbs"], 2), "peak": HBM_PEAK_GBS,
                        "unit": "GB/s", "frac": round(r["hbm_gbs"] / HBM_PEAK_GBS, 4),
@@ -1552,11 +1592,13 @@ def main():
     if args.workload == "moe_decode" and not args.no_dense:
         # the decode as the model runs it: the layer's shared expert added
         # after the routed sum (c/gmoe.h:325-336), one launch
+        # and routed by the reference router in the same launch
         line["decode_variants"] = []
-        m2, r2, c2 = run_workload("moe_decode_shared", lib, pkg, rt, args, cpu is not None)
-        line["decode_variants"].append(line_of(m2, r2, c2, args.steps, args.warmup))
-        print("bench: moe_decode_shared done (%.4f ms/step)" % r2["ms_per_step"],
-              file=sys.stderr, flush=True)
+        for name in ("moe_decode_shared", "moe_decode_router"):
+            m2, r2, c2 = run_workload(name, lib, pkg, rt, args, cpu is not None)
+            line["decode_variants"].append(line_of(m2, r2, c2, args.steps, args.warmup))
+            print("bench: %s done (%.4f ms/step)" % (name, r2["ms_per_step"]),
+                  file=sys.stderr, flush=True)
     if args.workload == "moe_decode" and not args.no_prefill:
         # the metric's second half ("...; prefill grouped-GEMM
         # TFLOP/s (%MFMA)"): configs 4 and 3, each a full step of its own

@@ -256,6 +256,27 @@ int apus_ghip_moe_decode_dev(ApusGhipStore *s, const uint16_t *x,
                              const float *w, int topk, uint16_t *out,
                              void *stream);
 
+/* --- the engine's decode step in one launch: the reference router
+ * (apus_gmoe_router, c/gmoe.h:191-208: gate logits gate_w [E, dim] bf16 .
+ * x in f32, numpy-stable sigmoid scores, stable top-k of score + gate_bias
+ * -- the bias selects, it never weighs -- and w = the selected scores over
+ * their numpy pairwise sum + 1e-20, times route_scale) feeding the routed
+ * experts and the ascending-expert combine (c/gmoe.h:294-320), and the
+ * shared expert when the store holds one (c/gmoe.h:325-336). Replaces
+ * apus_ghip_moe_router_dev followed by apus_ghip_moe_decode_dev (the same
+ * logits, picks, weights and outputs, bitwise) with one launch: the
+ * workgroups compute the gate logits, hand them over as words tagged with
+ * the launch, and each selects for itself. idx_out / w_out (device [topk],
+ * both or neither): the picks in selection order. E <= 512 and E <= 8 x the
+ * device's CUs; 16-byte aligned x and gate_w. Stream-ordered, the same
+ * no-overlap and no-capture rules as apus_ghip_moe_decode_dev; device-side
+ * failures go to apus_ghip_store_status. No counterpart in the Metal
+ * backend. */
+int apus_ghip_moe_decode_router_dev(ApusGhipStore *s, const uint16_t *x,
+                                    const uint16_t *gate_w, const float *gate_bias,
+                                    float route_scale, int topk, uint16_t *out,
+                                    int32_t *idx_out, float *w_out, void *stream);
+
 /* --- routed MoE prefill (T tokens): the reference runs, per token, the
  * selected experts and the ordered combine (c/gmoe.h:278-320, expert body
  * c/gmoe.h:210-227); here the same result is computed as grouped GEMMs over

@@ -143,3 +143,98 @@ def test_router_drives_decode(ghip):
         assert_close_combined(got, want[0], fl, "router -> decode")
     finally:
         ghip.apus_ghip_store_close(s)
+
+
+def fused_case(ghip, E, dim, inter, topk, gw, bias, x, shared=None, seed=0):
+    """The router-fed decode (one launch) against the two-launch form
+    (router, then the decode with its picks) on the same store and inputs:
+    the same picks and weights and the same outputs, bitwise; and against
+    the oracle's router + experts (+ shared expert) + combine."""
+    from test_gpu_moe import open_store, random_slabs
+    from test_gpu_shared import floor_all
+    rng = np.random.default_rng(seed)
+    slabs = random_slabs(E, dim, inter, rng)
+    s = open_store(ghip, E, dim, inter)
+    try:
+        for e, sl in enumerate(slabs):
+            assert ghip.apus_ghip_store_put(s, e, O.ptr(sl), sl.nbytes) == 0
+        if shared is not None:
+            assert ghip.apus_ghip_store_put_shared(s, O.ptr(shared), shared.nbytes) == 0
+        dgw, db, dx = G.dev(gw), G.dev(bias), G.dev(x)
+        di, dw, do1 = G.empty(topk * 4), G.empty(topk * 4), G.empty(dim * 2)
+        fi, fw, do2 = G.empty(topk * 4), G.empty(topk * 4), G.empty(dim * 2)
+        assert ghip.apus_ghip_moe_router_dev(G.vp(dx), G.vp(dgw), None, G.vp(db), E, dim,
+                                             topk, 2.5, None, G.vp(di), G.vp(dw),
+                                             G.stream()) == 0
+        assert ghip.apus_ghip_moe_decode_dev(s, G.vp(dx), None, G.vp(di), G.vp(dw), topk,
+                                             G.vp(do1), G.stream()) == 0
+        assert ghip.apus_ghip_moe_decode_router_dev(s, G.vp(dx), G.vp(dgw), G.vp(db), 2.5,
+                                                    topk, G.vp(do2), G.vp(fi), G.vp(fw),
+                                                    G.stream()) == 0, \
+            ghip.apus_ghip_last_error()
+        two = (G.host(di, np.int32, (topk,)), G.host(dw, np.float32, (topk,)),
+               G.host(do1, np.uint16, (dim,)))
+        one = (G.host(fi, np.int32, (topk,)), G.host(fw, np.float32, (topk,)),
+               G.host(do2, np.uint16, (dim,)))
+        for a, b, what in zip(two, one, ("idx", "w", "out")):
+            assert np.array_equal(a, b), "fused vs two launches: " + what
+        code = ctypes.c_uint32(1)
+        assert ghip.apus_ghip_store_status(s, None, 1, ctypes.byref(code)) == 0
+        assert code.value == 0
+        sc, idx, w = O.gmoe_router(gw, bias, x, topk)
+        want = O.moe_forward(slabs, dim, inter, x, idx[None], w[None], threads=8,
+                             shared=shared)
+        fl = floor_all(slabs, shared, dim, inter, x, idx[None], w[None])[0]
+        return one, idx, w, want[0], fl
+    finally:
+        ghip.apus_ghip_store_close(s)
+
+
+@pytest.mark.parametrize("E,dim,inter,topk", [(288, 4096, 256, 8), (64, 256, 128, 4),
+                                              (300, 512, 128, 16), (16, 128, 128, 1),
+                                              (512, 1024, 128, 9)])
+def test_router_fused_decode(ghip, E, dim, inter, topk):
+    gw, bias, x = inputs(E * 5 + dim + topk, E, dim)
+    (gidx, gwt, out), idx, w, want, fl = fused_case(ghip, E, dim, inter, topk, gw, bias, x,
+                                                    seed=E + topk)
+    b = np.sort(O.gmoe_router(gw, bias, x, topk)[0] + bias)[::-1]
+    if b[topk - 1] - b[topk] > 1e-5:                 # no near-tie at this spacing
+        assert np.array_equal(gidx, idx)
+        assert np.allclose(gwt, w, rtol=1e-5, atol=0)
+        assert_close_combined(out, want, fl, "fused router decode E=%d" % E)
+
+
+def test_router_fused_ties_and_bias(ghip):
+    """Through the one-launch path: equal gate rows (equal logits and biases)
+    resolve to the lower id, in the reference's order; a bias that selects
+    experts 100..107 selects them but does not weigh them."""
+    E, dim, inter, topk = 128, 256, 128, 6
+    gw, bias, x = inputs(31, E, dim, ties=True)
+    gw[[2, 7, 33]] = O.f32_to_bf16(np.full(dim, 0.5, np.float32) * np.sign(
+        O.bf16_to_f32(x)))                            # the three tied rows lead
+    (gidx, gwt, out), idx, w, want, fl = fused_case(ghip, E, dim, inter, topk, gw, bias, x)
+    assert list(gidx[:3]) == [2, 7, 33]
+    assert np.array_equal(gidx, idx)
+    assert np.allclose(gwt, w, rtol=1e-5, atol=0)
+    assert_close_combined(out, want, fl, "ties")
+    gw, bias, x = inputs(32, E, dim)
+    bias[:] = 0.0
+    bias[100:108] = 10.0
+    (gidx, gwt, out), idx, w, want, fl = fused_case(ghip, E, dim, inter, 8, gw, bias, x)
+    assert sorted(gidx.tolist()) == list(range(100, 108))
+    sc = O.gmoe_router(gw, bias, x, 8)[0]
+    assert np.allclose(gwt, sc[gidx] / sc[gidx].sum() * 2.5, rtol=2e-6)
+    assert_close_combined(out, want, fl, "bias selects")
+
+
+def test_router_fused_decode_with_shared_expert(ghip):
+    """The whole MoE sublayer of c/gmoe.h:265-337 in one launch: router,
+    routed experts, shared expert."""
+    from test_gpu_moe import random_slabs
+    E, dim, inter, topk = 64, 512, 256, 8
+    gw, bias, x = inputs(77, E, dim)
+    shared = random_slabs(1, dim, inter, np.random.default_rng(78))[0]
+    (gidx, gwt, out), idx, w, want, fl = fused_case(ghip, E, dim, inter, topk, gw, bias, x,
+                                                    shared=shared, seed=79)
+    assert np.array_equal(gidx, idx)
+    assert_close_combined(out, want, fl, "router + routed + shared, one launch")
