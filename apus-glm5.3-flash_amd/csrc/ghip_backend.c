@@ -589,7 +589,8 @@ int apus_ghip_store_open(ApusGhipStore **out, int n_experts, size_t dim,
     int bad = hipMalloc((void **)&s->nan_flags, ((size_t)n_experts + 1) * 4) != hipSuccess
            || hipMemset(s->nan_flags, 0, ((size_t)n_experts + 1) * 4) != hipSuccess
            || hipMalloc((void **)&s->ws.hw, GHIP_HW_SLOTS * inter * 4) != hipSuccess
-           || hipMemset(s->ws.hw, 0, GHIP_HW_SLOTS * inter * 4) != hipSuccess
+           /* both h buffers start as the sentinel (every byte 0xff) */
+           || hipMemset(s->ws.hw, 0xff, GHIP_HW_SLOTS * inter * 4) != hipSuccess
            || (s->ws.hw_inter = (uint32_t)inter) == 0
            || hipMalloc((void **)&s->ws.err, 4) != hipSuccess
            || hipMemset(s->ws.err, 0, 4) != hipSuccess

@@ -42,17 +42,21 @@ hipError_t ghip_launch_bf16_linear(const uint16_t *w, const uint16_t *x,
                                    const hipEvent_t *ev, hipStream_t st);
 
 /* K3 MoE decode workspace: the SwiGLU activations h handed from the
- * gate/up phase to the down phase as tagged words (bf16 value in bits
- * 0..15, the writing launch's tag in 16..31; zero-filled at creation), an
- * error word, and the host's current tag. */
+ * gate/up phase to the down phase as words of two bf16 values (the even
+ * row in bits 0..15), in two buffers that alternate between launches: the
+ * one a launch writes holds only the sentinel 0xffffffff when it starts,
+ * and it refills the other (both filled at creation); an error word, the
+ * host's current tag (the router's logit words) and buffer parity. */
 typedef struct {
-    uint32_t *hw;         /* device [17 slots, hw_inter] u32: 16 routed + the shared expert */
+    uint32_t *hw;         /* device [2][17 slots][hw_inter / 2] u32: 16 routed + the shared
+                             expert, per buffer */
     uint32_t hw_inter;    /* inter the words were sized for */
     uint32_t *err;        /* device u32: 2 = invalid expert id, 4 = hand-off wait ran out */
     uint64_t *lw;         /* device [512] u64: the router-fed decode's tagged gate logits
                              (the launch's tag in bits 32..47, the f32 logit in 0..31) */
     uint32_t n_cu;        /* grid: one workgroup per CU */
     uint32_t tag;         /* host: the last launch's tag (0 before the first) */
+    uint32_t hpar;        /* host: the h buffer the next launch writes (0 or 1) */
 } GhipMoeDecodeWs;
 
 /* The reference router's inputs for the router-fed decode (c/gmoe.h:191-208):

@@ -17,11 +17,14 @@
  *            combine y = bf16(y + bf16(bf16(o)*w)) (c/gmoe.h:307-320) runs
  *            in-workgroup -- no float atomics, no cross-workgroup reduction,
  *            deterministic.
- * Hand-off of h between the phases: every h value is stored as one 32-bit
- * word carrying the value and this launch's tag, with a device-coherent
- * store; a reader polls the words with device-coherent loads until each
- * carries the tag (bounded). No fence, counter or kernel boundary is
- * involved, and a reader needs nothing but the words it reads.
+ * Hand-off of h between the phases: two h values per 32-bit word, stored
+ * with a device-coherent store into a buffer that holds only the sentinel
+ * MD_HSENT until this launch writes it (two buffers alternate between
+ * launches; each launch refills the other one, which the launch before it
+ * read and the launch after it writes); a reader polls the words with
+ * device-coherent loads until none is the sentinel (bounded). No fence,
+ * counter or barrier between workgroups is involved, and a reader needs
+ * nothing but the words it reads.
  *
  * Weight streaming: waves pull their 16-row chunks (128-wide k, one scale
  * block) through registers (whole-line 16-byte loads), write each to a
@@ -40,6 +43,18 @@
 #define MD_MAXK 16               /* max routed slots */
 #define MD_LDS_MAX (144 * 1024)  /* dynamic LDS limit of the decode kernel */
 #define MD_SPIN_MAX (1u << 18)   /* bounded wait for the device-wide hand-off */
+#define MD_HSENT 0xffffffffu     /* an h word not written yet in this launch */
+
+/* Two h values (bf16 bits, lo = the even row) as one hand-off word. The
+ * sentinel would be a pair of all-ones NaNs (a NaN whose 32-bit source has
+ * every mantissa bit set, as the bf16 narrowing keeps NaN payloads): that
+ * pair is stored with the even row's NaN payload one lower (0xfffe), still
+ * a NaN of the same sign, so every word a launch stores differs from the
+ * sentinel. */
+__device__ __forceinline__ uint32_t md_hpack(uint32_t lo, uint32_t hi) {
+    const uint32_t wd = lo | (hi << 16);
+    return wd == MD_HSENT ? wd - 1u : wd;
+}
 
 /* ------------------------------------------------------------------------ */
 /* routing                                                                  */
@@ -262,11 +277,12 @@ __device__ __forceinline__ void md_route_finish(MdShared &sh, int topk) {
  * SwiGLU; workgroup b takes item groups b, b + G, ... of GU_IPW items; wave
  * w streams item (w / 2)'s half (w % 2) of K through registers and a
  * wave-private pair of LDS slots (no barriers inside the stream); the
- * halves are summed in LDS in a fixed order (deterministic). The 16 h values of an item go to hw[q] in
- * HBM as tagged words (lanes 0..15 of the item's even wave). */
+ * halves are summed in LDS in a fixed order (deterministic). The 16 h
+ * values of an item go to hw[q] in HBM as 8 hand-off words (lanes 0..7 of
+ * the item's even wave, two rows each). */
 __device__ __forceinline__ void md_phase_gateup(const GhipBank &bank, const uint16_t *xs,
                                                 uint8_t *ring_base, MdShared &sh,
-                                                float limit, uint32_t *hw, uint32_t tag) {
+                                                float limit, uint32_t *hw) {
     const uint32_t dim = bank.dim, inter = bank.inter;
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -345,15 +361,20 @@ __device__ __forceinline__ void md_phase_gateup(const GhipBank &bank, const uint
             }
         }
         __syncthreads();
-        if (live && half == 0 && lane < 16) {     /* fixed order: half 0 + half 1 */
-            const float gs = sh.red[slot][0][0][lane] + sh.red[slot][1][0][lane];
-            const float us = sh.red[slot][0][1][lane] + sh.red[slot][1][1][lane];
-            const uint32_t hv = ghip_swiglu(ghip_bf16_round(gs), ghip_bf16_round(us), limit);
-            /* the value and this launch's tag in one word, stored
-             * device-coherently: the word itself tells a reader on any XCD
-             * that it is this launch's value */
-            __hip_atomic_store(hw + (size_t)q * inter + r0 + lane, (tag << 16) | hv,
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (live && half == 0 && lane < 8) {      /* fixed order: half 0 + half 1 */
+            uint32_t hv[2];
+#pragma unroll
+            for (uint32_t k = 0; k < 2; k++) {
+                const uint32_t r = 2u * lane + k;
+                const float gs = sh.red[slot][0][0][r] + sh.red[slot][1][0][r];
+                const float us = sh.red[slot][0][1][r] + sh.red[slot][1][1][r];
+                hv[k] = ghip_swiglu(ghip_bf16_round(gs), ghip_bf16_round(us), limit);
+            }
+            /* rows 2j and 2j + 1 in one word, stored device-coherently: a
+             * word that is not the sentinel is this launch's, on any XCD */
+            __hip_atomic_store(hw + (size_t)q * (inter / 2u) + r0 / 2u + lane,
+                               md_hpack(hv[0], hv[1]), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
         }
         __syncthreads();
     }
@@ -437,22 +458,28 @@ __device__ __forceinline__ void md_shared_gateup(const GhipBank &bank,
 }
 
 /* After the routing barrier: the shared expert's 8 h values of rows 8hb..
- * (lane j < 8 of the calling wave): the partial sums of waves 1..7 in that
- * order, the reference's bf16 roundings and SwiGLU, stored as tagged words
- * (as the routed slots' h) in slot MD_SH_SLOT. */
+ * (lane j < 4 of the calling wave: rows 8hb + 2j and 8hb + 2j + 1): the
+ * partial sums of waves 1..7 in that order, the reference's bf16 roundings
+ * and SwiGLU, stored as hand-off words (as the routed slots' h) in slot
+ * MD_SH_SLOT. */
 __device__ __forceinline__ void md_shared_h(const MdShared &sh, uint32_t hb, uint32_t inter,
-                                            float limit, uint32_t *hw, uint32_t tag) {
+                                            float limit, uint32_t *hw) {
     const uint32_t lane = threadIdx.x & 63u;
-    if (lane < 8u) {
-        float gs = sh.sred[1][lane], us = sh.sred[1][8u + lane];
+    if (lane < 4u) {
+        uint32_t hv[2];
 #pragma unroll
-        for (uint32_t w = 2; w < MD_NW; w++) {
-            gs = gs + sh.sred[w][lane];
-            us = us + sh.sred[w][8u + lane];
+        for (uint32_t k = 0; k < 2; k++) {
+            const uint32_t r = 2u * lane + k;
+            float gs = sh.sred[1][r], us = sh.sred[1][8u + r];
+#pragma unroll
+            for (uint32_t w = 2; w < MD_NW; w++) {
+                gs = gs + sh.sred[w][r];
+                us = us + sh.sred[w][8u + r];
+            }
+            hv[k] = ghip_swiglu(ghip_bf16_round(gs), ghip_bf16_round(us), limit);
         }
-        const uint32_t hv = ghip_swiglu(ghip_bf16_round(gs), ghip_bf16_round(us), limit);
-        __hip_atomic_store(hw + (size_t)MD_SH_SLOT * inter + hb * 8u + lane, (tag << 16) | hv,
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(hw + (size_t)MD_SH_SLOT * (inter / 2u) + hb * 4u + lane,
+                           md_hpack(hv[0], hv[1]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -626,34 +653,34 @@ __device__ __forceinline__ void md_combine(const MdShared &sh, uint32_t r0,
     }
 }
 
-/* inter h values into LDS (hs [inter] bf16) by the calling wave alone, from
- * the tagged words at src (one slot's words, or a range of them; value in
- * bits 0..15, the writing launch's tag in 16..31): the lanes load their
- * words with device-coherent loads and
- * re-poll the ones that do not carry this launch's tag yet (their gate/up
- * item is still running on another CU), at most MD_SPIN_MAX rounds.
- * Returns false (the same in every lane) when a word is still missing
- * then. No workgroup barrier: each wave goes on to its own slot's rows as
- * soon as that slot's h is in. */
-__device__ __forceinline__ bool md_stage_h_wave(const uint32_t *src, uint32_t inter,
-                                                uint32_t tag, uint16_t *hs) {
+/* nw hand-off words (2 nw h values) into LDS (hs32 [nw] words, the bf16
+ * pairs as stored) by the calling wave alone, from the words at src (one
+ * slot's words, or a range of them): the lanes load their words with
+ * device-coherent loads and re-poll the ones that still hold the sentinel
+ * (their gate/up item is still running on another CU), at most MD_SPIN_MAX
+ * rounds. Returns false (the same in every lane) when a word is still
+ * missing then. No workgroup barrier: each wave goes on to its own slot's
+ * rows as soon as that slot's h is in. */
+__device__ __forceinline__ bool md_stage_h_wave(const uint32_t *src, uint32_t nw,
+                                                uint32_t *hs32) {
     constexpr uint32_t PER = 16;
     const uint32_t lane = threadIdx.x & 63u;
-    for (uint32_t i0 = 0; i0 < inter; i0 += 64u * PER) {
+    for (uint32_t i0 = 0; i0 < nw; i0 += 64u * PER) {
         uint32_t v[PER];
 #pragma unroll
         for (uint32_t u = 0; u < PER; u++) {
             const uint32_t i = i0 + u * 64u + lane;
-            v[u] = __hip_atomic_load(src + (i < inter ? i : inter - 1u), __ATOMIC_RELAXED,
+            v[u] = __hip_atomic_load(src + (i < nw ? i : nw - 1u), __ATOMIC_RELAXED,
                                      __HIP_MEMORY_SCOPE_AGENT);
         }
-        /* the wave polls until all its words carry the tag (uniform exit) */
+        /* the wave polls until none of its words is the sentinel (uniform
+         * exit) */
         for (uint32_t it = 0;; it++) {
             uint32_t miss = 0;
 #pragma unroll
             for (uint32_t u = 0; u < PER; u++) {
                 const uint32_t i = i0 + u * 64u + lane;
-                miss |= (i < inter && (v[u] >> 16) != tag) ? 1u << u : 0u;
+                miss |= (i < nw && v[u] == MD_HSENT) ? 1u << u : 0u;
             }
             if (!__builtin_amdgcn_readfirstlane((uint32_t)(__ballot(miss != 0u) != 0ull)))
                 break;
@@ -668,7 +695,7 @@ __device__ __forceinline__ bool md_stage_h_wave(const uint32_t *src, uint32_t in
 #pragma unroll
         for (uint32_t u = 0; u < PER; u++) {
             const uint32_t i = i0 + u * 64u + lane;
-            if (i < inter) hs[i] = (uint16_t)v[u];
+            if (i < nw) hs32[i] = v[u];
         }
     }
     return true;
@@ -871,10 +898,14 @@ __device__ __forceinline__ void md_route_router(const uint64_t *lw, const float 
 /* the decode launch                                                        */
 /* ------------------------------------------------------------------------ */
 
-/* One launch of gridDim.x workgroups (one per CU), 8 waves each. hw: the
- * tagged h words ([max topk][inter] u32), tag: this launch's tag (1..65535;
- * the host clears hw whenever the tag wraps, so no stale word carries a
- * live tag). The hand-off needs every workgroup resident at once: the grid
+/* One launch of gridDim.x workgroups (one per CU), 8 waves each. hw: this
+ * launch's h words ([max topk + 1][inter / 2] u32, two bf16 per word), all
+ * MD_HSENT when the launch starts; hw_clr: the other buffer (clr_words
+ * words), which the launch refills with MD_HSENT for the next one (the
+ * launch before this one read it, and stream order has it done). tag:
+ * this launch's tag for the router's logit words (1..65535; the host
+ * clears those whenever the tag wraps, so no stale word carries a live
+ * tag). The hand-off needs every workgroup resident at once: the grid
  * is one workgroup per CU, which an otherwise idle device always holds.
  * When other work holds CUs, a workgroup may wait for a slot while the
  * resident ones wait for its h: a wait for h that runs out (MD_SPIN_MAX
@@ -895,8 +926,8 @@ template <bool SHARED, bool ROUTER>
 __global__ __launch_bounds__(MD_NW * 64, 1) void k_moe_decode(
     GhipBank bank, const uint16_t *__restrict__ x, const float *__restrict__ logits,
     const int32_t *__restrict__ idx, const float *__restrict__ w, int topk, float limit,
-    uint32_t *hw, uint32_t tag, uint32_t *__restrict__ err, uint16_t *__restrict__ out,
-    MdRouter rtr) {
+    uint32_t *hw, uint32_t *hw_clr, uint32_t clr_words, uint32_t tag,
+    uint32_t *__restrict__ err, uint16_t *__restrict__ out, MdRouter rtr) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t dl[];
     __shared__ MdShared sh;
     const uint32_t tid = threadIdx.x;
@@ -948,11 +979,18 @@ __global__ __launch_bounds__(MD_NW * 64, 1) void k_moe_decode(
         GHIP_VMCNT(0);
         __syncthreads();
         if (SHARED && wv == 1 && blockIdx.x * 8u < inter)
-            md_shared_h(sh, blockIdx.x, inter, limit, hw, tag);
+            md_shared_h(sh, blockIdx.x, inter, limit, hw);
     }
 
-    /* --- phase B: gate/up + SwiGLU -> tagged h words ------------------- */
-    md_phase_gateup(bank, xs, gu_ring, sh, limit, hw, tag);
+    /* the other h buffer back to the sentinel for the next launch (at most
+     * one word per thread at the model's shapes; its store latency joins
+     * the first gate/up stage's wait) */
+    for (uint32_t i = blockIdx.x * (MD_NW * 64u) + tid; i < clr_words;
+         i += gridDim.x * (MD_NW * 64u))
+        __hip_atomic_store(hw_clr + i, MD_HSENT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+    /* --- phase B: gate/up + SwiGLU -> h hand-off words ------------------ */
+    md_phase_gateup(bank, xs, gu_ring, sh, limit, hw);
 
     /* --- phase C: down + combine per 16 output rows -------------------- */
     const uint32_t nsel = __builtin_amdgcn_readfirstlane(sh.nsel);
@@ -975,8 +1013,8 @@ __global__ __launch_bounds__(MD_NW * 64, 1) void k_moe_decode(
             /* the shared expert's down rows over this wave's share of
              * inter, while the routed slots' h is still on its way */
             if (rg == blockIdx.x && sc1 > sc0)
-                hss_ok = md_stage_h_wave(hw + (size_t)MD_SH_SLOT * inter + sc0 * 128u,
-                                         (sc1 - sc0) * 128u, tag, hss);
+                hss_ok = md_stage_h_wave(hw + (size_t)MD_SH_SLOT * (inter / 2u) + sc0 * 64u,
+                                         (sc1 - sc0) * 64u, (uint32_t *)hss);
             ghip_f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
             if (hss_ok && sc1 > sc0) {
                 const uint32_t nkb = inter >> 7;
@@ -1001,8 +1039,8 @@ __global__ __launch_bounds__(MD_NW * 64, 1) void k_moe_decode(
              * pass), then at once its down rows; a wave whose wait runs
              * out flags the error and computes nothing */
             if (base + wv < nsel && (base > 0 || rg == blockIdx.x || nsel > MD_NW))
-                hs_ok = md_stage_h_wave(hw + (size_t)(base + wv) * inter, inter, tag,
-                                        hs + (size_t)wv * inter);
+                hs_ok = md_stage_h_wave(hw + (size_t)(base + wv) * (inter / 2u), inter / 2u,
+                                        (uint32_t *)(hs + (size_t)wv * inter));
             const bool ok = hs_ok;
             if (ok) {
                 md_phase_down(bank, sh, r0, base, hs, ring, hd);
@@ -1139,30 +1177,32 @@ extern "C" hipError_t ghip_launch_moe_decode(const GhipBank *bank,
         return hipErrorInvalidValue;
     /* the shared expert's gate/up rows go 8 to a workgroup, in one pass */
     if (shared && (size_t)inter > (size_t)ws->n_cu * 8) return hipErrorInvalidValue;
-    /* the tag is host state advanced per call, so a launch recorded into a
-     * graph would replay with a stale tag: refuse to be captured */
+    /* the tag and the h buffer parity are host state advanced per call, so
+     * a launch recorded into a graph would replay with stale ones: refuse
+     * to be captured */
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
         return hipErrorStreamCaptureUnsupported;
     /* one workgroup per CU (the LDS use keeps it at one); the tag names
-     * this launch's h and logit words: 1..65535, and when it wraps the
-     * words are cleared first (by fill kernels, ordered on st), so a word
-     * left from 65535 launches ago cannot pass for this launch's */
+     * this launch's logit words: 1..65535, and when it wraps the words are
+     * cleared first (by a fill kernel, ordered on st), so a word left from
+     * 65535 launches ago cannot pass for this launch's. The h words need
+     * no tag: the launch writes buffer ws->hpar, which holds only the
+     * sentinel, and refills the other one. */
     hipError_t e;
     if (++ws->tag > 0xffffu) {
-        if ((e = ghip_launch_fill_u32(ws->hw, (size_t)(MD_MAXK + 1) * inter, 0u, st))
-            != hipSuccess)
-            return e;
         if (ws->lw && (e = ghip_launch_fill_u32((uint32_t *)ws->lw, 2 * (size_t)RT_MAXE, 0u,
                                                 st)) != hipSuccess)
             return e;
         ws->tag = 1;
     }
+    const size_t hbuf = (size_t)(MD_MAXK + 1) * (ws->hw_inter / 2u);
+    uint32_t *hcur = ws->hw + (ws->hpar ? hbuf : 0), *hclr = ws->hw + (ws->hpar ? 0 : hbuf);
     hipEvent_t e0 = ev ? ev[0] : nullptr, e1 = ev ? ev[1] : nullptr;
     const dim3 grid(ws->n_cu), blk(MD_NW * 64);
 #define MD_LAUNCH(S, R_)                                                               \
     GHIP_LAUNCH(e0, e1, (k_moe_decode<S, R_>), grid, blk, lds, st, *bank, x, logits, idx, \
-                w, topk, limit, ws->hw, ws->tag, ws->err, out, rtr)
+                w, topk, limit, hcur, hclr, (uint32_t)hbuf, ws->tag, ws->err, out, rtr)
     if (shared) {
         if (router) MD_LAUNCH(true, true);
         else MD_LAUNCH(true, false);
@@ -1171,7 +1211,10 @@ extern "C" hipError_t ghip_launch_moe_decode(const GhipBank *bank,
         else MD_LAUNCH(false, false);
     }
 #undef MD_LAUNCH
-    return hipGetLastError();
+    /* the next launch writes the buffer this one refills (only once this
+     * one is enqueued: a launch that never ran refilled nothing) */
+    if ((e = hipGetLastError()) == hipSuccess) ws->hpar ^= 1u;
+    return e;
 }
 
 extern "C" hipError_t ghip_moe_decode_init(void) {

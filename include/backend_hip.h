@@ -240,14 +240,16 @@ int apus_ghip_moe_router_dev(const uint16_t *x, const uint16_t *gate_w,
  * c/gmoe.h:210-227 + 307-320 (+ 325-336 when the store holds a shared
  * expert, apus_ghip_store_put_shared), without the router. One
  * persistent launch (one workgroup per CU, all resident at once): routing,
- * gate/up GEMVs with the SwiGLU epilogue (activations to HBM as words
- * tagged with the launch), then down GEMVs, each wave starting as soon as
- * its expert's activations carry the tag, and the ascending-expert
- * bf16-per-add combine. Calls that share a store must not overlap in time
- * (one stream). Each call advances a host-side tag that names its
- * activations, so the device variant cannot be captured into a graph (a
- * replay would reuse the recorded tag): it returns 1 on a capturing
- * stream and launches nothing.
+ * gate/up GEMVs with the SwiGLU epilogue (activations to HBM, two per word,
+ * into a buffer that holds only a sentinel until the launch writes it),
+ * then down GEMVs, each wave starting as soon as its expert's activations
+ * are all in, and the ascending-expert bf16-per-add combine. Calls that
+ * share a store must not overlap in time (one stream). Each call flips a
+ * host-side parity that picks which of two activation buffers it writes
+ * (it refills the other for the next call) and advances a host-side tag,
+ * so the device variant cannot be captured into a graph (a replay would
+ * reuse the recorded buffer): it returns 1 on a capturing stream and
+ * launches nothing.
  * Routing either given (idx/w [topk]) or computed on the device from
  * logits [n_experts] f32: stable top-k (ties -> lower id), w = softmax over
  * the k selected logits. Host-pointer variant is synchronous. */

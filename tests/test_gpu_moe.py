@@ -296,10 +296,11 @@ def test_config2_golden(ghip, pkg):
 
 
 def test_moe_decode_tag_wrap(ghip):
-    """The hand-off tag is 16 bits: launch 65536 on a workspace clears the h
-    words (a fill kernel ordered on the stream) and restarts at tag 1. Calls
-    on both sides of the wrap, enqueued back to back after 65,527 others,
-    give the outputs the same inputs gave on the fresh workspace, bitwise."""
+    """The launch tag is 16 bits: launch 65536 on a workspace clears the
+    router's logit words (a fill kernel ordered on the stream) and restarts
+    at tag 1, while the h buffers keep alternating. Calls on both sides of
+    the wrap, enqueued back to back after 65,527 others, give the outputs
+    the same inputs gave on the fresh workspace, bitwise."""
     E, dim, inter = 16, 256, 128
     rng = np.random.default_rng(65536)
     slabs = random_slabs(E, dim, inter, rng)
@@ -340,10 +341,11 @@ def test_moe_decode_tag_wrap(ghip):
 
 
 def test_moe_decode_refuses_graph_capture(small):
-    """The decode's hand-off tag is host state advanced per call, so a
-    launch recorded into a HIP graph would replay with a stale tag: the
-    device entry refuses a capturing stream (returns 1, launches nothing),
-    the capture ends cleanly, and calls afterwards are unaffected."""
+    """Which h buffer a decode call writes is host state flipped per call
+    (with the launch tag), so a launch recorded into a HIP graph would
+    replay into a stale buffer: the device entry refuses a capturing stream
+    (returns 1, launches nothing), the capture ends cleanly, and calls
+    afterwards are unaffected."""
     ghip, s, slabs, (E, dim, inter) = small
     rt = G.rt()
     rng = np.random.default_rng(404)
@@ -372,9 +374,10 @@ def test_moe_decode_refuses_graph_capture(small):
 
 def test_moe_decode_back_to_back_calls(small):
     """Decode calls enqueued back to back on one stream, no host sync in
-    between: every h word a launch writes carries that launch's tag, so a
-    launch never takes an earlier launch's h for its own, and every output
-    equals the same call run alone, bitwise."""
+    between: a launch writes h into the buffer the launch before it refilled
+    with the sentinel (the two buffers alternate), so a launch never takes
+    an earlier launch's h for its own, and every output equals the same
+    call run alone, bitwise."""
     ghip, s, slabs, (E, dim, inter) = small
     rng = np.random.default_rng(21)
     calls = []
