@@ -401,6 +401,36 @@ def test_moe_decode_back_to_back_calls(small):
     assert status(ghip, s) == 0
 
 
+def test_moe_decode_all_ones_nan_activations(small):
+    """An h pair of two all-ones NaNs (0xffff, 0xffff) would read as the
+    hand-off's "not written yet" sentinel; the decode stores such a pair
+    with the even row's NaN payload one lower. A token whose activations
+    are all that NaN (whether its h pairs collide depends on the NaN
+    payload the device arithmetic carries) must still end promptly: no
+    hand-off error, every output NaN like the oracle's, and the next call
+    on the same store within the tolerance of the oracle."""
+    ghip, s, slabs, (E, dim, inter) = small
+    x = np.full(dim, 0xFFFF, np.uint16)
+    idx = np.array([0, 5, 9, 12], np.int32)
+    w = np.array([0.4, 0.3, 0.2, 0.1], np.float32)
+    out = np.empty(dim, np.uint16)
+    assert ghip.apus_ghip_moe_decode(s, O.ptr(x), O.ptr(idx), O.ptr(w), len(idx),
+                                     O.ptr(out)) == 0, ghip.apus_ghip_last_error()
+    assert status(ghip, s) == 0
+    want = O.moe_forward(slabs, dim, inter, x, idx[None], w[None])[0]
+    nan = lambda b: ((b & 0x7F80) == 0x7F80) & ((b & 0x7F) != 0)
+    assert nan(want).all()
+    assert nan(out).all()
+    rng = np.random.default_rng(77)
+    x2 = O.f32_to_bf16(rng.standard_normal(dim).astype(np.float32))
+    after = np.empty(dim, np.uint16)
+    assert ghip.apus_ghip_moe_decode(s, O.ptr(x2), O.ptr(idx), O.ptr(w), len(idx),
+                                     O.ptr(after)) == 0, ghip.apus_ghip_last_error()
+    want2, eo = O.moe_forward(slabs, dim, inter, x2, idx[None], w[None], want_expert_out=True)
+    assert_close_combined(after, want2[0], moe_floor(eo, w[None], idx[None])[0],
+                          "the call after the NaN token")
+
+
 def status(ghip, s, clear=1, stream=None):
     code = ctypes.c_uint32(0xFFFFFFFF)
     assert ghip.apus_ghip_store_status(s, stream, clear, ctypes.byref(code)) == 0, \
