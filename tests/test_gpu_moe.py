@@ -401,6 +401,37 @@ def test_moe_decode_back_to_back_calls(small):
     assert status(ghip, s) == 0
 
 
+def test_moe_decode_refused_calls_between_launches(small):
+    """Calls the entry refuses (topk 0 or past 16) launch nothing and leave
+    the workspace's h-buffer parity where it was: valid calls enqueued back
+    to back with refused ones between them give the outputs they give run
+    alone, bitwise, and no device failure is recorded."""
+    ghip, s, slabs, (E, dim, inter) = small
+    rng = np.random.default_rng(33)
+    calls = []
+    for k in (8, 5, 8, 2):
+        x = O.f32_to_bf16(rng.standard_normal(dim).astype(np.float32))
+        idx = rng.choice(E, k, replace=False).astype(np.int32)
+        w = rng.uniform(0.05, 0.5, k).astype(np.float32)
+        calls.append((x, idx, w))
+    alone = []
+    for x, idx, w in calls:
+        out = np.empty(dim, np.uint16)
+        assert ghip.apus_ghip_moe_decode(s, O.ptr(x), O.ptr(idx), O.ptr(w), len(idx),
+                                         O.ptr(out)) == 0
+        alone.append(out)
+    bufs = [(G.dev(x), G.dev(idx), G.dev(w), G.empty(dim * 2), len(idx)) for x, idx, w in calls]
+    for dx, di, dw, do, k in bufs:
+        assert ghip.apus_ghip_moe_decode_dev(s, G.vp(dx), None, G.vp(di), G.vp(dw), k,
+                                             G.vp(do), G.stream()) == 0
+        for bad in (0, 17):
+            assert ghip.apus_ghip_moe_decode_dev(s, G.vp(dx), None, G.vp(di), G.vp(dw), bad,
+                                                 G.vp(do), G.stream()) != 0
+    for (dx, di, dw, do, k), want in zip(bufs, alone):
+        assert np.array_equal(G.host(do, np.uint16, (dim,)), want), "k=%d" % k
+    assert status(ghip, s) == 0
+
+
 def test_moe_decode_all_ones_nan_activations(small):
     """An h pair of two all-ones NaNs (0xffff, 0xffff) would read as the
     hand-off's "not written yet" sentinel; the decode stores such a pair
