@@ -83,6 +83,44 @@ def test_decode_shared_vs_oracle(ghip, dim, inter, k, nan_shared):
         ghip.apus_ghip_store_close(s)
 
 
+def test_decode_shared_back_to_back(ghip):
+    """Shared-expert decodes enqueued back to back on one stream, the
+    routed slot count changing from call to call (more than 8 slots in one
+    of them): the shared expert's h words sit beside the routed slots' in
+    the two alternating h buffers, and every output equals the same call
+    run alone, bitwise, with no device failure recorded."""
+    E, dim, inter = 16, 256, 128
+    s, slabs, shared, rng = make_store(ghip, E, dim, inter, 505)
+    try:
+        calls = []
+        for k in (8, 2, 12, 1, 8):
+            x = O.f32_to_bf16(rng.standard_normal(dim).astype(np.float32))
+            idx = rng.permutation(E)[:k].astype(np.int32)
+            w = rng.uniform(0.05, 0.6, k).astype(np.float32)
+            calls.append((x, idx, w))
+        alone = []
+        for x, idx, w in calls:
+            out = np.empty(dim, np.uint16)
+            assert ghip.apus_ghip_moe_decode(s, O.ptr(x), O.ptr(idx), O.ptr(w), len(idx),
+                                             O.ptr(out)) == 0, ghip.apus_ghip_last_error()
+            alone.append(out)
+        bufs = [(G.dev(x), G.dev(idx), G.dev(w), G.empty(dim * 2), len(idx))
+                for x, idx, w in calls]
+        for dx, di, dw, do, k in bufs:
+            assert ghip.apus_ghip_moe_decode_dev(s, G.vp(dx), None, G.vp(di), G.vp(dw), k,
+                                                 G.vp(do), G.stream()) == 0
+        for (dx, di, dw, do, k), want in zip(bufs, alone):
+            assert np.array_equal(G.host(do, np.uint16, (dim,)), want), "k=%d" % k
+        assert status(ghip, s) == 0
+        x, idx, w = calls[2]
+        want = want_of(slabs, shared, dim, inter, x, idx[None], w[None])
+        assert_close_combined(alone[2], want[0], floor_all(slabs, shared, dim, inter, x,
+                                                           idx[None], w[None])[0],
+                              "shared, 12 slots")
+    finally:
+        ghip.apus_ghip_store_close(s)
+
+
 def test_decode_shared_device_routing_and_dropped_ids(ghip):
     """Device routing from logits with the shared expert; and a call whose
     every routed id is outside the bank: the routed sum is empty (+0), the
