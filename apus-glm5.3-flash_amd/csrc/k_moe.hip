@@ -107,9 +107,11 @@ __device__ __forceinline__ uint32_t rt_wave_max(uint32_t k) {
  * DPP wave max of the lanes' heads; of the lanes whose head equals it the
  * lowest one holds the lowest index with that key (its head is its lowest
  * such index, and lower lanes hold lower indices), and it drops its head.
- * Lane j < k returns pick j's index and its key in mykey. */
-template <int R>
-__device__ __forceinline__ int rt_select(uint32_t (&key)[R], int topk, uint32_t &mykey) {
+ * Lane j < k returns pick j's index and its key in mykey. KC > 0: the
+ * count is KC at compile time (topk == KC), so the rounds unroll and one
+ * round's remaining register moves overlap the next round's wave max. */
+template <int R, int KC = 0>
+__device__ __forceinline__ int rt_select_n(uint32_t (&key)[R], int topk, uint32_t &mykey) {
     const uint32_t lane = threadIdx.x & 63u;
     uint32_t ss[R];
 #pragma unroll
@@ -127,7 +129,9 @@ __device__ __forceinline__ int rt_select(uint32_t (&key)[R], int topk, uint32_t 
         }
     int myid = -1;
     mykey = 0u;
-    for (int j = 0; j < topk; j++) {
+    const int nk = KC > 0 ? KC : topk;
+#pragma unroll
+    for (int j = 0; j < nk; j++) {
         const uint32_t wm = rt_wave_max(key[0]);
         const uint32_t wl = (uint32_t)__builtin_ctzll(__ballot(key[0] == wm));
         const uint32_t widx = wl * (uint32_t)R + (uint32_t)__builtin_amdgcn_readlane((int)ss[0], wl);
@@ -145,6 +149,12 @@ __device__ __forceinline__ int rt_select(uint32_t (&key)[R], int topk, uint32_t 
         }
     }
     return myid;
+}
+
+/* rt_select_n with the model's top-8 unrolled */
+template <int R>
+__device__ __forceinline__ int rt_select(uint32_t (&key)[R], int topk, uint32_t &mykey) {
+    return topk == 8 ? rt_select_n<R, 8>(key, 8, mykey) : rt_select_n<R>(key, topk, mykey);
 }
 
 /* Selection of the harness routing from logits by one wave: the stable
