@@ -240,6 +240,15 @@ __device__ __forceinline__ float pf_bf16_round(float x) {
     return __uint_as_float((uint32_t)pf_bf16_bits(x) << 16);
 }
 
+/* pf_bf16_round of two values with one packed convert */
+__device__ __forceinline__ float2 pf_bf16_round2(float a, float b) {
+    typedef __bf16 pf_bf2 __attribute__((ext_vector_type(2)));
+    typedef float pf_f2 __attribute__((ext_vector_type(2)));
+    const pf_bf2 h = __builtin_convertvector((pf_f2){a, b}, pf_bf2);
+    const uint32_t u = __builtin_bit_cast(uint32_t, h);
+    return make_float2(__uint_as_float(u << 16), __uint_as_float(u & 0xffff0000u));
+}
+
 /* SwiGLU of the fp32 gate / up accumulators: each rounded to bf16 first,
  * then the clamps (compares, so a NaN stays NaN as in the reference) */
 __device__ __forceinline__ uint16_t pf_swiglu(float accg, float accu, float limit) {
@@ -1039,19 +1048,39 @@ __global__ __launch_bounds__(256) void k_pf_combine(
 #pragma unroll
     for (int q = 0; q < 8; q++) y[q] = 0.0f;
     for (uint32_t r0 = 0; r0 < n; r0 += 8) {
+        /* the rows and weights of up to 8 pairs first (one LDS wait), then
+         * all their loads (rows past n re-read the last one, unused) */
+        int32_t rr[8];
+        float wr[8];
+#pragma unroll
+        for (int r = 0; r < 8; r++) {
+            const uint32_t i = min(r0 + (uint32_t)r, n - 1u);
+            rr[r] = srow[i];
+            wr[r] = sw[i];
+        }
         ghip_u32x4 v[8];
 #pragma unroll
-        for (int r = 0; r < 8; r++)
-            if (r0 + r < n) v[r] = *(const ghip_u32x4 *)(O + (size_t)srow[r0 + r] * dim + d);
+        for (int r = 0; r < 8; r++) v[r] = *(const ghip_u32x4 *)(O + (size_t)rr[r] * dim + d);
+        /* an unconditional use of each row pins its load here, so all are
+         * in flight at once (the compiler would otherwise sink each load
+         * behind the exit test before its row's arithmetic) */
+#pragma unroll
+        for (int r = 0; r < 8; r++) asm volatile("" ::"v"(v[r]));
 #pragma unroll
         for (int r = 0; r < 8; r++) {
             if (r0 + r >= n) break;
-            const float wr = sw[r0 + r];
 #pragma unroll
-            for (int q = 0; q < 8; q++) {
-                const uint32_t bits = (v[r][q >> 1] >> (16 * (q & 1))) & 0xffffu;
-                const float cq = ghip_bf16_round(ghip_bf16_f32(bits) * wr);
-                y[q] = ghip_bf16_round(y[q] + cq);
+            for (int q = 0; q < 8; q += 2) {
+                /* two elements a step: bf16 -> f32, the weight, the RNE
+                 * narrows of the product and of the sum on the packed
+                 * hardware convert (the reference's bits for every finite
+                 * value, c/gmoe.h:307-320) */
+                const uint32_t pr = v[r][q >> 1];
+                float2 c = pf_bf16_round2(__uint_as_float(pr << 16) * wr[r],
+                                          __uint_as_float(pr & 0xffff0000u) * wr[r]);
+                float2 s2 = pf_bf16_round2(y[q] + c.x, y[q + 1] + c.y);
+                y[q] = s2.x;
+                y[q + 1] = s2.y;
             }
         }
     }
