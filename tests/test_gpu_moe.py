@@ -198,12 +198,14 @@ def test_moe_decode_vs_oracle(small, k):
         assert np.array_equal(out, out2), "run-to-run determinism"
 
 
-@pytest.mark.parametrize("dim,inter,k", [(256, 128, 12), (4352, 128, 4), (4352, 256, 11)])
+@pytest.mark.parametrize("dim,inter,k", [(256, 128, 12), (4352, 128, 4), (4352, 256, 11),
+                                         (256, 384, 8), (512, 640, 5)])
 def test_moe_decode_multipass(ghip, dim, inter, k):
     """The decode's second passes: more than 8 slots (the down phase takes
     the slots 8 at a time per workgroup) and more 16-row output groups than
     workgroups (a workgroup takes a second row group, reusing its staged
-    h), against the oracle and run to run."""
+    h), and intermediate sizes of an odd count of 128-blocks (the h
+    hand-off words hold row pairs), against the oracle and run to run."""
     E = 16
     rng = np.random.default_rng(dim + k)
     slabs = random_slabs(E, dim, inter, rng, nan_codes_in=(5,))

@@ -44,7 +44,8 @@ def make_store(ghip, E, dim, inter, seed, nan_shared=False):
 @pytest.mark.parametrize("dim,inter,k,nan_shared", [(256, 128, 1, False), (256, 128, 8, True),
                                                     (256, 128, 12, False),
                                                     (4352, 128, 4, False),
-                                                    (4352, 256, 11, True)])
+                                                    (4352, 256, 11, True),
+                                                    (256, 384, 8, False)])
 def test_decode_shared_vs_oracle(ghip, dim, inter, k, nan_shared):
     """One token, given routing, shared expert: k = 1 and 8, more than 8
     slots (two down passes), more output row groups than workgroups, and a
