@@ -634,6 +634,53 @@ __device__ __forceinline__ void md_phase_down(const GhipBank &bank, MdShared &sh
     }
 }
 
+/* bf16 rounding on the hardware RNE narrow (v_cvt_pk_bf16_f32): the bits
+ * of ghip_bf16_round for every finite value, subnormals included, and a
+ * quiet NaN for a NaN (the NaNs the combine sees come from the device's
+ * own arithmetic, quiet already) */
+__device__ __forceinline__ float md_bf16_rnd(float x) {
+    return __uint_as_float((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x) << 16);
+}
+__device__ __forceinline__ float2 md_bf16_rnd2(float a, float b) {
+    typedef __bf16 md_bf2 __attribute__((ext_vector_type(2)));
+    typedef float md_f2 __attribute__((ext_vector_type(2)));
+    const uint32_t u = __builtin_bit_cast(uint32_t,
+                                          __builtin_convertvector((md_f2){a, b}, md_bf2));
+    return make_float2(__uint_as_float(u << 16), __uint_as_float(u & 0xffff0000u));
+}
+
+/* y over the first nsel (<= KC) slots in combine order: every slot's order
+ * word, output and weight is read before the sum (two LDS round trips; the
+ * order words past nsel are masked into range and their terms left out),
+ * the products bf16(bf16(o) * w) are independent, and only the running sum
+ * is a chain */
+template <int KC>
+__device__ __forceinline__ float md_combine_sum(const MdShared &sh, uint32_t nsel,
+                                                uint32_t tid) {
+    uint32_t q[KC];
+#pragma unroll
+    for (int i = 0; i < KC; i++) q[i] = sh.ord[i] & (MD_MAXK - 1u);
+    float o[KC], wq[KC];
+#pragma unroll
+    for (int i = 0; i < KC; i++) {
+        o[i] = sh.oq[q[i]][tid];
+        wq[i] = sh.wt[q[i]];
+    }
+    float c[KC];
+#pragma unroll
+    for (int i = 0; i < KC; i += 2) {
+        const float2 eo = md_bf16_rnd2(o[i], o[i + 1]);
+        const float2 cc = md_bf16_rnd2(eo.x * wq[i], eo.y * wq[i + 1]);
+        c[i] = cc.x;
+        c[i + 1] = cc.y;
+    }
+    float y = 0.0f;
+#pragma unroll
+    for (int i = 0; i < KC; i++)
+        if ((uint32_t)i < nsel) y = md_bf16_rnd(y + c[i]);
+    return y;
+}
+
 /* the ascending-expert combine of the nsel expert outputs in sh.oq: y =
  * bf16(y + bf16(bf16(o) * w)), from +0 (c/gmoe.h:307-320). Call after a
  * barrier. */
@@ -642,14 +689,9 @@ __device__ __forceinline__ void md_combine(const MdShared &sh, uint32_t r0,
                                            uint16_t *__restrict__ out) {
     const uint32_t tid = threadIdx.x;
     if (tid < 16) {
-        const uint32_t nsel = sh.nsel;
-        float y = 0.0f;
-        for (uint32_t i = 0; i < nsel; i++) {
-            const uint32_t q = sh.ord[i];
-            float eo = ghip_bf16_round(sh.oq[q][tid]);
-            float c = ghip_bf16_round(eo * sh.wt[q]);
-            y = ghip_bf16_round(y + c);
-        }
+        const uint32_t nsel = __builtin_amdgcn_readfirstlane(sh.nsel);
+        float y = nsel <= 8u ? md_combine_sum<8>(sh, nsel, tid)
+                             : md_combine_sum<MD_MAXK>(sh, nsel, tid);
         if constexpr (SHARED) {
             /* the shared expert's output (its waves' partials in wave
              * order, one bf16 rounding), added last with one more rounding
