@@ -7,8 +7,8 @@
  *            none waits for another): the harness routing (stable top-k of
  *            f32 logits, ties -> lower id) or given idx/w, a repeated id
  *            keeping its first slot (c/gmoe.h:309-312). Only the selected
- *            ids are needed to start streaming; the softmax weights and the
- *            ascending-id combine order are computed later.
+ *            ids are needed to start streaming; the softmax weights (kept
+ *            at their ascending-id combine positions) are computed later.
  *   gate/up  per (slot q, 16 rows) the g and u GEMVs over dim with the FP8
  *            dequant fused (bit-exact weights) and the SwiGLU epilogue of
  *            c/gmoe.h:217-225 -> h[q] in HBM.
@@ -195,12 +195,11 @@ __device__ __forceinline__ int md_select(const float *__restrict__ logits, int t
 
 /* Per-workgroup shared state (static LDS). Slots: the kept routing picks
  * in selection order (logits) or given order (idx); sel[q] is slot q's
- * expert, wt[q] its weight, ord[i] the slot of the i-th smallest expert id
- * (the combine order). */
+ * expert. Combine positions: position i is the i-th smallest kept expert
+ * id; wt[i] is its weight and oq[i] its output rows. */
 struct MdShared {
     int32_t sel[MD_MAXK];
     float wt[MD_MAXK];
-    uint32_t ord[MD_MAXK];
     float lg[MD_MAXK];           /* logits path: slot q's logit */
     int32_t te[MD_MAXK];
     float tw[MD_MAXK];
@@ -218,9 +217,9 @@ struct MdShared {
 
 /* Phase A, wave 0 only: the routing picks into sh.sel / sh.nsel. Given
  * idx/w: a repeated id keeps its first slot (c/gmoe.h:309-312), invalid ids
- * are dropped and flagged; kept slots stay in the given order, with their
- * weights and the ascending-id order. Logits: the selected ids and their
- * logits (weights and order come later, md_route_finish). */
+ * are dropped and flagged; kept slots stay in the given order, their
+ * weights at their ascending-id combine positions. Logits: the selected ids
+ * and their logits (the weights come later, md_route_finish). */
 __device__ __forceinline__ void md_route_ids(const float *__restrict__ logits,
                                              const int32_t *__restrict__ idx,
                                              const float *__restrict__ w, int topk, int E,
@@ -255,15 +254,15 @@ __device__ __forceinline__ void md_route_ids(const float *__restrict__ logits,
         rank += ((kept >> q) & 1u) && __builtin_amdgcn_readlane(e, q) < e;
     if (keep) {
         sh.sel[slot] = e;
-        sh.wt[slot] = wj;
-        sh.ord[rank] = (uint32_t)slot;
+        sh.wt[rank] = wj;
     }
     if (lane == 0) sh.nsel = (uint32_t)__popcll(kept);
 }
 
 /* Logits path, wave 0, after phase A: softmax over the k selected logits in
  * slot order (m = slot 0's logit, e_q = expf(l_q - m), s = e_0 + e_1 + ...
- * ascending q, w = e / s) and the ascending-id order. */
+ * ascending q, w = e / s), each weight stored at its slot's combine
+ * position (ascending id). */
 __device__ __forceinline__ void md_route_finish(MdShared &sh, int topk) {
     const int lane = threadIdx.x & 63;
     const int myid = lane < topk ? sh.sel[lane] : 0x7fffffff;
@@ -277,10 +276,7 @@ __device__ __forceinline__ void md_route_finish(MdShared &sh, int topk) {
                                                      __builtin_bit_cast(int, ej), j));
     int rank = 0;
     for (int j = 0; j < topk; j++) rank += __builtin_amdgcn_readlane(myid, j) < myid;
-    if (lane < topk) {
-        sh.wt[lane] = ej / ssum;
-        sh.ord[rank] = (uint32_t)lane;
-    }
+    if (lane < topk) sh.wt[rank] = ej / ssum;
 }
 
 /* Phase B: items = (slot q, 16 rows): gate and up GEMVs over dim and the
@@ -577,6 +573,10 @@ __device__ __forceinline__ void md_phase_down(const GhipBank &bank, MdShared &sh
     const uint32_t nsel = __builtin_amdgcn_readfirstlane(sh.nsel);
     if (base + wv < nsel) {
         const uint32_t e = (uint32_t)__builtin_amdgcn_readfirstlane(sh.sel[base + wv]);
+        /* the slot's combine position: how many kept ids are smaller (the
+         * kept ids are distinct) */
+        const int32_t si = lane < nsel ? sh.sel[lane] : 0x7fffffff;
+        const uint32_t pos = (uint32_t)__popcll(__ballot(si < (int32_t)e));
         const uint8_t *slab = bank.base + (size_t)e * bank.stride;
         const uint8_t *rows = slab + bank.off_dw + (size_t)r0 * inter;
         const float *srow = (const float *)(slab + bank.off_ds) + (size_t)(r0 >> 7) * nkb;
@@ -630,7 +630,7 @@ __device__ __forceinline__ void md_phase_down(const GhipBank &bank, MdShared &sh
             if (rem > 1u) step(NR{}, t + 1u, 1u, hd.b0, hd.b1);
             if (rem > 2u) step(NR{}, t + 2u, 2u, hd.c0, hd.c1);
         }
-        if (g == 0) sh.oq[base + wv][n] = acc[0];
+        if (g == 0) sh.oq[pos][n] = acc[0];
     }
 }
 
@@ -649,22 +649,18 @@ __device__ __forceinline__ float2 md_bf16_rnd2(float a, float b) {
     return make_float2(__uint_as_float(u << 16), __uint_as_float(u & 0xffff0000u));
 }
 
-/* y over the first nsel (<= KC) slots in combine order: every slot's order
- * word, output and weight is read before the sum (two LDS round trips; the
- * order words past nsel are masked into range and their terms left out),
- * the products bf16(bf16(o) * w) are independent, and only the running sum
- * is a chain */
+/* y over the first nsel (<= KC) combine positions: every position's output
+ * and weight is read before the sum (one LDS round trip; the positions past
+ * nsel are left out), the products bf16(bf16(o) * w) are independent, and
+ * only the running sum is a chain */
 template <int KC>
 __device__ __forceinline__ float md_combine_sum(const MdShared &sh, uint32_t nsel,
                                                 uint32_t tid) {
-    uint32_t q[KC];
-#pragma unroll
-    for (int i = 0; i < KC; i++) q[i] = sh.ord[i] & (MD_MAXK - 1u);
     float o[KC], wq[KC];
 #pragma unroll
     for (int i = 0; i < KC; i++) {
-        o[i] = sh.oq[q[i]][tid];
-        wq[i] = sh.wt[q[i]];
+        o[i] = sh.oq[i][tid];
+        wq[i] = sh.wt[i];
     }
     float c[KC];
 #pragma unroll
@@ -886,8 +882,8 @@ __device__ __forceinline__ void rt_sigmoid_select(Logit lg, const float *__restr
  * 0..31; device-coherent stores and loads, as the h hand-off), polled until
  * each carries the tag (bounded: on a run-out nothing is selected and
  * err |= 4), then the reference router's selection and weights
- * (rt_router_core) into the slots: sel/wt in selection order, ord the
- * ascending-id combine order. Workgroup 0 also writes the picks to
+ * (rt_router_core): sel in selection order, wt at the ascending-id combine
+ * positions. Workgroup 0 also writes the picks to
  * idx_out / w_out when given. sc: LDS [E]. */
 template <int R>
 __device__ __forceinline__ void md_route_router(const uint64_t *lw, const float *__restrict__ bias,
@@ -936,8 +932,7 @@ __device__ __forceinline__ void md_route_router(const uint64_t *lw, const float 
     for (int j = 0; j < topk; j++) rank += __builtin_amdgcn_readlane(id_or_max, j) < id_or_max;
     if ((int)lane < topk) {
         sh.sel[lane] = myid;
-        sh.wt[lane] = myw;
-        sh.ord[rank] = lane;
+        sh.wt[rank] = myw;
         if (idx_out && blockIdx.x == 0) {
             idx_out[lane] = myid;
             w_out[lane] = myw;
