@@ -64,7 +64,7 @@ def test_decode_shared_vs_oracle(ghip, dim, inter, k, nan_shared):
             st = assert_close_combined(out, want[0], floor_all(slabs, shared, dim, inter, x,
                                                                idx[None], w[None])[0],
                                        "decode shared dim=%d k=%d" % (dim, k))
-            record("shared_decode_dim%d_k%d_t%d" % (dim, k, trial), st)
+            record("shared_decode_dim%d_inter%d_k%d_t%d" % (dim, inter, k, trial), st)
             out2 = np.empty(dim, np.uint16)
             assert ghip.apus_ghip_moe_decode(s, O.ptr(x), O.ptr(idx), O.ptr(w), k,
                                              O.ptr(out2)) == 0
