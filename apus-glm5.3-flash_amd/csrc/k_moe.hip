@@ -969,17 +969,21 @@ struct MdRouter {
     float *w_out;                /* [topk] or NULL */
 };
 
+/* The arguments the routing phase needs come first, so they arrive with the
+ * kernel's first kernel-argument loads and the logits and x loads wait for
+ * one round of them, not two; n_experts and dim repeat bank's. */
 template <bool SHARED, bool ROUTER>
 __global__ __launch_bounds__(MD_NW * 64, 1) void k_moe_decode(
-    GhipBank bank, const uint16_t *__restrict__ x, const float *__restrict__ logits,
-    const int32_t *__restrict__ idx, const float *__restrict__ w, int topk, float limit,
-    uint32_t *hw, uint32_t *hw_clr, uint32_t clr_words, uint32_t tag,
-    uint32_t *__restrict__ err, uint16_t *__restrict__ out, MdRouter rtr) {
+    const float *__restrict__ logits, const uint16_t *__restrict__ x,
+    const int32_t *__restrict__ idx, const float *__restrict__ w,
+    uint32_t *__restrict__ err, int topk, uint32_t n_experts, uint32_t dim,
+    GhipBank bank, float limit, uint32_t *hw, uint32_t *hw_clr, uint32_t clr_words,
+    uint32_t tag, uint16_t *__restrict__ out, MdRouter rtr) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t dl[];
     __shared__ MdShared sh;
     const uint32_t tid = threadIdx.x;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t dim = bank.dim, inter = bank.inter;
+    const uint32_t inter = bank.inter;
     uint16_t *xs = (uint16_t *)dl;
     uint8_t *gu_ring = dl + ((dim * 2u + 1023u) & ~1023u);
 
@@ -993,7 +997,7 @@ __global__ __launch_bounds__(MD_NW * 64, 1) void k_moe_decode(
             /* the gate logits: wave v of workgroup b computes expert
              * b + v * G's, published as a tagged word (c/gmoe.h:168-173) */
             const uint32_t r = blockIdx.x + wv * gridDim.x;
-            if (r < bank.n_experts) {
+            if (r < n_experts) {
                 const float acc = rt_gate_dot(rtr.gate_w + (size_t)r * dim, x, dim, tid & 63u);
                 if ((tid & 63u) == 0)
                     __hip_atomic_store(rtr.lw + r, ((uint64_t)tag << 32) | __float_as_uint(acc),
@@ -1003,14 +1007,14 @@ __global__ __launch_bounds__(MD_NW * 64, 1) void k_moe_decode(
         if (wv == 0) {
             if constexpr (ROUTER) {
                 float *rsc = (float *)gu_ring;            /* wave 0's area: idle in phase A */
-                if (bank.n_experts <= 5 * 64)
-                    md_route_router<5>(rtr.lw, rtr.bias, bank.n_experts, topk, rtr.scale, tag,
+                if (n_experts <= 5 * 64)
+                    md_route_router<5>(rtr.lw, rtr.bias, n_experts, topk, rtr.scale, tag,
                                        rsc, sh, err, rtr.idx_out, rtr.w_out);
                 else
-                    md_route_router<8>(rtr.lw, rtr.bias, bank.n_experts, topk, rtr.scale, tag,
+                    md_route_router<8>(rtr.lw, rtr.bias, n_experts, topk, rtr.scale, tag,
                                        rsc, sh, err, rtr.idx_out, rtr.w_out);
             } else {
-                md_route_ids(logits, idx, w, topk, (int)bank.n_experts, sh,
+                md_route_ids(logits, idx, w, topk, (int)n_experts, sh,
                              blockIdx.x == 0 ? err : nullptr);
             }
         } else if (SHARED && blockIdx.x * 8u < inter)
@@ -1248,8 +1252,9 @@ extern "C" hipError_t ghip_launch_moe_decode(const GhipBank *bank,
     hipEvent_t e0 = ev ? ev[0] : nullptr, e1 = ev ? ev[1] : nullptr;
     const dim3 grid(ws->n_cu), blk(MD_NW * 64);
 #define MD_LAUNCH(S, R_)                                                               \
-    GHIP_LAUNCH(e0, e1, (k_moe_decode<S, R_>), grid, blk, lds, st, *bank, x, logits, idx, \
-                w, topk, limit, hcur, hclr, (uint32_t)hbuf, ws->tag, ws->err, out, rtr)
+    GHIP_LAUNCH(e0, e1, (k_moe_decode<S, R_>), grid, blk, lds, st, logits, x, idx, w, ws->err, \
+                topk, bank->n_experts, bank->dim, *bank, limit, hcur, hclr, (uint32_t)hbuf,    \
+                ws->tag, out, rtr)
     if (shared) {
         if (router) MD_LAUNCH(true, true);
         else MD_LAUNCH(true, false);
