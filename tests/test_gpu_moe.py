@@ -263,6 +263,29 @@ def test_moe_decode_dev_logits(small):
                  moe_floor(eo, w[None], idx[None])[0], "device routing")
 
 
+@pytest.mark.parametrize("topk", [3, 12, 16])
+def test_moe_decode_dev_logits_topk(small, topk):
+    """Device routing at other top-k: fewer slots than waves, and more (a
+    second down pass per workgroup; the combine over 16 positions, its
+    weights placed by the softmax step), with a tie inside the selection."""
+    ghip, s, slabs, (E, dim, inter) = small
+    rng = np.random.default_rng(50 + topk)
+    for trial in range(2):
+        logits = rng.standard_normal(E).astype(np.float32)
+        logits[2] = logits[9] = np.float32(2.75)      # a tie -> lower id first
+        x = O.f32_to_bf16((rng.standard_normal(dim) * (1 + 2 * trial)).astype(np.float32))
+        idx, w = O.route_softmax(logits, topk)
+        want, eo = O.moe_forward(slabs, dim, inter, x, idx[None], w[None],
+                                 want_expert_out=True)
+        dx, dl, dout = G.dev(x), G.dev(logits), G.empty(dim * 2)
+        assert ghip.apus_ghip_moe_decode_dev(s, G.vp(dx), G.vp(dl), None, None, topk,
+                                             G.vp(dout), G.stream()) == 0
+        assert_close_combined(G.host(dout, np.uint16, (dim,)), want[0],
+                              moe_floor(eo, w[None], idx[None])[0],
+                              "device routing topk=%d trial %d" % (topk, trial))
+        assert status(ghip, s, stream=G.stream()) == 0
+
+
 def test_config2_golden(ghip, pkg):
     """288-expert synthetic bank (~7.2 GB in HBM), one
     token, device top-8 + softmax; expected output written by the reference
