@@ -16,8 +16,10 @@ its roofline, its CPU leg, the step against both rooflines and the
 weight-only GB/s of the reference benches.
 
 --workload dense_gemv / dense_gemv_c0 run config 1 / 0 alone (--m for M);
-timed regions start after a lead of unrelated device work, so they measure
-back-to-back device steps, not Python's launch rate. --workload dense_gemm runs
+timed regions measure back-to-back device steps, not Python's launch rate:
+after a warmup long enough for the device to settle, the host stays ahead of
+the device (a step of 12 us or more against ~3 us per launch), and only config
+0's 4.5 us steps start behind a long lead of unrelated device work. --workload dense_gemm runs
 the four DSA FP8 projections at M = 2048 prefill rows (the fp8blk_linear
 hook's MFMA GEMM path), in TFLOP/s. --workload bf16_gemv runs the LM head
 through the bf16_gemm hook; --workload moe_decode_router runs config 2 routed
@@ -128,12 +130,23 @@ def lead(st, us=2000):
         raise RuntimeError("apus_ghip_stream_hold: %s" % _LIB.apus_ghip_last_error())
 
 
-def timed(rt, st, step, first, steps):
+def long_lead(steps):
+    """A lead long enough for the host to enqueue every timed step before
+    the device reaches the first (for steps not much longer than a launch)."""
+    return min(20000, max(2000, 15 * steps))
+
+
+def timed(rt, st, step, first, steps, lead_us=300):
     """Events around exactly `steps` steps enqueued back to back on st
-    (after a synchronize and a lead, see lead()); ms per step."""
+    (after a synchronize and a lead, see lead()); ms per step. The default
+    lead is a short head start: when a step takes several host launches'
+    time the host stays ahead by itself, and a long idle hold before the
+    timed steps measurably slows them (the device leaves its steady state:
+    a 20 ms hold cost 0.4-0.8 us per decode step and 0.5 us per config-1
+    step). Steps close to the launch time pass long_lead(steps)."""
     st.synchronize()
     rt.synchronize()
-    lead(st, min(20000, max(2000, 15 * steps)))
+    lead(st, lead_us)
     e0, e1 = rt.Event(), rt.Event()
     e0.record(st)
     for i in range(steps):
@@ -446,7 +459,10 @@ def bench_dense_gemv(lib, pkg, rt, steps, warmup, M=1, cfg=1):
 
     for i in range(warmup):
         step(i)
-    ms = timed(rt, st, step, warmup, steps)
+    # config 0's 4.5 us steps are close to a launch's host time: all of them
+    # are enqueued behind a long lead before the device starts them
+    ms = timed(rt, st, step, warmup, steps,
+               lead_us=long_lead(steps) if cfg == 0 else 300)
     kt = kernel_times(lib, rt, step, warmup + steps, steps, 2,
                       {"k_fp8_gemv": (0, 1)})
     step(0)                        # weight copy 0, the CPU leg's inputs (untimed)
@@ -1540,12 +1556,13 @@ def main():
                     help="moe_decode only: skip the config 0/1 dense GEMV objects")
     args = ap.parse_args()
     # The decode steps are tens of microseconds of GPU work each, launched
-    # from a Python loop: a long warmup lets the launches build a lead over
-    # the GPU, so the timed steps measure the device, not Python's jitter
-    # (same kernel times; 20 warmup steps read ~7% lower step rates).
-    dflt = {"moe_decode": (2000, 500), "moe_decode_router": (2000, 500),
-            "moe_decode_shared": (2000, 500),
-            "dense_gemv": (2000, 500), "dense_gemv_c0": (2000, 500),
+    # from a Python loop. The warmup runs the device into its steady state
+    # before the timed steps (a store's first few thousand decode steps run
+    # up to ~1.5 us slower: 500 warmup steps measured 36.2-38.0 us, 10,000
+    # steps 35.7 us per decode step).
+    dflt = {"moe_decode": (2000, 10000), "moe_decode_router": (2000, 10000),
+            "moe_decode_shared": (2000, 10000),
+            "dense_gemv": (2000, 5000), "dense_gemv_c0": (2000, 5000),
             "bf16_gemv": (2000, 500),
             "prefill_zipf": (40, 5), "prefill_stack": (5, 2),
             "library_gemm": (10, 3)}
