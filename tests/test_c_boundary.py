@@ -1,6 +1,7 @@
 """The boundary from a compiled C caller (tests/c, built by build.py with
-tests/c/Makefile): the engine TU of INTEGRATION.md section 2(a) linked
-without the library (its stubs decline, the table stays NULL) and with it
+tests/c/Makefile): the engine TU (tests/c/engine_tu.c: the engine's own
+hook table and the no-backend stubs a maintainer adds) linked without the
+library (its stubs decline, the table stays NULL) and with it
 (the library fills the engine's own table; the hooks' floors, M gate and
 results at BASELINE configs 0 and 1 against the oracle on the GPU box)."""
 import os
