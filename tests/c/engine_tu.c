@@ -2,9 +2,8 @@
  * engine_tu.c — the engine-side lines a maintainer adds next to the Metal
  * hook table in the bf16.h implementation TU (c/bf16.h:157-172): the
  * engine's own (strong) hook table, all-NULL until apus_ghip_enable fills
- * it, and -- in a build that
- * does not link libapus_ghip.so -- stubs that decline, so the plain CPU
- * build still links.
+ * it, and -- in a build that does not link libapus_ghip.so -- stubs that
+ * decline, so the plain CPU build still links.
  *
  * The stubs are compiled only when the library is NOT linked
  * (APUS_GHIP_LINKED undefined). A weak stub defined in the executable is
