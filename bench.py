@@ -1062,7 +1062,10 @@ def cpu_store_load(lib, n_experts=8, budget_s=8.0):
 # --------------------------------------------------------------------------
 
 PREFILL = {
-    "prefill_zipf": dict(layers=1, T=2048, zipf=1.1, seed=0xC3, steps=40, warmup=5,
+    # config 3's steps settle over the first ~0.3 s after its bank is filled
+    # (5 warmup steps read 1.96-1.98 ms, 150 read 1.94); config 4's 16-layer
+    # steps are long enough that more warmup only heats the device
+    "prefill_zipf": dict(layers=1, T=2048, zipf=1.1, seed=0xC3, steps=40, warmup=150,
                          desc="BASELINE config 3: 288 experts, T=2048, Zipf(1.1) top-8"),
     "prefill_stack": dict(layers=16, T=8192, zipf=0.0, seed=0xC4, steps=5, warmup=2,
                           desc="BASELINE config 4: 16 layers x 288 experts, "
